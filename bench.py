@@ -1,0 +1,203 @@
+"""Benchmark of the KernelIR hot path on one MI355X.
+
+Headline (BASELINE.json metric): serve.decode_attention HBM GB/s at the
+Qwen2-0.5B GQA shape (14 query / 2 KV heads, head_dim 64, bf16), batch 32,
+per-sequence lengths uniform in [L/2, L] for L = 8192.  One step
+is one decode-attention launch over that batch with all inputs resident in
+HBM.  ``value`` is algorithmic bytes x steps / wall time of the timed region;
+``roofline`` divides the algorithmic bytes of one launch by the launch's mean
+duration measured with HIP events on the launch stream.  The CPU baseline is
+the oracle (eager PyTorch restatement of the reference executor) on a bounded
+sample of the same workload on the host cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "llm-compiler_amd"))
+
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "decode-attn HBM GB/s (% of peak) + decode tok/s, Qwen2-0.5B shape, 1 GPU"
+
+BATCH, QH, KVH, D, LMAX = 32, 14, 2, 64, 8192
+SEED = 2
+
+
+def decode_inputs(device, batch=BATCH, lmax=LMAX, seed=SEED):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    lengths = torch.randint(lmax // 2, lmax + 1, (batch,), generator=g)
+    query = torch.randn(batch, QH, 1, D, generator=g).bfloat16()
+    key = torch.randn(batch, lmax, KVH, D, generator=g).bfloat16()
+    value = torch.randn(batch, lmax, KVH, D, generator=g).bfloat16()
+    mask = torch.zeros(batch, 1, 1, lmax, dtype=torch.bfloat16)
+    tensors = [query, key, value, lengths, mask]
+    return [t.to(device) for t in tensors]
+
+
+def decode_bytes(lengths: torch.Tensor, batch=BATCH) -> int:
+    """Algorithmic HBM bytes of one decode-attention launch (bf16).
+
+    K and V rows of every attended token (2 x KVH x D x 2 B = 512 B/token), the
+    mask entry of every attended token (2 B), q and the output (B x QH x D x
+    2 B each) and the int64 lengths.
+    """
+
+    tokens = int(lengths.sum().item())
+    return tokens * (2 * KVH * D * 2 + 2) + 2 * batch * QH * D * 2 + batch * 8
+
+
+def cpu_baseline(seconds_budget: float = 20.0) -> dict:
+    """Oracle decode attention on the host cores over a bounded sample."""
+
+    sys.path.insert(0, str(ROOT))
+    from oracle import kernels as ref
+
+    sample_batch = 4
+    q, k, v, lengths, mask = decode_inputs("cpu", batch=sample_batch)
+    ref.decode_attention(q, k, v, lengths, mask, groups=QH // KVH, scale=D**-0.5)
+    reps, start = 0, time.perf_counter()
+    while True:
+        ref.decode_attention(q, k, v, lengths, mask, groups=QH // KVH, scale=D**-0.5)
+        reps += 1
+        elapsed = time.perf_counter() - start
+        if elapsed > seconds_budget / 4 or reps >= 20:
+            break
+    per_call = elapsed / reps
+    gbs = decode_bytes(lengths, batch=sample_batch) / per_call / 1e9
+    return {
+        "value": round(gbs, 3),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (
+            f"oracle decode_attention (eager torch CPU, bf16), batch {sample_batch} "
+            f"of the same L={LMAX} workload, {reps} reps, {per_call * 1e3:.1f} ms/call"
+        ),
+    }
+
+
+def bench_decode_attention(steps: int, warmup: int, split_tokens: int) -> dict:
+    from stateful_llm_compiler_hip.backends import hip_decode_attention
+
+    device = torch.device("cuda:0")
+    q, k, v, lengths, mask = decode_inputs(device)
+    nbytes = decode_bytes(lengths.cpu())
+
+    def step():
+        return hip_decode_attention(q, k, v, lengths, mask, scale=D**-0.5, split_tokens=split_tokens)
+
+    # Warm the workspace and the library, then capture one step in a HIP graph
+    # so host launch overhead does not throttle a ~15 us kernel.
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = step()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+
+    # Per-launch durations with events on the replay stream.
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(min(steps, 200))]
+    for s, e in events:
+        s.record()
+        graph.replay()
+        e.record()
+    torch.cuda.synchronize()
+    durations_ms = [s.elapsed_time(e) for s, e in events]
+    kernel_us = 1e3 * sum(durations_ms) / len(durations_ms)
+
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    del out
+    achieved = nbytes / (kernel_us * 1e-6) / 1e9
+    return {
+        "elapsed": elapsed,
+        "bytes": nbytes,
+        "kernel_us": kernel_us,
+        "achieved_gbs": achieved,
+        "tokens": int(lengths.sum().item()),
+    }
+
+
+def main() -> None:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=2000)
+    parser.add_argument("--warmup", type=int, default=50)
+    parser.add_argument("--split-tokens", type=int, default=0)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(
+            "bench.py measures the single-GPU hot path only; this build has no "
+            "multi-GPU path (see the sharding paragraph of the design notes).",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X (torch.cuda.is_available() is False)", file=sys.stderr)
+        sys.exit(2)
+
+    result = bench_decode_attention(args.steps, args.warmup, args.split_tokens)
+    value = result["bytes"] * args.steps / result["elapsed"] / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(result["elapsed"] * 1e3 / args.steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/K/V, lengths U[L/2, L])",
+        "config": {
+            "workload": "serve.decode_attention GQA QH14/KVH2/D64, B=32, L=8192, lengths U[4096,8192], contiguous_bshd KV, int64 lengths, zero bf16 mask",
+            "global_batch": BATCH,
+            "seq_len": LMAX,
+            "attended_tokens": result["tokens"],
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(result["achieved_gbs"], 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(result["achieved_gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel_us": round(result["kernel_us"], 3),
+            "algorithmic_bytes": result["bytes"],
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

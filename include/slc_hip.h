@@ -1,0 +1,154 @@
+/*
+ * slc_hip.h -- C ABI of the gfx950 (MI355X) KernelIR backend.
+ *
+ * Every entry point launches hand-written HIP kernels on the stream it is
+ * given and returns immediately (no host synchronisation).  Pointers are
+ * device pointers; strides are in ELEMENTS; the innermost (head-dim / hidden)
+ * axis of every tensor must be contiguous (stride 1), exactly as the
+ * reference's Python wrappers require.
+ *
+ * Return value: SLC_OK (0) on success, SLC_ERR_INVALID_ARGUMENT (-1) when an
+ * argument check fails, or a positive hipError_t from the launch.  The text of
+ * the last error of the calling thread is available from slc_hip_last_error().
+ *
+ * Reference interfaces replaced (paths relative to the reference repository,
+ * src/stateful_llm_compiler/):
+ *   slc_hip_decode_attention   backends/triton_attention.py:134-210
+ *                              (triton_decode_attention; semantics of
+ *                              execution.py:281-327)
+ *   slc_hip_kv_store           backends/triton_kv.py:71-129 (triton_kv_store;
+ *                              semantics of execution.py:743-781 native_kv_store)
+ *   slc_hip_rms_norm           backends/triton_rmsnorm.py:205-443
+ *                              (triton_rms_norm; semantics of execution.py:674-692)
+ *   slc_hip_rope               backends/triton_rope.py:299-390 (triton_rope;
+ *                              semantics of execution.py:741-767)
+ *   slc_hip_linear             backends/triton_linear.py:87-148 (triton_linear)
+ *                              and triton_executor.py:159-176 (kernel.cublas.linear)
+ *   slc_hip_prefill_attention  backends/triton_prefill_attention.py:152-232
+ *                              (semantics of execution.py:707-739)
+ */
+#ifndef SLC_HIP_H_
+#define SLC_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define SLC_API __attribute__((visibility("default")))
+#else
+#define SLC_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype tags used for every tensor argument */
+enum slc_dtype {
+  SLC_F32 = 0,
+  SLC_F16 = 1,
+  SLC_BF16 = 2,
+  SLC_I32 = 3,
+  SLC_I64 = 4
+};
+
+enum slc_status { SLC_OK = 0, SLC_ERR_INVALID_ARGUMENT = -1 };
+
+/* Library version (major*10000 + minor*100 + patch). */
+SLC_API int slc_hip_version(void);
+
+/* Message describing the last failure on the calling thread ("" if none). */
+SLC_API const char* slc_hip_last_error(void);
+
+/*
+ * kv_store: scatter the current step's K/V rows into the preallocated
+ * B x capacity x H x D buffers.
+ *   key_buffer/value_buffer : [batch, capacity, heads, head_dim], contiguous
+ *   key/value               : [batch, heads, tokens, head_dim], strides
+ *                             (sb, sh, st) in elements, head_dim contiguous
+ *   positions               : [batch] int64 (first destination row per batch)
+ * Row t of batch b lands at buffer row positions[b] + t; rows whose position is
+ * outside [0, capacity) are skipped (the reference masks them the same way).
+ * The copy is bit-exact for every dtype.
+ */
+SLC_API int slc_hip_kv_store(void* key_buffer, void* value_buffer, const void* key,
+                     const void* value, const int64_t* positions, int dtype,
+                     int64_t batch, int64_t heads, int64_t tokens,
+                     int64_t head_dim, int64_t capacity, int64_t key_stride_b,
+                     int64_t key_stride_h, int64_t key_stride_t,
+                     int64_t value_stride_b, int64_t value_stride_h,
+                     int64_t value_stride_t, void* stream);
+
+/*
+ * decode_attention: single-token GQA attention that reads the physical KV
+ * buffers directly.
+ *   query        : [batch, q_heads, 1, head_dim], strides (q_sb, q_sh)
+ *   key/value    : physical buffers indexed [b, s, h, :] with strides
+ *                  (kv_sb, kv_ss, kv_sh) -- contiguous_bshd buffers have
+ *                  (capacity*H*D, H*D, D); BHSD views are accepted as well.
+ *                  Both buffers must share these strides.
+ *   lengths      : [batch] of lengths_dtype (SLC_I64 or SLC_I32) on device
+ *   mask         : additive mask [batch, 1, 1, mask_len] with strides
+ *                  (mask_sb, mask_ss), dtype mask_dtype; may be NULL (= zeros)
+ *   output       : [batch, q_heads, 1, head_dim], strides (out_sb, out_sh),
+ *                  same dtype as query
+ *   workspace    : device scratch of at least
+ *                  slc_hip_decode_attention_workspace_size(...) bytes
+ *                  (may be NULL when that size is 0)
+ * Token s of batch b is attended iff s < min(lengths[b], mask_len, capacity).
+ * kv head of query head h is h / (q_heads / kv_heads).
+ * split_tokens selects the split-sequence chunk (0 = automatic).
+ */
+SLC_API int64_t slc_hip_decode_attention_workspace_size(int64_t batch, int64_t q_heads,
+                                                int64_t head_dim,
+                                                int64_t mask_len,
+                                                int64_t kv_heads, int dtype,
+                                                int64_t split_tokens);
+
+SLC_API int slc_hip_decode_attention(
+    const void* query, const void* key_buffer, const void* value_buffer,
+    const void* lengths, int lengths_dtype, const void* mask, int mask_dtype,
+    void* output, void* workspace, int64_t workspace_bytes, int dtype,
+    int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+    int64_t capacity, int64_t mask_len, int64_t q_stride_b, int64_t q_stride_h,
+    int64_t kv_stride_b, int64_t kv_stride_s, int64_t kv_stride_h,
+    int64_t mask_stride_b, int64_t mask_stride_s, int64_t out_stride_b,
+    int64_t out_stride_h, float scale, int64_t split_tokens, void* stream);
+
+/*
+ * rms_norm over the last axis:
+ *   normalized = x * rsqrt(mean(x^2) + epsilon)            (fp32)
+ *   round_before_weight=1 : out = weight * round(normalized, norm_dtype)
+ *   round_before_weight=0 : out = round(normalized * weight, out_dtype)
+ * input rows are [rows, hidden] with row stride in_stride_row; output rows
+ * have stride out_stride_row.  norm_dtype is the dtype the normalized value
+ * is materialised in before the weight multiply (the reference's
+ * output_dtype or the input dtype).
+ */
+SLC_API int slc_hip_rms_norm(const void* input, const void* weight, void* output,
+                     int in_dtype, int weight_dtype, int out_dtype,
+                     int norm_dtype, int64_t rows, int64_t hidden,
+                     int64_t in_stride_row, int64_t out_stride_row,
+                     float epsilon, int round_before_weight, void* stream);
+
+/*
+ * rope (dual output, Qwen2 half rotation):
+ *   q' = round(q*cos) + round(rotate_half(q)*sin), same for k,
+ *   rotate_half(x) = cat(-x[D/2:], x[:D/2]);
+ * query [B, QH, T, D], key [B, KVH, T, D], cos/sin [B, T, D]; every tensor
+ * passes (sb, sh, st) or (sb, st) strides in elements; all share one dtype.
+ */
+SLC_API int slc_hip_rope(const void* query, const void* key, const void* cosine,
+                 const void* sine, void* query_out, void* key_out, int dtype,
+                 int64_t batch, int64_t q_heads, int64_t kv_heads,
+                 int64_t tokens, int64_t head_dim, int64_t q_sb, int64_t q_sh,
+                 int64_t q_st, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                 int64_t cos_sb, int64_t cos_st, int64_t sin_sb,
+                 int64_t sin_st, int64_t qo_sb, int64_t qo_sh, int64_t qo_st,
+                 int64_t ko_sb, int64_t ko_sh, int64_t ko_st, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SLC_HIP_H_ */

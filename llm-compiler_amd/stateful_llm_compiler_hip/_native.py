@@ -1,0 +1,130 @@
+"""ctypes binding of ``libslc_hip.so`` (the C ABI declared in include/slc_hip.h).
+
+The library is loaded lazily on first use and never replaced by anything
+else: if it is missing or fails to load, every kernel entry point raises
+``NativeLibraryError``.  There is no PyTorch or CPU fallback behind these
+functions.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch
+
+LIBRARY_PATH = Path(
+    os.environ.get(
+        "SLC_HIP_LIBRARY",
+        str(Path(__file__).resolve().parent / "libslc_hip.so"),
+    )
+)
+
+SLC_F32 = 0
+SLC_F16 = 1
+SLC_BF16 = 2
+SLC_I32 = 3
+SLC_I64 = 4
+
+_DTYPE_TAGS = {
+    torch.float32: SLC_F32,
+    torch.float16: SLC_F16,
+    torch.bfloat16: SLC_BF16,
+    torch.int32: SLC_I32,
+    torch.int64: SLC_I64,
+}
+
+# Every exported symbol with its ctypes signature.  The tests check that this
+# table and include/slc_hip.h list the same entry points.
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "slc_hip_version": (_I, []),
+    "slc_hip_last_error": (ctypes.c_char_p, []),
+    "slc_hip_kv_store": (
+        _I,
+        [_P, _P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _P],
+    ),
+    "slc_hip_decode_attention_workspace_size": (
+        _L,
+        [_L, _L, _L, _L, _L, _I, _L],
+    ),
+    "slc_hip_decode_attention": (
+        _I,
+        [_P, _P, _P, _P, _I, _P, _I, _P, _P, _L, _I]
+        + [_L] * 15
+        + [_F, _L, _P],
+    ),
+    "slc_hip_rms_norm": (
+        _I,
+        [_P, _P, _P, _I, _I, _I, _I, _L, _L, _L, _L, _F, _I, _P],
+    ),
+    "slc_hip_rope": (
+        _I,
+        [_P] * 6 + [_I] + [_L] * 5 + [_L] * 16 + [_P],
+    ),
+}
+
+
+class NativeLibraryError(RuntimeError):
+    """The gfx950 kernel library is missing or could not be loaded."""
+
+
+class KernelLaunchError(RuntimeError):
+    """A C entry point rejected its arguments or a launch failed."""
+
+
+_lock = threading.Lock()
+_library: ctypes.CDLL | None = None
+
+
+def library() -> ctypes.CDLL:
+    """Load (once) and return the kernel library; raise if it is unavailable."""
+
+    global _library
+    if _library is not None:
+        return _library
+    with _lock:
+        if _library is not None:
+            return _library
+        if not LIBRARY_PATH.exists():
+            raise NativeLibraryError(
+                f"{LIBRARY_PATH} does not exist; build it with "
+                "`python llm-compiler_amd/stateful_llm_compiler_hip/build.py` "
+                "(or __graft_entry__.build())"
+            )
+        try:
+            lib = ctypes.CDLL(str(LIBRARY_PATH))
+        except OSError as error:
+            raise NativeLibraryError(
+                f"cannot load {LIBRARY_PATH}: {error}"
+            ) from error
+        for name, (restype, argtypes) in SIGNATURES.items():
+            function = getattr(lib, name)
+            function.restype = restype
+            function.argtypes = argtypes
+        _library = lib
+        return lib
+
+
+def dtype_tag(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_TAGS[dtype]
+    except KeyError as error:
+        raise ValueError(f"unsupported dtype {dtype}") from error
+
+
+def current_stream(device: torch.device) -> int:
+    """Raw hipStream_t of PyTorch's current stream on ``device``."""
+
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        message = library().slc_hip_last_error().decode(errors="replace")
+        raise KernelLaunchError(f"{what} failed (status {status}): {message}")

@@ -1,0 +1,13 @@
+"""gfx950 kernel wrappers (drop-ins for the reference's backends/triton_*)."""
+
+from .hip_attention import hip_decode_attention
+from .hip_kv import hip_kv_store
+from .hip_rmsnorm import hip_rms_norm
+from .hip_rope import hip_rope
+
+__all__ = [
+    "hip_decode_attention",
+    "hip_kv_store",
+    "hip_rms_norm",
+    "hip_rope",
+]

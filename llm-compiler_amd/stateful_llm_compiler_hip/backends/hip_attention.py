@@ -1,0 +1,157 @@
+"""``kernel.hip.decode_attention``: GQA single-token attention on gfx950.
+
+Drop-in for the reference's ``triton_decode_attention``
+(src/stateful_llm_compiler/backends/triton_attention.py:134-210): same
+arguments, same validation (``ValueError`` on device/shape/stride/dtype
+problems), same result (a new tensor shaped like ``query``).  The math is the
+reference executor's (execution.py:281-327).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _native
+
+
+# Split-sequence workspaces, one per (device, stream).  The kernel keeps the
+# ticket counters at the head of the workspace at zero between launches, so a
+# workspace is zero-filled once when it is created and then reused; launches
+# that share a workspace must be ordered (same stream).
+_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor | None:
+    if nbytes <= 0:
+        return None
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    workspace = _WORKSPACES.get(key)
+    if workspace is None or workspace.numel() < nbytes:
+        workspace = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = workspace
+    return workspace
+
+
+def hip_decode_attention(
+    query: torch.Tensor,
+    key_buffer: torch.Tensor,
+    value_buffer: torch.Tensor,
+    lengths: torch.Tensor,
+    attention_mask: torch.Tensor | None,
+    *,
+    scale: float,
+    split_tokens: int = 0,
+) -> torch.Tensor:
+    """B x H x 1 x D GQA decode attention over a B x Cap x KVH x D buffer.
+
+    ``key_buffer``/``value_buffer`` are indexed ``[b, s, h, :]``; the
+    reference's contiguous_bshd buffers are the normal case, and any view with
+    a contiguous head dim and equal K/V strides (for example a BHSD buffer
+    permuted to BSHD) is accepted.  ``lengths`` is int64 (the runtime's
+    dtype) or int32.  ``attention_mask`` is B x 1 x 1 x S additive, or None
+    for an all-zero mask over the whole capacity.
+    """
+
+    tensors = [query, key_buffer, value_buffer, lengths]
+    if attention_mask is not None:
+        tensors.append(attention_mask)
+    if not all(tensor.is_cuda for tensor in tensors):
+        raise ValueError("HIP decode attention: all tensors must be on the GPU")
+    if (
+        query.ndim != 4
+        or query.shape[2] != 1
+        or key_buffer.ndim != 4
+        or key_buffer.shape != value_buffer.shape
+        or (
+            attention_mask is not None
+            and (
+                attention_mask.ndim != 4
+                or attention_mask.shape[1] != 1
+                or attention_mask.shape[2] != 1
+            )
+        )
+    ):
+        raise ValueError("HIP decode attention: illegal shapes")
+    batch, query_heads, _, head_dim = query.shape
+    capacity = key_buffer.shape[1]
+    kv_heads = key_buffer.shape[2]
+    if (
+        batch != key_buffer.shape[0]
+        or (attention_mask is not None and batch != attention_mask.shape[0])
+        or lengths.shape != (batch,)
+        or query_heads % kv_heads
+        or head_dim != key_buffer.shape[3]
+    ):
+        raise ValueError("HIP decode attention: GQA or batch shapes do not match")
+    if lengths.dtype not in (torch.int64, torch.int32):
+        raise ValueError("HIP decode attention: lengths must be int64 (or int32)")
+    if query.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError(f"HIP decode attention: unsupported dtype {query.dtype}")
+    if key_buffer.dtype != query.dtype or value_buffer.dtype != query.dtype:
+        raise ValueError("HIP decode attention: Q/K/V dtypes must match")
+    if key_buffer.stride() != value_buffer.stride() or key_buffer.stride(3) != 1:
+        raise ValueError(
+            "HIP decode attention: K/V buffers need equal strides and a "
+            "contiguous head dim"
+        )
+    if query.stride(-1) != 1:
+        raise ValueError("HIP decode attention: query head dim must be contiguous")
+    if attention_mask is not None and attention_mask.dtype not in (
+        torch.float16,
+        torch.bfloat16,
+        torch.float32,
+    ):
+        raise ValueError("HIP decode attention: mask must be floating point")
+    if head_dim > 256:
+        raise ValueError("HIP decode attention: head_dim above 256")
+
+    lib = _native.library()
+    output = torch.empty_like(query)
+    if batch == 0:
+        return output
+    dtype = _native.dtype_tag(query.dtype)
+    mask_len = capacity if attention_mask is None else attention_mask.shape[-1]
+    nbytes = lib.slc_hip_decode_attention_workspace_size(
+        batch, query_heads, head_dim, mask_len, kv_heads, dtype, split_tokens
+    )
+    stream = _native.current_stream(query.device)
+    workspace = _workspace(query.device, stream, nbytes)
+    if attention_mask is None:
+        mask_ptr, mask_dtype, mask_sb, mask_ss = None, 0, 0, 0
+    else:
+        mask_ptr = attention_mask.data_ptr()
+        mask_dtype = _native.dtype_tag(attention_mask.dtype)
+        mask_sb, mask_ss = attention_mask.stride(0), attention_mask.stride(3)
+    status = lib.slc_hip_decode_attention(
+        query.data_ptr(),
+        key_buffer.data_ptr(),
+        value_buffer.data_ptr(),
+        lengths.data_ptr(),
+        _native.dtype_tag(lengths.dtype),
+        mask_ptr,
+        mask_dtype,
+        output.data_ptr(),
+        None if workspace is None else workspace.data_ptr(),
+        nbytes,
+        dtype,
+        batch,
+        query_heads,
+        kv_heads,
+        head_dim,
+        capacity,
+        mask_len,
+        query.stride(0),
+        query.stride(1),
+        key_buffer.stride(0),
+        key_buffer.stride(1),
+        key_buffer.stride(2),
+        mask_sb,
+        mask_ss,
+        output.stride(0),
+        output.stride(1),
+        float(scale),
+        int(split_tokens),
+        stream,
+    )
+    _native.check(status, "slc_hip_decode_attention")
+    return output

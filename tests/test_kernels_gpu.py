@@ -1,0 +1,343 @@
+"""GPU parity of each gfx950 kernel against the CPU oracle (same seeded inputs).
+
+Bars: kv_store bit-exact; rope bit-exact (it reproduces the eager rounding
+points); fp32 within 1e-5 relative; bf16 within 2e-2 absolute.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (
+    announce,
+    assert_bf16_close,
+    assert_bitwise_equal,
+    assert_fp32_close,
+    generator,
+)
+from oracle import kernels as ref
+
+pytestmark = pytest.mark.gpu
+
+
+# ----------------------------------------------------------------- kv_store
+
+
+def _kv_store_case(gpu, batch, heads, tokens, head_dim, capacity, positions, dtype, seed, strided=False):
+    g = generator(seed)
+    key_buffer = torch.randn(batch, capacity, heads, head_dim, generator=g).to(dtype)
+    value_buffer = torch.randn(batch, capacity, heads, head_dim, generator=g).to(dtype)
+    if strided:
+        # B x T x H x D projection output viewed as B x H x T x D (the layout the
+        # model hands to kv_store).
+        key = torch.randn(batch, tokens, heads, head_dim, generator=g).to(dtype).transpose(1, 2)
+        value = torch.randn(batch, tokens, heads, head_dim, generator=g).to(dtype).transpose(1, 2)
+    else:
+        key = torch.randn(batch, heads, tokens, head_dim, generator=g).to(dtype)
+        value = torch.randn(batch, heads, tokens, head_dim, generator=g).to(dtype)
+    positions = torch.tensor(positions, dtype=torch.int64)
+
+    from stateful_llm_compiler_hip.backends import hip_kv_store
+
+    kb, vb = key_buffer.to(gpu), value_buffer.to(gpu)
+    kd, vd = key.to(gpu), value.to(gpu)
+    if strided:
+        kd = key.transpose(1, 2).contiguous().to(gpu).transpose(1, 2)
+        vd = value.transpose(1, 2).contiguous().to(gpu).transpose(1, 2)
+    hip_kv_store(kb, vb, kd, vd, positions.to(gpu))
+    torch.cuda.synchronize()
+
+    width = torch.int16 if dtype != torch.float32 else torch.int32
+    exp_k = key_buffer.view(width).numpy().copy()
+    exp_v = value_buffer.view(width).numpy().copy()
+    ref.kv_store(exp_k, exp_v, key.contiguous().view(width).numpy(), value.contiguous().view(width).numpy(), positions.numpy())
+    assert_bitwise_equal(kb.cpu().view(width), torch.from_numpy(exp_k))
+    assert_bitwise_equal(vb.cpu().view(width), torch.from_numpy(exp_v))
+
+
+def test_kv_store_reference_positions(gpu):
+    # Reference KAT: positions [1, 5, 9], capacity 16 (test_triton_backend.py:436-466).
+    announce("kv_store KAT positions=[1,5,9] cap=16")
+    _kv_store_case(gpu, 3, 2, 1, 8, 16, [1, 5, 9], torch.float32, 1)
+
+
+@pytest.mark.parametrize("batch", [1, 8, 64])
+@pytest.mark.parametrize("tokens", [1, 128, 512])
+def test_kv_store_config3_bitexact(gpu, batch, tokens):
+    announce(f"kv_store bf16 B={batch} T={tokens} cap=8192")
+    g = generator(100 + batch + tokens)
+    positions = torch.randint(0, 8192 - tokens + 1, (batch,), generator=g).tolist()
+    _kv_store_case(gpu, batch, 2, tokens, 64, 8192, positions, torch.bfloat16, 7 + batch, strided=True)
+
+
+def test_kv_store_capacity_overflow_rows_are_dropped(gpu):
+    announce("kv_store overflow rows dropped")
+    _kv_store_case(gpu, 2, 2, 6, 64, 16, [13, 0], torch.bfloat16, 3)
+
+
+def test_kv_store_odd_head_dim_fp16(gpu):
+    announce("kv_store fp16 D=6 (2-byte units)")
+    _kv_store_case(gpu, 2, 3, 4, 6, 10, [0, 5], torch.float16, 4)
+
+
+# --------------------------------------------------------- decode_attention
+
+
+def _decode_case(
+    gpu,
+    batch,
+    q_heads,
+    kv_heads,
+    head_dim,
+    capacity,
+    lengths,
+    dtype,
+    seed,
+    *,
+    mask_len=None,
+    mask_kind="zeros",
+    layout="bshd",
+    length_dtype=torch.int64,
+    split_tokens=0,
+):
+    from stateful_llm_compiler_hip.backends import hip_decode_attention
+
+    g = generator(seed)
+    mask_len = capacity if mask_len is None else mask_len
+    query = torch.randn(batch, q_heads, 1, head_dim, generator=g).to(dtype)
+    key_buffer = torch.randn(batch, capacity, kv_heads, head_dim, generator=g).to(dtype)
+    value_buffer = torch.randn(batch, capacity, kv_heads, head_dim, generator=g).to(dtype)
+    if mask_kind == "zeros":
+        mask = torch.zeros(batch, 1, 1, mask_len, dtype=dtype)
+    else:
+        mask = (torch.randn(batch, 1, 1, mask_len, generator=g) * 2.0).to(dtype)
+    lengths_t = torch.tensor(lengths, dtype=torch.int64)
+    expected = ref.decode_attention(
+        query,
+        key_buffer,
+        value_buffer,
+        lengths_t,
+        mask,
+        groups=q_heads // kv_heads,
+        scale=head_dim**-0.5,
+    )
+    if layout == "bhsd":
+        # Physical [B, KVH, Lmax, D] buffer presented through a BSHD view.
+        kd = key_buffer.permute(0, 2, 1, 3).contiguous().to(gpu).permute(0, 2, 1, 3)
+        vd = value_buffer.permute(0, 2, 1, 3).contiguous().to(gpu).permute(0, 2, 1, 3)
+    else:
+        kd, vd = key_buffer.to(gpu), value_buffer.to(gpu)
+    actual = hip_decode_attention(
+        query.to(gpu),
+        kd,
+        vd,
+        lengths_t.to(length_dtype).to(gpu),
+        mask.to(gpu),
+        scale=head_dim**-0.5,
+        split_tokens=split_tokens,
+    )
+    torch.cuda.synchronize()
+    return actual.cpu(), expected
+
+
+def test_decode_attention_reference_lengths_fp32(gpu):
+    # Reference KAT: per-batch lengths [7, 31, 65], cap 65, QH4 KVH2 D16, fp32,
+    # tolerance 3e-5 (test_triton_backend.py:380-434).
+    announce("decode KAT fp32 lengths=[7,31,65]")
+    actual, expected = _decode_case(gpu, 3, 4, 2, 16, 65, [7, 31, 65], torch.float32, 5)
+    torch.testing.assert_close(actual, expected, rtol=3e-5, atol=3e-5)
+    assert_fp32_close(actual, expected)
+
+
+@pytest.mark.parametrize("batch", [1, 8, 32, 64])
+@pytest.mark.parametrize("max_len", [64, 1024, 8192])
+def test_decode_attention_config2_bf16(gpu, batch, max_len):
+    announce(f"decode bf16 B={batch} L={max_len}")
+    g = generator(batch * 7 + max_len)
+    lengths = torch.randint(max_len // 2, max_len + 1, (batch,), generator=g).tolist()
+    actual, expected = _decode_case(gpu, batch, 14, 2, 64, max_len, lengths, torch.bfloat16, batch + max_len)
+    assert_bf16_close(actual, expected)
+
+
+def test_decode_attention_config2_bf16_long(gpu):
+    announce("decode bf16 B=8 L=32768")
+    g = generator(11)
+    lengths = torch.randint(16384, 32769, (8,), generator=g).tolist()
+    actual, expected = _decode_case(gpu, 8, 14, 2, 64, 32768, lengths, torch.bfloat16, 12)
+    assert_bf16_close(actual, expected)
+
+
+@pytest.mark.parametrize("layout", ["bshd", "bhsd"])
+@pytest.mark.parametrize("length_dtype", [torch.int64, torch.int32])
+def test_decode_attention_layouts_and_length_dtypes(gpu, layout, length_dtype):
+    announce(f"decode bf16 layout={layout} lengths={length_dtype}")
+    actual, expected = _decode_case(
+        gpu, 4, 14, 2, 64, 1024, [1, 333, 1000, 1024], torch.bfloat16, 21,
+        layout=layout, length_dtype=length_dtype,
+    )
+    assert_bf16_close(actual, expected)
+
+
+@pytest.mark.parametrize("split", [128, 256, 2048])
+def test_decode_attention_forced_split(gpu, split):
+    announce(f"decode bf16 split_tokens={split}")
+    actual, expected = _decode_case(
+        gpu, 3, 14, 2, 64, 2048, [2048, 1, 1500], torch.bfloat16, 31, split_tokens=split, mask_kind="random",
+    )
+    assert_bf16_close(actual, expected)
+
+
+def test_decode_attention_random_mask_short_mask(gpu):
+    # Mask shorter than the capacity bounds the attended prefix (execution.py:301-327).
+    announce("decode bf16 mask_len < capacity, random mask")
+    actual, expected = _decode_case(
+        gpu, 5, 14, 2, 64, 512, [10, 300, 512, 200, 1], torch.bfloat16, 41,
+        mask_len=300, mask_kind="random",
+    )
+    assert_bf16_close(actual, expected)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_attention_head_dim_128(gpu, dtype):
+    announce(f"decode {dtype} D=128 QH4 KVH2")
+    actual, expected = _decode_case(gpu, 8, 4, 2, 128, 1024, [1024, 513, 2, 700, 999, 64, 65, 1000], dtype, 51)
+    assert_bf16_close(actual, expected)
+
+
+def test_decode_attention_fp32_qwen_shape(gpu):
+    announce("decode fp32 QH14 KVH2 D64 L=1024")
+    actual, expected = _decode_case(gpu, 4, 14, 2, 64, 1024, [1024, 600, 17, 900], torch.float32, 61, mask_kind="random")
+    assert_fp32_close(actual, expected)
+
+
+def test_decode_attention_generic_group_size(gpu):
+    # 32 query heads per KV head exceed one MFMA tile: generic kernel path.
+    announce("decode bf16 QH32 KVH1 (generic)")
+    actual, expected = _decode_case(gpu, 2, 32, 1, 64, 256, [256, 100], torch.bfloat16, 71)
+    assert_bf16_close(actual, expected)
+
+
+def test_decode_attention_zero_length_is_nan(gpu):
+    # The reference softmax over an all -inf row is NaN; so is the kernel's.
+    announce("decode bf16 zero length")
+    actual, expected = _decode_case(gpu, 2, 14, 2, 64, 128, [0, 50], torch.bfloat16, 81)
+    assert torch.isnan(expected[0]).all() and torch.isnan(actual[0]).all()
+    assert_bf16_close(actual[1], expected[1])
+
+
+def test_decode_attention_positions_past_length_are_ignored(gpu):
+    # Invariance: garbage (including inf/NaN bit patterns) after the length
+    # must not change the result.
+    from stateful_llm_compiler_hip.backends import hip_decode_attention
+
+    announce("decode bf16 garbage past length")
+    g = generator(91)
+    batch, cap = 2, 256
+    q = torch.randn(batch, 14, 1, 64, generator=g).bfloat16().to(gpu)
+    k = torch.randn(batch, cap, 2, 64, generator=g).bfloat16().to(gpu)
+    v = torch.randn(batch, cap, 2, 64, generator=g).bfloat16().to(gpu)
+    lengths = torch.tensor([100, 37], device=gpu)
+    mask = torch.zeros(batch, 1, 1, cap, dtype=torch.bfloat16, device=gpu)
+    base = hip_decode_attention(q, k, v, lengths, mask, scale=0.125)
+    k2, v2 = k.clone(), v.clone()
+    k2[0, 100:] = float("nan")
+    v2[0, 100:] = float("inf")
+    k2[1, 37:] = float("inf")
+    v2[1, 37:] = float("nan")
+    again = hip_decode_attention(q, k2, v2, lengths, mask, scale=0.125)
+    torch.cuda.synchronize()
+    assert_bitwise_equal(again, base)
+
+
+# ------------------------------------------------------------------ rms_norm
+
+
+@pytest.mark.parametrize("rows", [1, 8, 64, 512, 32768])
+def test_rms_norm_bf16_round_before_weight(gpu, rows):
+    from stateful_llm_compiler_hip.backends import hip_rms_norm
+
+    announce(f"rms_norm bf16 rows={rows}")
+    g = generator(rows)
+    x = torch.randn(rows, 896, generator=g).bfloat16()
+    w = (1.0 + 0.1 * torch.randn(896, generator=g)).bfloat16()
+    expected = ref.rms_norm(x, w, epsilon=1e-6, round_before_weight=True)
+    actual = hip_rms_norm(x.to(gpu), w.to(gpu), epsilon=1e-6, round_before_weight=True)
+    torch.cuda.synchronize()
+    assert actual.dtype == expected.dtype
+    assert_bf16_close(actual, expected)
+
+
+@pytest.mark.parametrize("hidden", [896, 1536, 4096, 100])
+def test_rms_norm_fp32(gpu, hidden):
+    from stateful_llm_compiler_hip.backends import hip_rms_norm
+
+    announce(f"rms_norm fp32 hidden={hidden}")
+    g = generator(hidden)
+    x = torch.randn(3, 5, hidden, generator=g)
+    w = torch.randn(hidden, generator=g)
+    expected = ref.rms_norm(x, w, epsilon=1e-6)
+    actual = hip_rms_norm(x.to(gpu), w.to(gpu), epsilon=1e-6)
+    torch.cuda.synchronize()
+    assert_fp32_close(actual, expected)
+
+
+def test_rms_norm_fp16_and_output_dtype(gpu):
+    from stateful_llm_compiler_hip.backends import hip_rms_norm
+
+    announce("rms_norm fp16 in -> f32 out")
+    g = generator(5)
+    x = torch.randn(16, 1536, generator=g).half()
+    w = torch.randn(1536, generator=g).half()
+    expected = ref.rms_norm(x, w, epsilon=1e-5, output_dtype="f32")
+    actual = hip_rms_norm(x.to(gpu), w.to(gpu), epsilon=1e-5, output_dtype="f32")
+    torch.cuda.synchronize()
+    assert actual.dtype == torch.float32
+    assert_fp32_close(actual, expected, rtol=2e-3)
+
+
+# ---------------------------------------------------------------------- rope
+
+
+def _rope_inputs(batch, tokens, dtype, seed, past_max=4096):
+    g = generator(seed)
+    q = torch.randn(batch, tokens, 14, 64, generator=g).to(dtype).transpose(1, 2)
+    k = torch.randn(batch, tokens, 2, 64, generator=g).to(dtype).transpose(1, 2)
+    past = torch.randint(0, past_max + 1, (batch, 1), generator=g)
+    positions = past + torch.arange(tokens).view(1, -1)
+    inv_freq = 1.0 / (1e6 ** (torch.arange(0, 64, 2, dtype=torch.float32) / 64))
+    freqs = positions.float().unsqueeze(-1) * inv_freq.view(1, 1, -1)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return q, k, emb.cos().to(dtype), emb.sin().to(dtype)
+
+
+@pytest.mark.parametrize("batch", [1, 8, 64])
+@pytest.mark.parametrize("tokens", [1, 128, 512])
+def test_rope_config3_bitexact_bf16(gpu, batch, tokens):
+    from stateful_llm_compiler_hip.backends import hip_rope
+
+    announce(f"rope bf16 B={batch} T={tokens}")
+    q, k, cos, sin = _rope_inputs(batch, tokens, torch.bfloat16, batch * 1000 + tokens)
+    eq, ek = ref.rope(q, k, cos, sin)
+    qd = q.transpose(1, 2).contiguous().to(gpu).transpose(1, 2)
+    kd = k.transpose(1, 2).contiguous().to(gpu).transpose(1, 2)
+    aq, ak = hip_rope(qd, kd, cos.to(gpu), sin.to(gpu))
+    torch.cuda.synchronize()
+    assert_bitwise_equal(aq, eq)
+    assert_bitwise_equal(ak, ek)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_rope_other_dtypes_bitexact(gpu, dtype):
+    from stateful_llm_compiler_hip.backends import hip_rope
+
+    announce(f"rope {dtype}")
+    q, k, cos, sin = _rope_inputs(2, 7, dtype, 2026)
+    eq, ek = ref.rope(q, k, cos, sin)
+    aq, ak = hip_rope(q.to(gpu), k.to(gpu), cos.to(gpu), sin.to(gpu))
+    torch.cuda.synchronize()
+    assert_bitwise_equal(aq, eq)
+    assert_bitwise_equal(ak, ek)
