@@ -14,22 +14,13 @@ import torch
 from .. import _native
 
 
-# Split-sequence workspaces, one per (device, stream).  The kernel keeps the
-# ticket counters at the head of the workspace at zero between launches, so a
-# workspace is zero-filled once when it is created and then reused; launches
-# that share a workspace must be ordered (same stream).
-_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """Split-sequence partials; PyTorch's caching allocator makes this cheap and
+    keeps it legal inside HIP graph capture."""
 
-
-def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor | None:
     if nbytes <= 0:
         return None
-    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
-    workspace = _WORKSPACES.get(key)
-    if workspace is None or workspace.numel() < nbytes:
-        workspace = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-        _WORKSPACES[key] = workspace
-    return workspace
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
 
 
 def hip_decode_attention(
@@ -115,7 +106,7 @@ def hip_decode_attention(
         batch, query_heads, head_dim, mask_len, kv_heads, dtype, split_tokens
     )
     stream = _native.current_stream(query.device)
-    workspace = _workspace(query.device, stream, nbytes)
+    workspace = _workspace(query.device, nbytes)
     if attention_mask is None:
         mask_ptr, mask_dtype, mask_sb, mask_ss = None, 0, 0, 0
     else:

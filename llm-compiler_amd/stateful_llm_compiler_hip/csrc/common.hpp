@@ -85,6 +85,10 @@ __device__ __forceinline__ float load_as_f32(const void* base, int64_t index,
   return to_f32(static_cast<const f16_t*>(base)[index]);
 }
 
+__device__ __forceinline__ int slc_dtype_bytes(int dtype) {
+  return dtype == SLC_F32 ? 4 : 2;
+}
+
 __device__ __forceinline__ int64_t load_length(const void* lengths, int64_t b,
                                                int dtype) {
   if (dtype == SLC_I64) return static_cast<const int64_t*>(lengths)[b];

@@ -19,10 +19,11 @@
 //    softmax registers; V is staged through LDS (coalesced 16-byte writes,
 //    2-byte transposed reads on a bank-conflict-free padded layout).
 //  * Long sequences are split into chunks (split-sequence / flash-decoding) so a
-//    batch-32 decode still launches ~1000 workgroups for 256 CUs.  Each chunk
-//    writes its (max, sum, acc) partial; the last chunk of a (batch, kv-head)
-//    to finish (an atomic ticket per group) merges them and writes the output,
-//    so the whole op is a single launch.
+//    batch-32 decode still launches hundreds of workgroups for 256 CUs.  Each
+//    chunk writes its (max, sum, acc) partial and a small second kernel merges
+//    them.  (Merging inside the first kernel needs an agent-scope release per
+//    workgroup -- an L2 write-back -- which measured several times slower than
+//    the extra launch.)
 //  * Loops stop at the batch's own length, not at the capacity.
 // Other dtypes/shapes take a straightforward wave-per-token kernel.
 #include "common.hpp"
@@ -37,6 +38,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kTile = 32;   // tokens per wave iteration
 constexpr int kWaves = 4;   // wavefronts per workgroup
 constexpr int kMaxGroups = 16;
+constexpr int kMaxChunks = 256;  // split-sequence chunks per (batch, kv-head), merge LDS
 
 struct u16x8 {
   uint16_t v[8];
@@ -90,22 +92,23 @@ struct SharedLayout {
   static constexpr int kBytes = kVBytes > kCombineBytes ? kVBytes : kCombineBytes;
 };
 
-template <typename T, int D>
+// MK: mask element type (0 = no mask, else an slc_dtype tag + 1), a template
+// parameter so the load path has no data-dependent branches.
+template <typename T, int D, int MK>
 __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(
     const T* __restrict__ query, const T* __restrict__ key_buffer,
     const T* __restrict__ value_buffer, const void* __restrict__ lengths,
     int lengths_dtype, const void* __restrict__ mask, int mask_dtype,
     T* __restrict__ output, float* __restrict__ part_o,
-    float* __restrict__ part_ml, int* __restrict__ tickets, int q_heads,
-    int kv_heads, int groups,
-    int64_t capacity, int64_t mask_len, int64_t q_sb, int64_t q_sh,
-    int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int64_t m_sb, int64_t m_ss,
-    int64_t o_sb, int64_t o_sh, float scale_log2, int chunk_tokens,
+    float* __restrict__ part_ml, int q_heads,
+    int kv_heads, int groups, int64_t capacity, int64_t mask_len, int64_t q_sb,
+    int64_t q_sh, int64_t kv_sb, int kv_ss, int64_t kv_sh, int64_t m_sb,
+    int m_ss, int64_t o_sb, int64_t o_sh, float scale_log2, int chunk_tokens,
     int nchunks) {
   using M = Mfma<T>;
   using Layout = SharedLayout<T, D>;
-  constexpr int KK = D / 32;          // MFMA k-steps over head_dim
-  constexpr int DB = D / 16;          // 16-dim output blocks
+  constexpr int KK = D / 32;            // MFMA k-steps over head_dim
+  constexpr int DB = D / 16;            // 16-dim output blocks
   constexpr int UNITS_PER_ROW = D / 8;  // 16-byte units per V row
   constexpr int V_UNITS = kTile * UNITS_PER_ROW / 64;  // per lane per tile
   constexpr int VR = v_row<D>();
@@ -118,14 +121,15 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int g = lane >> 4;   // lane group: MFMA k-slice / output row block
-  const int c = lane & 15;   // MFMA row (A) / column (B, C)
+  const int g = lane >> 4;  // lane group: MFMA k-slice / output row block
+  const int c = lane & 15;  // MFMA row (A) / column (B, C)
 
-  int64_t end = slc::load_length(lengths, b, lengths_dtype);
-  end = end < 0 ? 0 : end;
-  end = end < mask_len ? end : mask_len;
-  end = end < capacity ? end : capacity;
-  const int64_t chunk_start = static_cast<int64_t>(chunk) * chunk_tokens;
+  int64_t end64 = slc::load_length(lengths, b, lengths_dtype);
+  end64 = end64 < 0 ? 0 : end64;
+  end64 = end64 < mask_len ? end64 : mask_len;
+  end64 = end64 < capacity ? end64 : capacity;
+  const int end = static_cast<int>(end64);  // host guarantees capacity < 2^31
+  const int chunk_start = chunk * chunk_tokens;
   if (nchunks > 1 && chunk_start >= end) {
     // Nothing of this batch in the chunk.  An empty sequence has no chunk to
     // merge, so chunk 0 writes its result (0/0 = NaN, like the reference's
@@ -138,8 +142,7 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(
     }
     return;
   }
-  int64_t chunk_end = chunk_start + chunk_tokens;
-  chunk_end = chunk_end < end ? chunk_end : end;
+  const int chunk_end = min(chunk_start + chunk_tokens, end);
 
   // Q^T as the B operand: lane (head c, k-slice g) holds dims kk*32+8g..+7.
   typename M::vec qv[KK];
@@ -156,8 +159,15 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(
     }
   }
 
-  const T* kbase = key_buffer + b * kv_sb + kvh * kv_sh;
-  const T* vbase = value_buffer + b * kv_sb + kvh * kv_sh;
+  // Per-(batch, kv-head) base pointers are wave-uniform; every per-lane offset
+  // below is a 32-bit byte offset from them.
+  const char* kbase = reinterpret_cast<const char*>(key_buffer + b * kv_sb + kvh * kv_sh);
+  const char* vbase = reinterpret_cast<const char*>(value_buffer + b * kv_sb + kvh * kv_sh);
+  const char* mbase = MK == 0 ? nullptr
+                              : static_cast<const char*>(mask) +
+                                    b * m_sb * slc::slc_dtype_bytes(mask_dtype);
+  const int row_bytes = kv_ss * 2;
+  const int mask_step = m_ss * slc::slc_dtype_bytes(mask_dtype);
   uint16_t* vtile = reinterpret_cast<uint16_t*>(smem) + wave * Layout::kVTileElems;
 
   float m_run = -INFINITY;
@@ -166,66 +176,78 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int64_t last_row = chunk_end > 0 ? chunk_end - 1 : 0;
-  auto load_tile = [&](int64_t t0, uint4 (&kr)[2][KK], uint4 (&vr)[V_UNITS]) {
+  const int last_row = chunk_end - 1;
+  // One tile = K rows for the S MFMAs, V rows for the LDS stage and the mask
+  // entries of the lane's 8 scores, all issued together so a single
+  // vmcnt wait covers them while the next tile is already in flight.
+  struct Tile {
+    uint4 k[2][KK];
+    uint4 v[V_UNITS];
+    float mk[8];
+  };
+  auto load_tile = [&](int t0, Tile& tile) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      int64_t tok = t0 + 16 * j + c;
-      tok = tok < last_row ? tok : last_row;
+      const int tok = min(t0 + 16 * j + c, last_row);
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
-        kr[j][kk] = *reinterpret_cast<const uint4*>(kbase + tok * kv_ss +
-                                                    kk * 32 + 8 * g);
+        tile.k[j][kk] = *reinterpret_cast<const uint4*>(
+            kbase + static_cast<uint32_t>(tok * row_bytes + (kk * 32 + 8 * g) * 2));
       }
     }
 #pragma unroll
     for (int i = 0; i < V_UNITS; ++i) {
       const int u = i * 64 + lane;
-      int64_t tok = t0 + u / UNITS_PER_ROW;
-      tok = tok < last_row ? tok : last_row;
-      vr[i] = *reinterpret_cast<const uint4*>(vbase + tok * kv_ss +
-                                              (u % UNITS_PER_ROW) * 8);
+      const int tok = min(t0 + u / UNITS_PER_ROW, last_row);
+      tile.v[i] = *reinterpret_cast<const uint4*>(
+          vbase + static_cast<uint32_t>(tok * row_bytes + (u % UNITS_PER_ROW) * 16));
     }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float mv = 0.0f;
+        if constexpr (MK != 0) {
+          const int tok = min(t0 + 16 * j + 4 * g + r, last_row);
+          const char* p = mbase + static_cast<uint32_t>(tok * mask_step);
+          if constexpr (MK == SLC_BF16 + 1) {
+            mv = slc::to_f32(*reinterpret_cast<const slc::bf16_t*>(p));
+          } else if constexpr (MK == SLC_F16 + 1) {
+            mv = slc::to_f32(*reinterpret_cast<const slc::f16_t*>(p));
+          } else {
+            mv = *reinterpret_cast<const float*>(p);
+          }
+        }
+        tile.mk[4 * j + r] = mv * kLog2e;
+      }
   };
 
-  int64_t t0 = chunk_start + static_cast<int64_t>(wave) * kTile;
-  uint4 kr[2][KK], vr[V_UNITS];
-  if (t0 < chunk_end) load_tile(t0, kr, vr);
-
-  for (; t0 < chunk_end; t0 += kWaves * kTile) {
-    // Prefetch the wave's next tile while this one is computed.
-    const int64_t t_next = t0 + kWaves * kTile;
-    uint4 kn[2][KK], vn[V_UNITS];
-    if (t_next < chunk_end) load_tile(t_next, kn, vn);
-
+  // Two tiles in flight per wave: while tile A is consumed, tile B (issued
+  // earlier) and the refill of A stream in.  Rows are clamped to the chunk, so
+  // the prefetches past the last tile are legal (and discarded).
+  auto compute_tile = [&](int t0, const Tile& tile) {
     // Stage V (rows past the chunk end are zeroed so 0 * garbage stays 0).
 #pragma unroll
     for (int i = 0; i < V_UNITS; ++i) {
       const int u = i * 64 + lane;
       const int row = u / UNITS_PER_ROW;
-      uint4 val = (t0 + row < chunk_end) ? vr[i] : make_uint4(0, 0, 0, 0);
-      uint2* dst = reinterpret_cast<uint2*>(vtile + row * VR +
-                                            (u % UNITS_PER_ROW) * 8);
+      const uint4 val = (t0 + row < chunk_end) ? tile.v[i] : make_uint4(0, 0, 0, 0);
+      uint2* dst = reinterpret_cast<uint2*>(vtile + row * VR + (u % UNITS_PER_ROW) * 8);
       dst[0] = make_uint2(val.x, val.y);
       dst[1] = make_uint2(val.z, val.w);
     }
 
-    // S^T tile: two 16-token MFMA blocks.
+    // S^T tile: two 16-token MFMA blocks; lane holds tokens 16j+4g+r, head c.
     float s[8];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       f32x4_t st = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        st = M::run(as_vec<T>(kr[j][kk]), qv[kk], st);
-      }
+      for (int kk = 0; kk < KK; ++kk) st = M::run(as_vec<T>(tile.k[j][kk]), qv[kk], st);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t tok = t0 + 16 * j + 4 * g + r;
-        float v = st[r] * scale_log2;
-        if (mask != nullptr && tok < chunk_end) {
-          v += slc::load_as_f32(mask, b * m_sb + tok * m_ss, mask_dtype) * kLog2e;
-        }
+        const int tok = t0 + 16 * j + 4 * g + r;
+        const float v = st[r] * scale_log2 + tile.mk[4 * j + r];
         s[4 * j + r] = tok < chunk_end ? v : -INFINITY;
       }
     }
@@ -268,13 +290,23 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
+  };
 
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) kr[j][kk] = kn[j][kk];
-#pragma unroll
-    for (int i = 0; i < V_UNITS; ++i) vr[i] = vn[i];
+  constexpr int kStride = kWaves * kTile;
+  // An empty chunk (a zero-length sequence when the grid has one chunk) has no
+  // row to clamp to (last_row would be -1): it loads nothing at all.
+  if (chunk_end > chunk_start) {
+    int t0 = chunk_start + wave * kTile;
+    Tile ta, tb;
+    load_tile(t0, ta);
+    load_tile(t0 + kStride, tb);
+    for (; t0 < chunk_end; t0 += 2 * kStride) {
+      compute_tile(t0, ta);
+      load_tile(t0 + 2 * kStride, ta);
+      if (t0 + kStride >= chunk_end) break;
+      compute_tile(t0 + kStride, tb);
+      load_tile(t0 + 3 * kStride, tb);
+    }
   }
 
   // Finish the per-lane partial sums of l over the 4 lane groups.
@@ -322,37 +354,68 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(
       }
     }
   }
-  if (nchunks == 1) return;
+}
 
-  // Split-sequence merge: the last chunk of this (batch, kv-head) to arrive
-  // combines every chunk's partial.  Release the partials, take a ticket,
-  // acquire the other chunks' partials.
-  __shared__ int is_last;
-  __threadfence();
-  __syncthreads();
+// Merge the split-sequence partials: one workgroup per (batch, kv-head).
+// Per-chunk weights exp2(m_i - M) / L go to LDS first; each output element is
+// then an independent weighted sum over the chunks.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void decode_attention_merge_kernel(
+    const float* __restrict__ part_o, const float* __restrict__ part_ml,
+    const void* __restrict__ lengths, int lengths_dtype, T* __restrict__ output,
+    int q_heads, int kv_heads, int groups, int64_t capacity, int64_t mask_len,
+    int64_t o_sb, int64_t o_sh, int chunk_tokens, int nchunks) {
+  __shared__ float sm_w[kMaxGroups * kMaxChunks];
+  __shared__ float sm_inv[kMaxGroups];
+  const int kvh = blockIdx.x % kv_heads;
+  const int64_t b = blockIdx.x / kv_heads;
+  const int tid = threadIdx.x;
+  int64_t end = slc::load_length(lengths, b, lengths_dtype);
+  end = end < 0 ? 0 : end;
+  end = end < mask_len ? end : mask_len;
+  end = end < capacity ? end : capacity;
+  if (end == 0) return;  // written (NaN) by the split kernel's chunk 0
   const int nvalid = static_cast<int>((end + chunk_tokens - 1) / chunk_tokens);
-  int* ticket = tickets + b * kv_heads + kvh;
-  if (tid == 0) is_last = atomicAdd(ticket, 1) == nvalid - 1;
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  for (int idx = tid; idx < groups * D; idx += 256) {
-    const int qh = kvh * groups + idx / D;
-    const int d = idx % D;
-    const int64_t base = (b * q_heads + qh) * nchunks;
-    float mmax = -INFINITY;
-    for (int i = 0; i < nvalid; ++i) mmax = fmaxf(mmax, part_ml[2 * (base + i)]);
-    const float mu = mmax == -INFINITY ? 0.0f : mmax;
-    float lsum = 0.0f, osum = 0.0f;
-    for (int i = 0; i < nvalid; ++i) {
-      const float f = fast_exp2(part_ml[2 * (base + i)] - mu);
-      lsum += f * part_ml[2 * (base + i) + 1];
-      osum += f * part_o[(base + i) * D + d];
-    }
-    output[b * o_sb + qh * o_sh + d] = slc::from_f32<T>(osum / lsum);
+  const int64_t head0 = b * q_heads + kvh * groups;
+  for (int idx = tid; idx < groups * nvalid; idx += 256) {
+    const int head = idx / nvalid;
+    const int i = idx % nvalid;
+    sm_w[head * kMaxChunks + i] = part_ml[2 * ((head0 + head) * nchunks + i)];
   }
-  // Leave the ticket at zero for the next launch that uses this workspace.
-  if (tid == 0) *ticket = 0;
+  __syncthreads();
+  if (tid < groups) {
+    const int head = tid;
+    const int64_t base = (head0 + head) * nchunks;
+    float mmax = -INFINITY;
+    for (int i = 0; i < nvalid; ++i) mmax = fmaxf(mmax, sm_w[head * kMaxChunks + i]);
+    const float mu = mmax == -INFINITY ? 0.0f : mmax;
+    float lsum = 0.0f;
+    for (int i = 0; i < nvalid; ++i) {
+      const float f = fast_exp2(sm_w[head * kMaxChunks + i] - mu);
+      sm_w[head * kMaxChunks + i] = f;
+      lsum += f * part_ml[2 * (base + i) + 1];
+    }
+    sm_inv[head] = 1.0f / lsum;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < groups * D; idx += 256) {
+    const int head = idx / D;
+    const int d = idx % D;
+    const float* po = part_o + (head0 + head) * nchunks * D + d;
+    const float* w = sm_w + head * kMaxChunks;
+    float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+    int i = 0;
+    for (; i + 4 <= nvalid; i += 4) {
+      o0 += w[i] * po[(i + 0) * D];
+      o1 += w[i + 1] * po[(i + 1) * D];
+      o2 += w[i + 2] * po[(i + 2) * D];
+      o3 += w[i + 3] * po[(i + 3) * D];
+    }
+    for (; i < nvalid; ++i) o0 += w[i] * po[i * D];
+    const int qh = kvh * groups + head;
+    output[b * o_sb + qh * o_sh + d] =
+        slc::from_f32<T>(((o0 + o1) + (o2 + o3)) * sm_inv[head]);
+  }
 }
 
 // Any dtype / head_dim <= 256 / any group size: one workgroup per
@@ -439,30 +502,31 @@ bool mfma_eligible(int dtype, int64_t head_dim, int64_t groups) {
          (head_dim == 64 || head_dim == 128) && groups <= kMaxGroups;
 }
 
-// Sequence chunk of the split-sequence grid: the smallest multiple of the
-// workgroup's 128-token sweep that keeps the grid near 4 workgroups per CU
-// (256 CUs on MI355X).
+// Sequence chunk of the split-sequence grid: the smallest power-of-two
+// multiple of the workgroup's 128-token sweep that keeps the grid at about one
+// workgroup per CU (256 CUs on MI355X); longer chunks amortise the per-wave
+// pipeline fill and keep the partials small.
 int64_t choose_chunk(int64_t batch, int64_t kv_heads, int64_t mask_len,
                      int64_t split_tokens) {
   const int64_t sweep = kWaves * kTile;
+  int64_t chunk;
   if (split_tokens > 0) {
-    return slc_host::ceil_div(split_tokens, sweep) * sweep;
+    chunk = slc_host::ceil_div(split_tokens, sweep) * sweep;
+  } else {
+    const int64_t target_groups = 256;
+    chunk = 2 * sweep;
+    while (batch * kv_heads * slc_host::ceil_div(mask_len, chunk) > target_groups) {
+      chunk *= 2;
+    }
   }
-  const int64_t target_groups = 1024;
-  int64_t chunk = 2 * sweep;
-  while (batch * kv_heads * slc_host::ceil_div(mask_len, chunk) > target_groups) {
-    chunk *= 2;
-  }
+  // The merge keeps every chunk's weight of a (batch, kv-head) in LDS.
+  while (slc_host::ceil_div(mask_len, chunk) > kMaxChunks) chunk *= 2;
   return chunk;
 }
 
 // Workspace layout of the split-sequence path:
-//   int   tickets[batch * kv_heads]            (zero between launches)
 //   float part_o[batch * q_heads * nchunks * D]
 //   float part_ml[batch * q_heads * nchunks * 2]
-int64_t tickets_bytes(int64_t batch, int64_t kv_heads) {
-  return slc_host::ceil_div(batch * kv_heads * 4, 256) * 256;
-}
 
 template <typename T, int D>
 int launch_mfma(const void* query, const void* kb, const void* vb,
@@ -471,28 +535,46 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
                 int64_t q_heads, int64_t kv_heads, int64_t capacity,
                 int64_t mask_len, const int64_t* st, float scale_log2,
                 int64_t chunk, int64_t nchunks, hipStream_t stream) {
-  int* tickets = nullptr;
   float* part_o = nullptr;
   float* part_ml = nullptr;
   if (nchunks > 1) {
-    tickets = static_cast<int*>(workspace);
-    part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                      tickets_bytes(batch, kv_heads));
+    part_o = static_cast<float*>(workspace);
     part_ml = part_o + batch * q_heads * nchunks * D;
   }
   const int groups = static_cast<int>(q_heads / kv_heads);
-  hipLaunchKernelGGL(
-      (decode_attention_mfma_kernel<T, D>),
-      dim3(static_cast<unsigned>(nchunks), static_cast<unsigned>(kv_heads),
-           static_cast<unsigned>(batch)),
-      dim3(256), 0, stream, static_cast<const T*>(query),
-      static_cast<const T*>(kb), static_cast<const T*>(vb), lengths,
-      lengths_dtype, mask, mask_dtype, static_cast<T*>(output), part_o, part_ml,
-      tickets, static_cast<int>(q_heads), static_cast<int>(kv_heads), groups,
-      capacity, mask_len, st[0], st[1], st[2], st[3], st[4], st[5], st[6],
-      st[7], st[8], scale_log2, static_cast<int>(chunk),
-      static_cast<int>(nchunks));
-  return slc_host::check_launch("slc_hip_decode_attention");
+  const dim3 grid(static_cast<unsigned>(nchunks), static_cast<unsigned>(kv_heads),
+                  static_cast<unsigned>(batch));
+#define SLC_MFMA(MK)                                                          \
+  hipLaunchKernelGGL((decode_attention_mfma_kernel<T, D, MK>), grid, dim3(256), \
+                     0, stream, static_cast<const T*>(query),                 \
+                     static_cast<const T*>(kb), static_cast<const T*>(vb),    \
+                     lengths, lengths_dtype, mask, mask_dtype,                \
+                     static_cast<T*>(output), part_o, part_ml,                \
+                     static_cast<int>(q_heads), static_cast<int>(kv_heads),   \
+                     groups, capacity, mask_len, st[0], st[1], st[2],         \
+                     static_cast<int>(st[3]), st[4], st[5],                   \
+                     static_cast<int>(st[6]), st[7], st[8], scale_log2,       \
+                     static_cast<int>(chunk), static_cast<int>(nchunks))
+  if (mask == nullptr) {
+    SLC_MFMA(0);
+  } else if (mask_dtype == SLC_BF16) {
+    SLC_MFMA(SLC_BF16 + 1);
+  } else if (mask_dtype == SLC_F16) {
+    SLC_MFMA(SLC_F16 + 1);
+  } else {
+    SLC_MFMA(SLC_F32 + 1);
+  }
+#undef SLC_MFMA
+  int rc = slc_host::check_launch("slc_hip_decode_attention");
+  if (rc != SLC_OK || nchunks == 1) return rc;
+  hipLaunchKernelGGL((decode_attention_merge_kernel<T, D>),
+                     dim3(static_cast<unsigned>(batch * kv_heads)), dim3(256), 0,
+                     stream, part_o, part_ml, lengths, lengths_dtype,
+                     static_cast<T*>(output), static_cast<int>(q_heads),
+                     static_cast<int>(kv_heads), groups, capacity, mask_len,
+                     st[7], st[8], static_cast<int>(chunk),
+                     static_cast<int>(nchunks));
+  return slc_host::check_launch("slc_hip_decode_attention(merge)");
 }
 
 template <typename T>
@@ -537,8 +619,7 @@ extern "C" int64_t slc_hip_decode_attention_workspace_size(
   const int64_t chunk = choose_chunk(batch, kv_heads, mask_len, split_tokens);
   const int64_t nchunks = slc_host::ceil_div(mask_len, chunk);
   if (nchunks <= 1) return 0;
-  return tickets_bytes(batch, kv_heads) +
-         batch * q_heads * nchunks * (head_dim + 2) * static_cast<int64_t>(sizeof(float));
+  return batch * q_heads * nchunks * (head_dim + 2) * static_cast<int64_t>(sizeof(float));
 }
 
 extern "C" int slc_hip_decode_attention(
@@ -586,14 +667,18 @@ extern "C" int slc_hip_decode_attention(
     const int64_t strides = q_stride_b | q_stride_h | kv_stride_b |
                             kv_stride_s | kv_stride_h;
     use_mfma = (bits & 15) == 0 && (strides & 7) == 0;
+    // Per-lane offsets inside one (batch, kv-head) slice are 32-bit.
+    const int64_t mask_es = mask == nullptr ? 0 : slc_host::dtype_size(mask_dtype);
+    use_mfma = use_mfma && kv_stride_s > 0 && mask_stride_s >= 0 &&
+               capacity * kv_stride_s * 2 < (int64_t{1} << 31) &&
+               mask_len * mask_stride_s * mask_es < (int64_t{1} << 31) &&
+               capacity < (int64_t{1} << 30);
   }
   if (use_mfma) {
     const int64_t chunk = choose_chunk(batch, kv_heads, ml, split_tokens);
     const int64_t nchunks = slc_host::ceil_div(ml, chunk);
     const int64_t need =
-        nchunks > 1 ? tickets_bytes(batch, kv_heads) +
-                          batch * q_heads * nchunks * (head_dim + 2) * 4
-                    : 0;
+        nchunks > 1 ? batch * q_heads * nchunks * (head_dim + 2) * 4 : 0;
     SLC_REQUIRE(nchunks <= 0x7fffffff, "slc_hip_decode_attention: too many chunks");
     SLC_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need),
                 "slc_hip_decode_attention: workspace of %lld bytes needed, got "
