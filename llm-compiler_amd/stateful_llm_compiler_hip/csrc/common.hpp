@@ -30,13 +30,10 @@ __device__ __forceinline__ float to_f32(f16_t x) {
   return static_cast<float>(h);
 }
 
+// float -> bf16, round to nearest even (v_cvt_pk_bf16_f32 on gfx950; NaN stays
+// NaN), the same rounding PyTorch applies.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t x = __float_as_uint(f);
-  if ((x & 0x7fffffffu) > 0x7f800000u) {
-    return static_cast<uint16_t>((x >> 16) | 0x0040u);
-  }
-  x += 0x7fffu + ((x >> 16) & 1u);
-  return static_cast<uint16_t>(x >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 template <typename T>

@@ -36,7 +36,12 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kTile = 32;   // tokens per wave iteration
-constexpr int kWaves = 4;   // wavefronts per workgroup
+#ifndef SLC_DECODE_WAVES
+#define SLC_DECODE_WAVES 4
+#endif
+constexpr int kWaves = SLC_DECODE_WAVES;  // wavefronts per split-kernel workgroup
+constexpr int kThreads = kWaves * 64;
+constexpr int kGenericWaves = 4;          // wavefronts of the generic kernel
 constexpr int kMaxGroups = 16;
 constexpr int kMaxChunks = 256;  // split-sequence chunks per (batch, kv-head), merge LDS
 
@@ -92,26 +97,47 @@ struct SharedLayout {
   static constexpr int kBytes = kVBytes > kCombineBytes ? kVBytes : kCombineBytes;
 };
 
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource over [base, base + bytes): loads at or past the end
+// return zero without touching memory (the hardware range check), which is how
+// rows past the chunk end are handled -- no clamps, no branches.
+// Callers pass wave-uniform values; readfirstlane states that to the compiler
+// so the resource stays in scalar registers (no per-lane waterfall loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  const uint64_t address = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(address));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(address >> 32));
+  void* uniform = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(uniform, 0, __builtin_amdgcn_readfirstlane(bytes),
+                                           0x00020000);
+}
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int offset) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 0));
+}
+
+// Rescale the running (max, sum, acc) only when a tile's max exceeds the
+// running max by more than this (log2 units): probabilities stay <= 2^8, and
+// most tiles skip the accumulator rescale entirely.
+constexpr float kRescaleThreshold = 8.0f;
+
 // MK: mask element type (0 = no mask, else an slc_dtype tag + 1), a template
 // parameter so the load path has no data-dependent branches.
 template <typename T, int D, int MK>
-__global__ __launch_bounds__(256) void decode_attention_mfma_kernel(
+__global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     const T* __restrict__ query, const T* __restrict__ key_buffer,
     const T* __restrict__ value_buffer, const void* __restrict__ lengths,
     int lengths_dtype, const void* __restrict__ mask, int mask_dtype,
     T* __restrict__ output, float* __restrict__ part_o,
-    float* __restrict__ part_ml, int q_heads,
-    int kv_heads, int groups, int64_t capacity, int64_t mask_len, int64_t q_sb,
-    int64_t q_sh, int64_t kv_sb, int kv_ss, int64_t kv_sh, int64_t m_sb,
-    int m_ss, int64_t o_sb, int64_t o_sh, float scale_log2, int chunk_tokens,
+    float* __restrict__ part_ml, int q_heads, int kv_heads, int groups,
+    int64_t capacity, int64_t mask_len, int64_t q_sb, int64_t q_sh,
+    int64_t kv_sb, int kv_ss, int64_t kv_sh, int64_t m_sb, int m_ss,
+    int64_t o_sb, int64_t o_sh, float scale_log2, int chunk_tokens,
     int nchunks) {
   using M = Mfma<T>;
   using Layout = SharedLayout<T, D>;
   constexpr int KK = D / 32;            // MFMA k-steps over head_dim
   constexpr int DB = D / 16;            // 16-dim output blocks
-  constexpr int UNITS_PER_ROW = D / 8;  // 16-byte units per V row
-  constexpr int V_UNITS = kTile * UNITS_PER_ROW / 64;  // per lane per tile
-  constexpr int VR = v_row<D>();
 
   __shared__ __attribute__((aligned(16))) unsigned char smem[Layout::kBytes];
 
@@ -119,7 +145,9 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(
   const int kvh = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  // readfirstlane: the wave index is wave-uniform, so everything derived from
+  // it (tile starts, buffer resources) lives in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int g = lane >> 4;  // lane group: MFMA k-slice / output row block
   const int c = lane & 15;  // MFMA row (A) / column (B, C)
@@ -128,14 +156,14 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(
   end64 = end64 < 0 ? 0 : end64;
   end64 = end64 < mask_len ? end64 : mask_len;
   end64 = end64 < capacity ? end64 : capacity;
-  const int end = static_cast<int>(end64);  // host guarantees capacity < 2^31
+  const int end = static_cast<int>(end64);  // host guarantees capacity < 2^30
   const int chunk_start = chunk * chunk_tokens;
   if (nchunks > 1 && chunk_start >= end) {
-    // Nothing of this batch in the chunk.  An empty sequence has no chunk to
+    // Nothing of this batch in the chunk.  An empty sequence has no partial to
     // merge, so chunk 0 writes its result (0/0 = NaN, like the reference's
     // softmax over an all -inf row).
     if (chunk == 0 && end == 0) {
-      for (int idx = tid; idx < groups * D; idx += 256) {
+      for (int idx = tid; idx < groups * D; idx += kThreads) {
         const int qh = kvh * groups + idx / D;
         output[b * o_sb + qh * o_sh + idx % D] = slc::from_f32<T>(0.0f / 0.0f);
       }
@@ -159,16 +187,28 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(
     }
   }
 
-  // Per-(batch, kv-head) base pointers are wave-uniform; every per-lane offset
-  // below is a 32-bit byte offset from them.
   const char* kbase = reinterpret_cast<const char*>(key_buffer + b * kv_sb + kvh * kv_sh);
   const char* vbase = reinterpret_cast<const char*>(value_buffer + b * kv_sb + kvh * kv_sh);
+  constexpr int kMaskBytes = MK == SLC_F32 + 1 ? 4 : 2;
   const char* mbase = MK == 0 ? nullptr
-                              : static_cast<const char*>(mask) +
-                                    b * m_sb * slc::slc_dtype_bytes(mask_dtype);
+                              : static_cast<const char*>(mask) + b * m_sb * kMaskBytes;
   const int row_bytes = kv_ss * 2;
-  const int mask_step = m_ss * slc::slc_dtype_bytes(mask_dtype);
-  uint16_t* vtile = reinterpret_cast<uint16_t*>(smem) + wave * Layout::kVTileElems;
+  const int mask_step = m_ss * kMaskBytes;
+
+  // Loop-invariant per-lane byte offsets inside a tile.
+  int koff[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) koff[j] = (16 * j + c) * row_bytes + 16 * g;
+  // 0/1 selector B operands: sel[h][k][n] = (k == n + 16h), so that
+  // V_block(16 x 32 dims) . sel[h] = the dims 16h..16h+15 of the block.
+  typename M::vec sel[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    u16x8 e;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) e.v[i] = (8 * g + i == c + 16 * h) ? bits_of<T>(1.0f) : 0;
+    sel[h] = __builtin_bit_cast(typename M::vec, e);
+  }
 
   float m_run = -INFINITY;
   float l_run = 0.0f;
@@ -176,67 +216,53 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int last_row = chunk_end - 1;
-  // One tile = K rows for the S MFMAs, V rows for the LDS stage and the mask
-  // entries of the lane's 8 scores, all issued together so a single
-  // vmcnt wait covers them while the next tile is already in flight.
   struct Tile {
     uint4 k[2][KK];
-    uint4 v[V_UNITS];
-    float mk[8];
+    uint4 v[2][KK];
+    float mk[MK == 0 ? 1 : 8];
   };
+  // One tile = 32 token rows of K and V (and the mask entries of the lane's 8
+  // scores) through buffer resources bounded at the chunk end.  K and V use
+  // the same lane layout: lane (row c, k-slice g) of 16-row block j holds
+  // dims kk*32+8g..+7 of token t0+16j+c.
   auto load_tile = [&](int t0, Tile& tile) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int tok = min(t0 + 16 * j + c, last_row);
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        tile.k[j][kk] = *reinterpret_cast<const uint4*>(
-            kbase + static_cast<uint32_t>(tok * row_bytes + (kk * 32 + 8 * g) * 2));
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < V_UNITS; ++i) {
-      const int u = i * 64 + lane;
-      const int tok = min(t0 + u / UNITS_PER_ROW, last_row);
-      tile.v[i] = *reinterpret_cast<const uint4*>(
-          vbase + static_cast<uint32_t>(tok * row_bytes + (u % UNITS_PER_ROW) * 16));
-    }
+    const int rows = chunk_end - t0;
+    const int nbytes = rows > 0 ? rows * row_bytes : 0;
+    const int64_t shift = static_cast<int64_t>(t0) * row_bytes;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + shift, nbytes);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + shift, nbytes);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float mv = 0.0f;
-        if constexpr (MK != 0) {
-          const int tok = min(t0 + 16 * j + 4 * g + r, last_row);
-          const char* p = mbase + static_cast<uint32_t>(tok * mask_step);
-          if constexpr (MK == SLC_BF16 + 1) {
-            mv = slc::to_f32(*reinterpret_cast<const slc::bf16_t*>(p));
-          } else if constexpr (MK == SLC_F16 + 1) {
-            mv = slc::to_f32(*reinterpret_cast<const slc::f16_t*>(p));
-          } else {
-            mv = *reinterpret_cast<const float*>(p);
-          }
-        }
-        tile.mk[4 * j + r] = mv * kLog2e;
+      for (int kk = 0; kk < KK; ++kk) {
+        tile.k[j][kk] = buffer_load16(rk, koff[j] + kk * 64);
+        tile.v[j][kk] = buffer_load16(rv, koff[j] + kk * 64);
       }
+    if constexpr (MK != 0) {
+      const __amdgpu_buffer_rsrc_t rm =
+          make_rsrc(mbase + static_cast<int64_t>(t0) * mask_step,
+                    rows > 0 ? rows * mask_step : 0);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int off = (16 * j + 4 * g + r) * mask_step;
+          float mv;
+          if constexpr (MK == SLC_F32 + 1) {
+            mv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, off, 0, 0));
+          } else if constexpr (MK == SLC_BF16 + 1) {
+            mv = slc::to_f32(slc::bf16_t{static_cast<uint16_t>(
+                __builtin_amdgcn_raw_buffer_load_b16(rm, off, 0, 0))});
+          } else {
+            mv = slc::to_f32(slc::f16_t{static_cast<uint16_t>(
+                __builtin_amdgcn_raw_buffer_load_b16(rm, off, 0, 0))});
+          }
+          tile.mk[4 * j + r] = mv * kLog2e;
+        }
+    }
   };
 
-  // Two tiles in flight per wave: while tile A is consumed, tile B (issued
-  // earlier) and the refill of A stream in.  Rows are clamped to the chunk, so
-  // the prefetches past the last tile are legal (and discarded).
   auto compute_tile = [&](int t0, const Tile& tile) {
-    // Stage V (rows past the chunk end are zeroed so 0 * garbage stays 0).
-#pragma unroll
-    for (int i = 0; i < V_UNITS; ++i) {
-      const int u = i * 64 + lane;
-      const int row = u / UNITS_PER_ROW;
-      const uint4 val = (t0 + row < chunk_end) ? tile.v[i] : make_uint4(0, 0, 0, 0);
-      uint2* dst = reinterpret_cast<uint2*>(vtile + row * VR + (u % UNITS_PER_ROW) * 8);
-      dst[0] = make_uint2(val.x, val.y);
-      dst[1] = make_uint2(val.z, val.w);
-    }
-
     // S^T tile: two 16-token MFMA blocks; lane holds tokens 16j+4g+r, head c.
     float s[8];
 #pragma unroll
@@ -246,9 +272,9 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(
       for (int kk = 0; kk < KK; ++kk) st = M::run(as_vec<T>(tile.k[j][kk]), qv[kk], st);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int tok = t0 + 16 * j + 4 * g + r;
-        const float v = st[r] * scale_log2 + tile.mk[4 * j + r];
-        s[4 * j + r] = tok < chunk_end ? v : -INFINITY;
+        float v = st[r] * scale_log2;
+        if constexpr (MK != 0) v += tile.mk[4 * j + r];
+        s[4 * j + r] = t0 + 16 * j + 4 * g + r < chunk_end ? v : -INFINITY;
       }
     }
 
@@ -257,9 +283,15 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(
     for (int i = 1; i < 8; ++i) mx = fmaxf(mx, s[i]);
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = fast_exp2(m_run - m_use);
+    if (__any(mx > m_run + kRescaleThreshold)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.0f : m_new));
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) acc[db] = acc[db] * alpha;
+      m_run = m_new;
+    }
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
     u16x8 pbits;
     float psum = 0.0f;
 #pragma unroll
@@ -268,34 +300,33 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(
       psum += p;
       pbits.v[i] = bits_of<T>(p);
     }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
+    l_run += psum;
     const typename M::vec pv = __builtin_bit_cast(typename M::vec, pbits);
 
-    // LDS writes above must land before the transposed reads below.
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-
+    // O^T[dim, head] += V^T . P^T.  V^T is produced in registers: V rows times
+    // a 0/1 selector (one MFMA per 16 tokens x 16 dims) land as lane
+    // (dim c, tokens 4g..4g+3) -- exactly the token slots of the P operand.
+    // The products are exact (x * 1 + 0), so converting back is lossless.
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
+      const f32x4_t zero = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      const f32x4_t x0 = M::run(as_vec<T>(tile.v[0][db >> 1]), sel[db & 1], zero);
+      const f32x4_t x1 = M::run(as_vec<T>(tile.v[1][db >> 1]), sel[db & 1], zero);
       u16x8 a;
-      const int dim = db * 16 + c;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int row = i < 4 ? 4 * g + i : 16 + 4 * g + (i - 4);
-        a.v[i] = vtile[row * VR + dim];
+      for (int r = 0; r < 4; ++r) {
+        a.v[r] = bits_of<T>(x0[r]);
+        a.v[4 + r] = bits_of<T>(x1[r]);
       }
-      acc[db] = acc[db] * alpha;
       acc[db] = M::run(__builtin_bit_cast(typename M::vec, a), pv, acc[db]);
     }
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
   };
 
+  // Two tiles in flight per wave: while tile A is consumed, tile B (issued
+  // earlier) and the refill of A stream in.  Prefetches past the chunk end are
+  // zero-length buffer ranges and touch no memory.
   constexpr int kStride = kWaves * kTile;
-  // An empty chunk (a zero-length sequence when the grid has one chunk) has no
-  // row to clamp to (last_row would be -1): it loads nothing at all.
-  if (chunk_end > chunk_start) {
+  {
     int t0 = chunk_start + wave * kTile;
     Tile ta, tb;
     load_tile(t0, ta);
@@ -328,7 +359,7 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(
       sm_o[(wave * kMaxGroups + c) * D + db * 16 + 4 * g + r] = acc[db][r];
   __syncthreads();
 
-  for (int idx = tid; idx < groups * D; idx += 256) {
+  for (int idx = tid; idx < groups * D; idx += kThreads) {
     const int head = idx / D;
     const int d = idx % D;
     float mmax = -INFINITY;
@@ -430,9 +461,9 @@ __global__ __launch_bounds__(256) void decode_attention_generic_kernel(
     int64_t capacity, int64_t mask_len, int64_t q_sb, int64_t q_sh,
     int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int64_t m_sb, int64_t m_ss,
     int64_t o_sb, int64_t o_sh, float scale_log2) {
-  __shared__ float sm_m[kWaves];
-  __shared__ float sm_l[kWaves];
-  __shared__ float sm_o[kWaves][NI * 64];
+  __shared__ float sm_m[kGenericWaves];
+  __shared__ float sm_l[kGenericWaves];
+  __shared__ float sm_o[kGenericWaves][NI * 64];
   const int64_t b = blockIdx.x / q_heads;
   const int h = blockIdx.x % q_heads;
   const int kvh = h / groups;
@@ -453,7 +484,7 @@ __global__ __launch_bounds__(256) void decode_attention_generic_kernel(
   float m_run = -INFINITY, l_run = 0.0f;
   const T* kbase = key_buffer + b * kv_sb + kvh * kv_sh;
   const T* vbase = value_buffer + b * kv_sb + kvh * kv_sh;
-  for (int64_t t = wave; t < end; t += kWaves) {
+  for (int64_t t = wave; t < end; t += kGenericWaves) {
     float dot = 0.0f;
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
@@ -485,10 +516,10 @@ __global__ __launch_bounds__(256) void decode_attention_generic_kernel(
   __syncthreads();
   for (int d = threadIdx.x; d < head_dim; d += 256) {
     float mmax = -INFINITY;
-    for (int w = 0; w < kWaves; ++w) mmax = fmaxf(mmax, sm_m[w]);
+    for (int w = 0; w < kGenericWaves; ++w) mmax = fmaxf(mmax, sm_m[w]);
     const float mu = mmax == -INFINITY ? 0.0f : mmax;
     float lsum = 0.0f, osum = 0.0f;
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < kGenericWaves; ++w) {
       const float f = exp2f(sm_m[w] - mu);
       lsum += f * sm_l[w];
       osum += f * sm_o[w][d];
@@ -545,7 +576,7 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
   const dim3 grid(static_cast<unsigned>(nchunks), static_cast<unsigned>(kv_heads),
                   static_cast<unsigned>(batch));
 #define SLC_MFMA(MK)                                                          \
-  hipLaunchKernelGGL((decode_attention_mfma_kernel<T, D, MK>), grid, dim3(256), \
+  hipLaunchKernelGGL((decode_attention_mfma_kernel<T, D, MK>), grid, dim3(kThreads), \
                      0, stream, static_cast<const T*>(query),                 \
                      static_cast<const T*>(kb), static_cast<const T*>(vb),    \
                      lengths, lengths_dtype, mask, mask_dtype,                \
