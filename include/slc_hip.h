@@ -147,6 +147,38 @@ SLC_API int slc_hip_rope(const void* query, const void* key, const void* cosine,
                  int64_t sin_st, int64_t qo_sb, int64_t qo_sh, int64_t qo_st,
                  int64_t ko_sb, int64_t ko_sh, int64_t ko_st, void* stream);
 
+/*
+ * linear: output[m, n] = sum_k input[m, k] * weight[n, k] (+ bias[n]),
+ * fp32 accumulation, one rounding to dtype on store.
+ *   input  : rows x in_features, row stride in_stride_row (elements)
+ *   weight : out_features x in_features, contiguous (PyTorch Linear layout)
+ *   bias   : out_features or NULL
+ *   output : rows x out_features, row stride out_stride_row
+ */
+SLC_API int slc_hip_linear(const void* input, const void* weight,
+                           const void* bias, void* output, int dtype,
+                           int64_t rows, int64_t out_features,
+                           int64_t in_features, int64_t in_stride_row,
+                           int64_t out_stride_row, void* stream);
+
+/*
+ * prefill_attention: multi-token GQA attention.
+ *   query [B, QH, T, D], key/value [B, KVH, T, D] with (sb, sh, st) strides,
+ *   mask  : additive [B, 1, T, T] with (m_sb, m_sq, m_sk) strides, dtype
+ *           mask_dtype, or NULL (= zeros)
+ *   causal: nonzero removes keys after each query (the op's causal=True)
+ *   output [B, QH, T, D] with (o_sb, o_sh, o_st) strides, dtype of query
+ * kv head of query head h is h / (QH / KVH).
+ */
+SLC_API int slc_hip_prefill_attention(
+    const void* query, const void* key, const void* value, const void* mask,
+    int mask_dtype, void* output, int dtype, int64_t batch, int64_t q_heads,
+    int64_t kv_heads, int64_t tokens, int64_t head_dim, int causal, int64_t q_sb,
+    int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t m_sb, int64_t m_sq,
+    int64_t m_sk, int64_t o_sb, int64_t o_sh, int64_t o_st, float scale,
+    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -63,6 +63,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I,
         [_P, _P, _P, _I, _I, _I, _I, _L, _L, _L, _L, _F, _I, _P],
     ),
+    "slc_hip_linear": (
+        _I,
+        [_P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _P],
+    ),
+    "slc_hip_prefill_attention": (
+        _I,
+        [_P, _P, _P, _P, _I, _P, _I, _L, _L, _L, _L, _L, _I] + [_L] * 15 + [_F, _P],
+    ),
     "slc_hip_rope": (
         _I,
         [_P] * 6 + [_I] + [_L] * 5 + [_L] * 16 + [_P],

@@ -1,0 +1,296 @@
+// linear: Y[M, N] = X[M, K] . W[N, K]^T (+ bias[N]), fp32 accumulation.
+//
+// Semantics: src/stateful_llm_compiler/backends/triton_linear.py:10-84 (fp32
+// accumulate, bias added in fp32, one rounding on store) and the reference
+// executor's F.linear (execution.py:694-705).
+//
+// MI355X design (bf16 / fp16):
+//  * X rows and W rows are both K-contiguous, which is exactly the operand
+//    layout of v_mfma_f32_16x16x32 (A rows = M, B columns = N, 8 consecutive k
+//    per lane), so neither operand needs a transpose.
+//  * Global -> LDS with fully coalesced 16-byte loads (8 lanes per 128-byte
+//    row segment of a 64-wide K tile), through buffer resources whose range
+//    check zero-fills rows past M / N.  LDS rows are XOR-swizzled on 16-byte
+//    chunks so the 16-row MFMA operand reads (ds_read_b128) are free of bank
+//    conflicts.  Two LDS buffers: tile k+1 is fetched into registers while
+//    tile k is multiplied.
+//  * The tile shape follows M: decode-sized M (<= 64) streams W with narrow
+//    M tiles and many workgroups along N (HBM-bound), prefill-sized M uses
+//    128 x 128 tiles (MFMA-bound).
+// fp32 (and shapes the vector path cannot take) use a classic LDS-tiled
+// FMA kernel.
+#include "common.hpp"
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct Mfma;
+template <>
+struct Mfma<slc::bf16_t> {
+  using vec = bf16x8_t;
+  static __device__ __forceinline__ f32x4_t run(vec a, vec b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma<slc::f16_t> {
+  using vec = f16x8_t;
+  static __device__ __forceinline__ f32x4_t run(vec a, vec b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const uint64_t address = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(address));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(address >> 32));
+  void* uniform = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+  const int clamped = bytes > 0x7fffffff ? 0x7fffffff : static_cast<int>(bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(uniform, 0, __builtin_amdgcn_readfirstlane(clamped),
+                                           0x00020000);
+}
+
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int offset) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 0));
+}
+
+constexpr int kBK = 64;            // K elements per tile (128 bytes of bf16)
+constexpr int kChunks = kBK / 8;   // 16-byte chunks per tile row
+
+// Byte offset of (row, 16-byte chunk) inside a swizzled LDS tile.
+__device__ __forceinline__ int lds_offset(int row, int chunk) {
+  return row * (kBK * 2) + ((chunk ^ (row & 7)) << 4);
+}
+
+template <typename T, int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(256) void linear_mfma_kernel(
+    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
+    T* __restrict__ y, int M, int N, int K, int64_t x_rs, int64_t y_rs) {
+  using MF = Mfma<T>;
+  static_assert(WM * WN == 4, "four waves per workgroup");
+  constexpr int TM = BM / WM;  // rows per wave
+  constexpr int TN = BN / WN;  // cols per wave
+  constexpr int FM = TM / 16;
+  constexpr int FN = TN / 16;
+  constexpr int XCH = BM * kChunks;  // 16-byte chunks per X tile
+  constexpr int WCH = BN * kChunks;
+  constexpr int XPT = (XCH + 255) / 256;  // chunks per thread
+  constexpr int WPT = (WCH + 255) / 256;
+  constexpr int XB = BM * kBK * 2;  // bytes per X tile
+  constexpr int WB = BN * kBK * 2;
+
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * (XB + WB)];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+  const int n0 = blockIdx.x * BN;
+  const int m0 = blockIdx.y * BM;
+
+  // Buffer resources over the workgroup's rows: rows past M / N read zero.
+  const int64_t x_rows = M - m0 < BM ? M - m0 : BM;
+  const int64_t w_rows = N - n0 < BN ? N - n0 : BN;
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(x + m0 * x_rs, x_rows > 0 ? (x_rows - 1) * x_rs * 2 + K * 2 : 0);
+  const __amdgpu_buffer_rsrc_t rw =
+      make_rsrc(w + static_cast<int64_t>(n0) * K, w_rows > 0 ? w_rows * K * 2 : 0);
+
+  uint4 xr[XPT], wr[WPT];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int ch = tid + 256 * i;
+      const int row = ch / kChunks, col = (ch % kChunks) * 8;
+      const bool ok = ch < XCH && row < x_rows && k0 + col < K;
+      xr[i] = ok ? buffer_load16(rx, static_cast<int>(row * x_rs + k0 + col) * 2)
+                 : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < WPT; ++i) {
+      const int ch = tid + 256 * i;
+      const int row = ch / kChunks, col = (ch % kChunks) * 8;
+      const bool ok = ch < WCH && row < w_rows && k0 + col < K;
+      wr[i] = ok ? buffer_load16(rw, (row * K + k0 + col) * 2) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto stash = [&](int buf) {
+    unsigned char* xs = smem + buf * (XB + WB);
+    unsigned char* ws = xs + XB;
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int ch = tid + 256 * i;
+      if (ch < XCH)
+        *reinterpret_cast<uint4*>(xs + lds_offset(ch / kChunks, ch % kChunks)) = xr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < WPT; ++i) {
+      const int ch = tid + 256 * i;
+      if (ch < WCH)
+        *reinterpret_cast<uint4*>(ws + lds_offset(ch / kChunks, ch % kChunks)) = wr[i];
+    }
+  };
+
+  f32x4_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int ktiles = (K + kBK - 1) / kBK;
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < ktiles) fetch((kt + 1) * kBK);
+    const unsigned char* xs = smem + buf * (XB + WB);
+    const unsigned char* ws = xs + XB;
+#pragma unroll
+    for (int kk = 0; kk < kBK / 32; ++kk) {
+      typename MF::vec a[FM], b[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int row = wm * TM + i * 16 + c;
+        a[i] = *reinterpret_cast<const typename MF::vec*>(xs + lds_offset(row, kk * 4 + g));
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int row = wn * TN + j * 16 + c;
+        b[j] = *reinterpret_cast<const typename MF::vec*>(ws + lds_offset(row, kk * 4 + g));
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = MF::run(a[i], b[j], acc[i][j]);
+    }
+    if (kt + 1 < ktiles) stash(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: lane (col c, rows 4g..4g+3) of each 16 x 16 fragment.
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int n = n0 + wn * TN + j * 16 + c;
+    if (n >= N) continue;
+    const float bv = bias != nullptr ? slc::to_f32(bias[n]) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm * TM + i * 16 + 4 * g + r;
+        if (m < M) y[m * y_rs + n] = slc::from_f32<T>(acc[i][j][r] + bv);
+      }
+  }
+}
+
+// Classic 16 x 16 LDS-tiled FMA GEMM for fp32 and unaligned shapes.
+template <typename T>
+__global__ __launch_bounds__(256) void linear_generic_kernel(
+    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
+    T* __restrict__ y, int M, int N, int K, int64_t x_rs, int64_t y_rs) {
+  __shared__ float xs[16][17];
+  __shared__ float ws[16][17];
+  const int tx = threadIdx.x & 15;  // n within the tile
+  const int ty = threadIdx.x >> 4;  // m within the tile
+  const int m = blockIdx.y * 16 + ty;
+  const int n = blockIdx.x * 16 + tx;
+  float acc = 0.0f;
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    const int xm = blockIdx.y * 16 + ty, xk = k0 + tx;
+    xs[ty][tx] = (xm < M && xk < K) ? slc::to_f32(x[xm * x_rs + xk]) : 0.0f;
+    const int wn_ = blockIdx.x * 16 + ty;
+    ws[ty][tx] = (wn_ < N && xk < K) ? slc::to_f32(w[static_cast<int64_t>(wn_) * K + xk]) : 0.0f;
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) acc += xs[ty][kk] * ws[tx][kk];
+    __syncthreads();
+  }
+  if (m < M && n < N) {
+    if (bias != nullptr) acc += slc::to_f32(bias[n]);
+    y[m * y_rs + n] = slc::from_f32<T>(acc);
+  }
+}
+
+template <typename T, int BM, int BN, int WM, int WN>
+int launch_mfma(const void* x, const void* w, const void* bias, void* y, int M,
+                int N, int K, int64_t x_rs, int64_t y_rs, hipStream_t stream) {
+  const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
+  hipLaunchKernelGGL((linear_mfma_kernel<T, BM, BN, WM, WN>), grid, dim3(256), 0,
+                     stream, static_cast<const T*>(x), static_cast<const T*>(w),
+                     static_cast<const T*>(bias), static_cast<T*>(y), M, N, K,
+                     x_rs, y_rs);
+  return slc_host::check_launch("slc_hip_linear");
+}
+
+template <typename T>
+int dispatch_mfma(const void* x, const void* w, const void* bias, void* y, int M,
+                  int N, int K, int64_t x_rs, int64_t y_rs, hipStream_t s) {
+  if (M <= 16) return launch_mfma<T, 16, 64, 1, 4>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
+  if (M <= 32) return launch_mfma<T, 32, 64, 2, 2>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
+  if (M <= 64) return launch_mfma<T, 64, 64, 2, 2>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
+  return launch_mfma<T, 128, 128, 2, 2>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
+}
+
+template <typename T>
+int launch_generic(const void* x, const void* w, const void* bias, void* y, int M,
+                   int N, int K, int64_t x_rs, int64_t y_rs, hipStream_t stream) {
+  const dim3 grid((N + 15) / 16, (M + 15) / 16);
+  hipLaunchKernelGGL((linear_generic_kernel<T>), grid, dim3(256), 0, stream,
+                     static_cast<const T*>(x), static_cast<const T*>(w),
+                     static_cast<const T*>(bias), static_cast<T*>(y), M, N, K,
+                     x_rs, y_rs);
+  return slc_host::check_launch("slc_hip_linear(generic)");
+}
+
+}  // namespace
+
+extern "C" int slc_hip_linear(const void* input, const void* weight,
+                              const void* bias, void* output, int dtype,
+                              int64_t rows, int64_t out_features,
+                              int64_t in_features, int64_t in_stride_row,
+                              int64_t out_stride_row, void* stream) {
+  SLC_REQUIRE(slc_host::is_float_dtype(dtype), "slc_hip_linear: bad dtype %d", dtype);
+  SLC_REQUIRE(rows >= 0 && out_features > 0 && in_features > 0,
+              "slc_hip_linear: bad sizes M=%lld N=%lld K=%lld", (long long)rows,
+              (long long)out_features, (long long)in_features);
+  SLC_REQUIRE(rows < (1LL << 31) && out_features < (1LL << 31) &&
+                  in_features < (1LL << 31),
+              "slc_hip_linear: sizes exceed 2^31");
+  if (rows == 0) return SLC_OK;
+  SLC_REQUIRE(input && weight && output, "slc_hip_linear: null pointer");
+  const int M = static_cast<int>(rows), N = static_cast<int>(out_features),
+            K = static_cast<int>(in_features);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint64_t bits = reinterpret_cast<uintptr_t>(input) |
+                        reinterpret_cast<uintptr_t>(weight);
+  // The vector path addresses each workgroup's X and W slices with 32-bit
+  // offsets and loads 16-byte chunks.
+  const bool vec_ok = (bits & 15) == 0 && K % 8 == 0 && in_stride_row % 8 == 0 &&
+                      static_cast<int64_t>(N) * K * 2 < (1LL << 31) &&
+                      128 * in_stride_row * 2 < (1LL << 31);
+  if (vec_ok && dtype == SLC_BF16)
+    return dispatch_mfma<slc::bf16_t>(input, weight, bias, output, M, N, K,
+                                      in_stride_row, out_stride_row, s);
+  if (vec_ok && dtype == SLC_F16)
+    return dispatch_mfma<slc::f16_t>(input, weight, bias, output, M, N, K,
+                                     in_stride_row, out_stride_row, s);
+  switch (dtype) {
+    case SLC_F32:
+      return launch_generic<float>(input, weight, bias, output, M, N, K,
+                                   in_stride_row, out_stride_row, s);
+    case SLC_BF16:
+      return launch_generic<slc::bf16_t>(input, weight, bias, output, M, N, K,
+                                         in_stride_row, out_stride_row, s);
+    default:
+      return launch_generic<slc::f16_t>(input, weight, bias, output, M, N, K,
+                                        in_stride_row, out_stride_row, s);
+  }
+}

@@ -1,0 +1,442 @@
+// prefill_attention: multi-token GQA attention (serve.prefill_attention).
+//
+// Semantics: src/stateful_llm_compiler/execution.py:707-739 (reference
+// executor) and backends/triton_prefill_attention.py:10-150 (fused kernel):
+//   out[b,h,q,:] = sum_k softmax_k(scale * q.k + mask[b,q,k]) v[b,k,h/g,:]
+// with keys k > q removed when the op is causal (causal=True); an additive
+// mask (B x 1 x T x T) is applied when given.  fp32 softmax and accumulation.
+//
+// MI355X design (bf16 / fp16, head_dim 64):
+//  * A workgroup is 4 waves x 16 queries of one (batch, query head); K/V tiles
+//    of 64 keys are loaded once per workgroup with coalesced 16-byte loads and
+//    shared through LDS (double buffered, prefetched into registers).
+//  * Each wave computes S^T[key, query] = K . Q^T with v_mfma_f32_16x16x32, so
+//    a lane owns one query column: the softmax max needs only two cross-lane
+//    shuffles per tile and the exponentials stay in registers.
+//  * O^T[dim, query] += V^T . P^T: V is written to LDS transposed, with keys
+//    placed in the order of the lanes' P registers, so both MFMA operands are
+//    single ds_read_b128 / register reads.
+//  * Causal: tiles entirely in a wave's future are skipped (and workgroups
+//    are launched heaviest-first); the diagonal tile is masked per element.
+// fp32 and other shapes take a simple wave-per-query kernel.
+#include "common.hpp"
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kRescaleThreshold = 8.0f;
+
+template <typename T>
+struct Mfma;
+template <>
+struct Mfma<slc::bf16_t> {
+  using vec = bf16x8_t;
+  static __device__ __forceinline__ f32x4_t run(vec a, vec b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma<slc::f16_t> {
+  using vec = f16x8_t;
+  static __device__ __forceinline__ f32x4_t run(vec a, vec b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+struct u16x8 {
+  uint16_t v[8];
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const uint64_t address = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(address));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(address >> 32));
+  void* uniform = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+  const int clamped = bytes > 0x7fffffff ? 0x7fffffff : static_cast<int>(bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(uniform, 0, __builtin_amdgcn_readfirstlane(clamped),
+                                           0x00020000);
+}
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int offset) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 0));
+}
+
+constexpr int kD = 64;       // head dim of the MFMA kernel
+constexpr int kKeys = 64;    // keys per tile
+constexpr int kQueries = 64; // queries per workgroup (4 waves x 16)
+constexpr int kRowBytes = kD * 2;
+constexpr int kTileBytes = kKeys * kRowBytes;  // 8 KB
+
+// K tile: row = key, 16-byte chunks XOR-swizzled by row.
+__device__ __forceinline__ int k_offset(int key, int chunk) {
+  return key * kRowBytes + ((chunk ^ (key & 7)) << 4);
+}
+// Position of a key inside its 32-key half in the V^T tile: the order of the
+// P operand's k-slots (lane group g holds keys 4g..4g+3 of both 16-key blocks).
+__device__ __forceinline__ int key_position(int key) {
+  const int half = key >> 5, k = key & 31;
+  return half * 32 + ((k & 15) >> 2) * 8 + (k >> 4) * 4 + (k & 3);
+}
+// V^T tile: row = dim, 64 key positions, 16-byte chunks XOR-swizzled by row.
+__device__ __forceinline__ int vt_offset(int dim, int position) {
+  return dim * kRowBytes + (((position >> 3) ^ (dim & 7)) << 4) + (position & 7) * 2;
+}
+
+template <typename T>
+__device__ __forceinline__ uint16_t bits_of(float f) {
+  return slc::from_f32<T>(f).bits;
+}
+
+// MK: mask element type (0 = none, else slc_dtype + 1).
+template <typename T, int MK, bool CAUSAL>
+__global__ __launch_bounds__(256) void prefill_attention_mfma_kernel(
+    const T* __restrict__ query, const T* __restrict__ key, const T* __restrict__ value,
+    const void* __restrict__ mask, T* __restrict__ output, int tokens, int q_heads,
+    int groups, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh,
+    int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t m_sb,
+    int64_t m_sq, int64_t m_sk, int64_t o_sb, int64_t o_sh, int64_t o_st,
+    float scale_log2) {
+  using M = Mfma<T>;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2][2][kTileBytes];
+
+  const int nqb = gridDim.x;
+  const int qb = CAUSAL ? nqb - 1 - static_cast<int>(blockIdx.x) : blockIdx.x;
+  const int h = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int kvh = h / groups;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int g = lane >> 4;
+  const int c = lane & 15;
+  const int q0 = qb * kQueries;
+  const int qw = q0 + wave * 16;  // first query of this wave
+  const int my_query = qw + c;
+
+  // Q^T as the B operand: lane (query c, k-slice g) holds dims kk*32+8g..+7.
+  typename M::vec qv[2];
+  {
+    const int qrow = my_query < tokens ? my_query : tokens - 1;
+    const T* qp = query + b * q_sb + h * q_sh + static_cast<int64_t>(qrow) * q_st;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+      qv[kk] = __builtin_bit_cast(typename M::vec,
+                                  *reinterpret_cast<const uint4*>(qp + kk * 32 + 8 * g));
+  }
+
+  const int64_t k_rows_bytes = (static_cast<int64_t>(tokens) - 1) * k_st * 2 + kRowBytes;
+  const int64_t v_rows_bytes = (static_cast<int64_t>(tokens) - 1) * v_st * 2 + kRowBytes;
+  const T* kbase = key + b * k_sb + kvh * k_sh;
+  const T* vbase = value + b * v_sb + kvh * v_sh;
+
+  // Keys this workgroup needs: all of them, or up to its last query if causal.
+  const int q_last = min(q0 + kQueries, tokens) - 1;
+  const int key_end = CAUSAL ? q_last + 1 : tokens;
+  const int ntiles = (key_end + kKeys - 1) / kKeys;
+
+  // Cooperative tile fetch: 512 16-byte chunks of K and of V, 2 + 2 per thread.
+  uint4 kr[2], vr[2];
+  auto fetch = [&](int k0) {
+    const __amdgpu_buffer_rsrc_t rk =
+        make_rsrc(kbase + static_cast<int64_t>(k0) * k_st,
+                  k_rows_bytes - static_cast<int64_t>(k0) * k_st * 2);
+    const __amdgpu_buffer_rsrc_t rv =
+        make_rsrc(vbase + static_cast<int64_t>(k0) * v_st,
+                  v_rows_bytes - static_cast<int64_t>(k0) * v_st * 2);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int ch = tid + 256 * i;
+      const int row = ch >> 3, col = (ch & 7) * 8;
+      kr[i] = buffer_load16(rk, static_cast<int>((row * k_st + col) * 2));
+      vr[i] = buffer_load16(rv, static_cast<int>((row * v_st + col) * 2));
+    }
+  };
+  auto stash = [&](int buf) {
+    unsigned char* ks = smem[buf][0];
+    unsigned char* vs = smem[buf][1];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int ch = tid + 256 * i;
+      const int row = ch >> 3, chunk = ch & 7;
+      *reinterpret_cast<uint4*>(ks + k_offset(row, chunk)) = kr[i];
+      const uint16_t* e = reinterpret_cast<const uint16_t*>(&vr[i]);
+      const int pos = key_position(row);
+#pragma unroll
+      for (int d = 0; d < 8; ++d)
+        *reinterpret_cast<uint16_t*>(vs + vt_offset(chunk * 8 + d, pos)) = e[d];
+    }
+  };
+
+  float m_run = -INFINITY, l_run = 0.0f;
+  f32x4_t acc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  constexpr int kMaskBytes = MK == SLC_F32 + 1 ? 4 : 2;
+  const char* mrow = nullptr;
+  if constexpr (MK != 0) {
+    const int qrow = my_query < tokens ? my_query : tokens - 1;
+    mrow = static_cast<const char*>(mask) + (b * m_sb + static_cast<int64_t>(qrow) * m_sq) * kMaskBytes;
+  }
+
+  if (ntiles > 0) {
+    fetch(0);
+    stash(0);
+  }
+  __syncthreads();
+  for (int kt = 0; kt < ntiles; ++kt) {
+    const int buf = kt & 1;
+    const int k0 = kt * kKeys;
+    if (kt + 1 < ntiles) fetch(k0 + kKeys);
+    // A tile wholly in this wave's future contributes nothing.
+    const bool active = !CAUSAL || k0 <= qw + 15;
+    if (active && qw < tokens) {
+      const unsigned char* ks = smem[buf][0];
+      const unsigned char* vs = smem[buf][1];
+      float s[16];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        f32x4_t st = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const auto a = *reinterpret_cast<const typename M::vec*>(
+              ks + k_offset(kb * 16 + c, kk * 4 + g));
+          st = M::run(a, qv[kk], st);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int kidx = k0 + kb * 16 + 4 * g + r;
+          float v = st[r] * scale_log2;
+          if constexpr (MK != 0) {
+            if (kidx < tokens) {
+              const char* p = mrow + static_cast<int64_t>(kidx) * m_sk * kMaskBytes;
+              float mv;
+              if constexpr (MK == SLC_F32 + 1) {
+                mv = *reinterpret_cast<const float*>(p);
+              } else if constexpr (MK == SLC_BF16 + 1) {
+                mv = slc::to_f32(*reinterpret_cast<const slc::bf16_t*>(p));
+              } else {
+                mv = slc::to_f32(*reinterpret_cast<const slc::f16_t*>(p));
+              }
+              v += mv * kLog2e;
+            }
+          }
+          bool valid = kidx < tokens;
+          if constexpr (CAUSAL) valid = valid && kidx <= my_query;
+          s[kb * 4 + r] = valid ? v : -INFINITY;
+        }
+      }
+      float mx = s[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      if (__any(mx > m_run + kRescaleThreshold)) {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.0f : m_new));
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) acc[db] = acc[db] * alpha;
+        m_run = m_new;
+      }
+      const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+      typename M::vec pv[2];
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        u16x8 bits;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float p = __builtin_amdgcn_exp2f(s[(2 * half + (i >> 2)) * 4 + (i & 3)] - m_use);
+          l_run += p;
+          bits.v[i] = bits_of<T>(p);
+        }
+        pv[half] = __builtin_bit_cast(typename M::vec, bits);
+      }
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const auto a = *reinterpret_cast<const typename M::vec*>(
+              vs + vt_offset(db * 16 + c, half * 32 + g * 8));
+          acc[db] = M::run(a, pv[half], acc[db]);
+        }
+    }
+    if (kt + 1 < ntiles) stash(buf ^ 1);
+    __syncthreads();
+  }
+
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run += __shfl_xor(l_run, 32, 64);
+  if (my_query < tokens) {
+    const float inv = 1.0f / l_run;
+    T* op = output + b * o_sb + h * o_sh + static_cast<int64_t>(my_query) * o_st;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) op[db * 16 + 4 * g + r] = slc::from_f32<T>(acc[db][r] * inv);
+  }
+}
+
+// Generic path: one wave per query row, shuffled dot products, online softmax.
+template <typename T, int NI>
+__global__ __launch_bounds__(256) void prefill_attention_generic_kernel(
+    const T* __restrict__ query, const T* __restrict__ key, const T* __restrict__ value,
+    const void* __restrict__ mask, int mask_dtype, T* __restrict__ output, int tokens,
+    int q_heads, int groups, int head_dim, int causal, int64_t q_sb, int64_t q_sh,
+    int64_t q_st, int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t v_sb,
+    int64_t v_sh, int64_t v_st, int64_t m_sb, int64_t m_sq, int64_t m_sk,
+    int64_t o_sb, int64_t o_sh, int64_t o_st, float scale_log2) {
+  const int lane = threadIdx.x & 63;
+  const int qi = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int h = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  if (qi >= tokens) return;
+  const int kvh = h / groups;
+  float q[NI], acc[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int d = lane + 64 * i;
+    q[i] = d < head_dim ? slc::to_f32(query[b * q_sb + h * q_sh + qi * q_st + d]) : 0.0f;
+    acc[i] = 0.0f;
+  }
+  const int key_end = causal ? qi + 1 : tokens;
+  float m_run = -INFINITY, l_run = 0.0f;
+  for (int kidx = 0; kidx < key_end; ++kidx) {
+    float dot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int d = lane + 64 * i;
+      if (d < head_dim) dot += q[i] * slc::to_f32(key[b * k_sb + kvh * k_sh + kidx * k_st + d]);
+    }
+    dot = slc::wave_sum(dot);
+    float s = dot * scale_log2;
+    if (mask != nullptr) s += slc::load_as_f32(mask, b * m_sb + qi * m_sq + kidx * m_sk, mask_dtype) * kLog2e;
+    const float m_new = fmaxf(m_run, s);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = exp2f(m_run - m_use);
+    const float p = exp2f(s - m_use);
+    l_run = l_run * alpha + p;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int d = lane + 64 * i;
+      const float v = d < head_dim ? slc::to_f32(value[b * v_sb + kvh * v_sh + kidx * v_st + d]) : 0.0f;
+      acc[i] = acc[i] * alpha + p * v;
+    }
+    m_run = m_new;
+  }
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int d = lane + 64 * i;
+    if (d < head_dim) output[b * o_sb + h * o_sh + qi * o_st + d] = slc::from_f32<T>(acc[i] / l_run);
+  }
+}
+
+template <typename T, int MK, bool CAUSAL>
+int launch_mfma(const void* q, const void* k, const void* v, const void* mask, void* out,
+                int64_t batch, int tokens, int q_heads, int groups, const int64_t* st,
+                float scale_log2, hipStream_t stream) {
+  const dim3 grid((tokens + kQueries - 1) / kQueries, q_heads, static_cast<unsigned>(batch));
+  hipLaunchKernelGGL((prefill_attention_mfma_kernel<T, MK, CAUSAL>), grid, dim3(256), 0, stream,
+                     static_cast<const T*>(q), static_cast<const T*>(k),
+                     static_cast<const T*>(v), mask, static_cast<T*>(out), tokens, q_heads,
+                     groups, st[0], st[1], st[2], st[3], st[4], st[5], st[6], st[7], st[8],
+                     st[9], st[10], st[11], st[12], st[13], st[14], scale_log2);
+  return slc_host::check_launch("slc_hip_prefill_attention");
+}
+
+template <typename T, bool CAUSAL>
+int dispatch_mask(const void* q, const void* k, const void* v, const void* mask,
+                  int mask_dtype, void* out, int64_t batch, int tokens, int q_heads,
+                  int groups, const int64_t* st, float scale_log2, hipStream_t s) {
+  if (mask == nullptr)
+    return launch_mfma<T, 0, CAUSAL>(q, k, v, mask, out, batch, tokens, q_heads, groups, st, scale_log2, s);
+  if (mask_dtype == SLC_BF16)
+    return launch_mfma<T, SLC_BF16 + 1, CAUSAL>(q, k, v, mask, out, batch, tokens, q_heads, groups, st, scale_log2, s);
+  if (mask_dtype == SLC_F16)
+    return launch_mfma<T, SLC_F16 + 1, CAUSAL>(q, k, v, mask, out, batch, tokens, q_heads, groups, st, scale_log2, s);
+  return launch_mfma<T, SLC_F32 + 1, CAUSAL>(q, k, v, mask, out, batch, tokens, q_heads, groups, st, scale_log2, s);
+}
+
+template <typename T>
+int launch_generic(const void* q, const void* k, const void* v, const void* mask,
+                   int mask_dtype, void* out, int64_t batch, int tokens, int q_heads,
+                   int groups, int head_dim, int causal, const int64_t* st,
+                   float scale_log2, hipStream_t stream) {
+  const dim3 grid((tokens + 3) / 4, q_heads, static_cast<unsigned>(batch));
+#define SLC_GEN(NI)                                                                      \
+  hipLaunchKernelGGL((prefill_attention_generic_kernel<T, NI>), grid, dim3(256), 0, stream, \
+                     static_cast<const T*>(q), static_cast<const T*>(k),                 \
+                     static_cast<const T*>(v), mask, mask_dtype, static_cast<T*>(out),   \
+                     tokens, q_heads, groups, head_dim, causal, st[0], st[1], st[2],     \
+                     st[3], st[4], st[5], st[6], st[7], st[8], st[9], st[10], st[11],    \
+                     st[12], st[13], st[14], scale_log2)
+  if (head_dim <= 64) {
+    SLC_GEN(1);
+  } else if (head_dim <= 128) {
+    SLC_GEN(2);
+  } else {
+    SLC_GEN(4);
+  }
+#undef SLC_GEN
+  return slc_host::check_launch("slc_hip_prefill_attention(generic)");
+}
+
+}  // namespace
+
+extern "C" int slc_hip_prefill_attention(
+    const void* query, const void* key, const void* value, const void* mask,
+    int mask_dtype, void* output, int dtype, int64_t batch, int64_t q_heads,
+    int64_t kv_heads, int64_t tokens, int64_t head_dim, int causal, int64_t q_sb,
+    int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t m_sb, int64_t m_sq,
+    int64_t m_sk, int64_t o_sb, int64_t o_sh, int64_t o_st, float scale,
+    void* stream) {
+  SLC_REQUIRE(slc_host::is_float_dtype(dtype), "slc_hip_prefill_attention: bad dtype %d", dtype);
+  SLC_REQUIRE(mask == nullptr || slc_host::is_float_dtype(mask_dtype),
+              "slc_hip_prefill_attention: bad mask dtype %d", mask_dtype);
+  SLC_REQUIRE(batch >= 0 && q_heads > 0 && kv_heads > 0 && tokens >= 0 && head_dim > 0 &&
+                  head_dim <= 256 && q_heads % kv_heads == 0,
+              "slc_hip_prefill_attention: bad sizes");
+  SLC_REQUIRE(batch <= 65535 && q_heads <= 65535 && tokens < (1LL << 30),
+              "slc_hip_prefill_attention: sizes exceed grid limits");
+  if (batch == 0 || tokens == 0) return SLC_OK;
+  SLC_REQUIRE(query && key && value && output, "slc_hip_prefill_attention: null pointer");
+  const int64_t st[15] = {q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh,
+                          v_st, m_sb, m_sq, m_sk, o_sb, o_sh, o_st};
+  const int groups = static_cast<int>(q_heads / kv_heads);
+  const float scale_log2 = scale * kLog2e;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int T_ = static_cast<int>(tokens);
+  const uint64_t bits = reinterpret_cast<uintptr_t>(query) | reinterpret_cast<uintptr_t>(key) |
+                        reinterpret_cast<uintptr_t>(value);
+  const int64_t strides = q_sb | q_sh | q_st | k_sb | k_sh | k_st | v_sb | v_sh | v_st;
+  // The MFMA kernel addresses one (batch, kv-head) K/V slice with 32-bit offsets.
+  const bool mfma_ok = (dtype == SLC_BF16 || dtype == SLC_F16) && head_dim == kD &&
+                       (bits & 15) == 0 && (strides & 7) == 0 && k_st >= kD && v_st >= kD &&
+                       tokens * (k_st > v_st ? k_st : v_st) * 2 < (1LL << 31);
+  if (mfma_ok) {
+    if (dtype == SLC_BF16) {
+      return causal ? dispatch_mask<slc::bf16_t, true>(query, key, value, mask, mask_dtype, output, batch, T_, static_cast<int>(q_heads), groups, st, scale_log2, s)
+                    : dispatch_mask<slc::bf16_t, false>(query, key, value, mask, mask_dtype, output, batch, T_, static_cast<int>(q_heads), groups, st, scale_log2, s);
+    }
+    return causal ? dispatch_mask<slc::f16_t, true>(query, key, value, mask, mask_dtype, output, batch, T_, static_cast<int>(q_heads), groups, st, scale_log2, s)
+                  : dispatch_mask<slc::f16_t, false>(query, key, value, mask, mask_dtype, output, batch, T_, static_cast<int>(q_heads), groups, st, scale_log2, s);
+  }
+  switch (dtype) {
+    case SLC_F32:
+      return launch_generic<float>(query, key, value, mask, mask_dtype, output, batch, T_,
+                                   static_cast<int>(q_heads), groups, static_cast<int>(head_dim),
+                                   causal, st, scale_log2, s);
+    case SLC_BF16:
+      return launch_generic<slc::bf16_t>(query, key, value, mask, mask_dtype, output, batch, T_,
+                                         static_cast<int>(q_heads), groups,
+                                         static_cast<int>(head_dim), causal, st, scale_log2, s);
+    default:
+      return launch_generic<slc::f16_t>(query, key, value, mask, mask_dtype, output, batch, T_,
+                                        static_cast<int>(q_heads), groups,
+                                        static_cast<int>(head_dim), causal, st, scale_log2, s);
+  }
+}

@@ -1,0 +1,185 @@
+"""GPU parity of the dense kernels (linear, prefill attention) against the oracle.
+
+Bars: fp32 within 1e-5 relative.  bf16 linear: every output within one bf16
+ulp of the exact (fp64) product of the same bf16 inputs, and within one ulp of
+the oracle's own bf16 result (both round an fp32 accumulation once, so they
+may differ by that rounding).  bf16 attention: 2e-2 absolute.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from helpers import announce, assert_bf16_close, assert_fp32_close, generator
+from oracle import kernels as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16_ulp(x: torch.Tensor) -> torch.Tensor:
+    # Spacing of bf16 numbers at |x| (8 significant bits).
+    mag = x.abs().clamp_min(2.0**-126)
+    return torch.exp2(torch.floor(torch.log2(mag)) - 7)
+
+
+def _check_linear_bf16(actual, x, w, b):
+    exact = x.double() @ w.double().T
+    if b is not None:
+        exact = exact + b.double()
+    oracle = ref.linear(x, w, b).double()
+    a = actual.double().cpu()
+    tol = _bf16_ulp(exact) * 1.0 + 1e-6
+    assert ((a - exact).abs() <= tol).all(), float((a - exact).abs().max())
+    tol_o = _bf16_ulp(oracle) * 1.0 + 1e-6
+    assert ((a - oracle).abs() <= tol_o + _bf16_ulp(exact)).all()
+
+
+@pytest.mark.parametrize("rows", [1, 8, 33, 64, 128, 1000])
+@pytest.mark.parametrize(
+    "k,n,bias",
+    [(896, 896, True), (896, 128, True), (896, 4864, False), (4864, 896, False)],
+)
+def test_linear_bf16_qwen_shapes(gpu, rows, k, n, bias):
+    from stateful_llm_compiler_hip.backends import hip_linear
+
+    announce(f"linear bf16 M={rows} K={k} N={n} bias={bias}")
+    g = generator(rows * 13 + k + n)
+    x = torch.randn(rows, k, generator=g).bfloat16()
+    w = (torch.randn(n, k, generator=g) * 0.02).bfloat16()
+    b = (torch.randn(n, generator=g) * 0.02).bfloat16() if bias else None
+    y = hip_linear(x.to(gpu), w.to(gpu), None if b is None else b.to(gpu))
+    torch.cuda.synchronize()
+    _check_linear_bf16(y, x, w, b)
+
+
+def test_linear_bf16_large_m_and_3d(gpu):
+    from stateful_llm_compiler_hip.backends import hip_linear
+
+    announce("linear bf16 3-D input [4, 1024, 896] -> 896")
+    g = generator(3)
+    x = torch.randn(4, 1024, 896, generator=g).bfloat16()
+    w = (torch.randn(896, 896, generator=g) * 0.02).bfloat16()
+    b = (torch.randn(896, generator=g) * 0.02).bfloat16()
+    y = hip_linear(x.to(gpu), w.to(gpu), b.to(gpu))
+    torch.cuda.synchronize()
+    assert y.shape == (4, 1024, 896)
+    _check_linear_bf16(y.reshape(-1, 896), x.reshape(-1, 896), w, b)
+
+
+@pytest.mark.parametrize("k", [72, 40, 100])
+def test_linear_bf16_k_tails(gpu, k):
+    from stateful_llm_compiler_hip.backends import hip_linear
+
+    announce(f"linear bf16 K tail K={k}")
+    g = generator(k)
+    x = torch.randn(70, k, generator=g).bfloat16()
+    w = (torch.randn(130, k, generator=g) * 0.1).bfloat16()
+    y = hip_linear(x.to(gpu), w.to(gpu))
+    torch.cuda.synchronize()
+    _check_linear_bf16(y, x, w, None)
+
+
+def test_linear_fp16(gpu):
+    from stateful_llm_compiler_hip.backends import hip_linear
+
+    announce("linear fp16")
+    g = generator(7)
+    x = torch.randn(40, 512, generator=g).half()
+    w = (torch.randn(1536, 512, generator=g) * 0.05).half()
+    b = (torch.randn(1536, generator=g) * 0.05).half()
+    y = hip_linear(x.to(gpu), w.to(gpu), b.to(gpu)).cpu().double()
+    exact = x.double() @ w.double().T + b.double()
+    # fp16 ulp: 11 significant bits
+    ulp = torch.exp2(torch.floor(torch.log2(exact.abs().clamp_min(2.0**-14))) - 10)
+    assert ((y - exact).abs() <= ulp + 1e-6).all()
+
+
+@pytest.mark.parametrize("rows", [1, 3, 17])
+def test_linear_fp32(gpu, rows):
+    from stateful_llm_compiler_hip.backends import hip_linear
+
+    announce(f"linear fp32 M={rows}")
+    g = generator(rows)
+    x = torch.randn(rows, 896, generator=g)
+    w = torch.randn(4864, 896, generator=g) * 0.02
+    b = torch.randn(4864, generator=g) * 0.02
+    y = hip_linear(x.to(gpu), w.to(gpu), b.to(gpu))
+    torch.cuda.synchronize()
+    assert_fp32_close(y, ref.linear(x, w, b))
+
+
+# -------------------------------------------------------- prefill attention
+
+
+def _prefill_case(gpu, batch, tokens, dtype, seed, *, mask_kind, causal, q_heads=14, kv_heads=2, head_dim=64):
+    from stateful_llm_compiler_hip.backends import hip_prefill_attention
+
+    g = generator(seed)
+    # Projection-layout views ([B, T, H, D] transposed), as the model produces them.
+    q = torch.randn(batch, tokens, q_heads, head_dim, generator=g).to(dtype).transpose(1, 2)
+    k = torch.randn(batch, tokens, kv_heads, head_dim, generator=g).to(dtype).transpose(1, 2)
+    v = torch.randn(batch, tokens, kv_heads, head_dim, generator=g).to(dtype).transpose(1, 2)
+    if mask_kind == "none":
+        mask = None
+    elif mask_kind == "causal":
+        future = torch.triu(torch.ones(tokens, tokens, dtype=torch.bool), diagonal=1)
+        mask = torch.zeros(batch, 1, tokens, tokens).masked_fill(future, float("-inf"))
+    elif mask_kind == "zeros":
+        mask = torch.zeros(batch, 1, tokens, tokens)
+    else:
+        mask = torch.randn(batch, 1, tokens, tokens, generator=g)
+    expected = ref.prefill_attention(
+        q, k, v, mask, groups=q_heads // kv_heads, scale=head_dim**-0.5, causal=causal
+    )
+
+    def dev(t):
+        return t.transpose(1, 2).contiguous().to(gpu).transpose(1, 2)
+
+    actual = hip_prefill_attention(
+        dev(q), dev(k), dev(v), None if mask is None else mask.to(gpu),
+        scale=head_dim**-0.5, causal=causal,
+    )
+    torch.cuda.synchronize()
+    return actual.cpu(), expected
+
+
+@pytest.mark.parametrize("batch,tokens", [(1, 7), (2, 64), (1, 100), (2, 128), (1, 1024)])
+def test_prefill_causal_flag_bf16(gpu, batch, tokens):
+    announce(f"prefill bf16 causal=True no mask B={batch} T={tokens}")
+    actual, expected = _prefill_case(gpu, batch, tokens, torch.bfloat16, tokens, mask_kind="none", causal=True)
+    assert_bf16_close(actual, expected)
+
+
+@pytest.mark.parametrize("tokens", [7, 130])
+def test_prefill_mask_provides_causality_bf16(gpu, tokens):
+    # causal="mask": the reference passes the causal -inf mask (qwen2.py:540-573).
+    announce(f"prefill bf16 causal mask T={tokens}")
+    actual, expected = _prefill_case(gpu, 2, tokens, torch.bfloat16, 5, mask_kind="causal", causal=False)
+    assert_bf16_close(actual, expected)
+
+
+def test_prefill_mask_and_flag_bf16(gpu):
+    announce("prefill bf16 random mask + causal flag")
+    actual, expected = _prefill_case(gpu, 2, 96, torch.bfloat16, 6, mask_kind="random", causal=True)
+    assert_bf16_close(actual, expected)
+
+
+def test_prefill_bidirectional_zero_mask_bf16(gpu):
+    # Reference case: an all-zero mask is bidirectional attention
+    # (test_prefill_attention.py:97-114).
+    announce("prefill bf16 zero mask bidirectional")
+    actual, expected = _prefill_case(gpu, 2, 80, torch.bfloat16, 7, mask_kind="zeros", causal=False)
+    assert_bf16_close(actual, expected)
+
+
+def test_prefill_fp32_generic(gpu):
+    announce("prefill fp32 causal mask T=33 QH4 KVH2 D64")
+    actual, expected = _prefill_case(gpu, 2, 33, torch.float32, 8, mask_kind="causal", causal=False, q_heads=4)
+    assert_fp32_close(actual, expected)
+
+
+def test_prefill_fp16_head_dim_128_generic(gpu):
+    announce("prefill fp16 D=128 (generic)")
+    actual, expected = _prefill_case(gpu, 1, 40, torch.float16, 9, mask_kind="none", causal=True, q_heads=4, head_dim=128)
+    assert_bf16_close(actual, expected)
