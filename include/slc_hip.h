@@ -67,12 +67,15 @@ SLC_API const char* slc_hip_last_error(void);
  *   key/value               : [batch, heads, tokens, head_dim], strides
  *                             (sb, sh, st) in elements, head_dim contiguous
  *   positions               : [batch] int64 (first destination row per batch)
+ *   overflow                : optional device int set to 1 when a row falls
+ *                             outside [0, capacity) (never cleared here)
  * Row t of batch b lands at buffer row positions[b] + t; rows whose position is
  * outside [0, capacity) are skipped (the reference masks them the same way).
  * The copy is bit-exact for every dtype.
  */
 SLC_API int slc_hip_kv_store(void* key_buffer, void* value_buffer, const void* key,
-                     const void* value, const int64_t* positions, int dtype,
+                     const void* value, const int64_t* positions,
+                     int* overflow, int dtype,
                      int64_t batch, int64_t heads, int64_t tokens,
                      int64_t head_dim, int64_t capacity, int64_t key_stride_b,
                      int64_t key_stride_h, int64_t key_stride_t,
@@ -178,6 +181,38 @@ SLC_API int slc_hip_prefill_attention(
     int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t m_sb, int64_t m_sq,
     int64_t m_sk, int64_t o_sb, int64_t o_sh, int64_t o_st, float scale,
     void* stream);
+
+/*
+ * Ops that complete a Qwen2 step without eager PyTorch kernels.  None has a
+ * separate reference kernel: the reference runs them as PyTorch ops
+ * (execution.py:500-528 handler table; qwen2.py model code cited per op).
+ *   embedding  : output[r, :] = table[ids[r], :]; ids outside [0, vocab) set
+ *                *bad_index (optional) and read row 0      (qwen2.py:427-430)
+ *   add        : output = a + b, elementwise, contiguous    (qwen2.py:288-294)
+ *   swiglu     : output = round(silu(gate)) * up             (qwen2.py:253-256)
+ *   rope_table : cos/sin[b, t, :] of cat(f, f), f = positions[b, t] * inv_freq
+ *                (fp32 math, rounded to dtype), outputs [B, T, D] contiguous
+ *                                                           (qwen2.py:136-149)
+ *   kv_advance : lengths_out = lengths_in + delta (may alias); sets *overflow
+ *                when a length leaves [0, capacity]          (execution.py:421-443)
+ *   argmax     : output[r] = index of the first maximum of row r
+ */
+SLC_API int slc_hip_embedding(const int64_t* ids, const void* table, void* output,
+                              int dtype, int64_t rows, int64_t hidden, int64_t vocab,
+                              int* bad_index, void* stream);
+SLC_API int slc_hip_add(const void* a, const void* b, void* output, int dtype,
+                        int64_t numel, void* stream);
+SLC_API int slc_hip_swiglu(const void* gate, const void* up, void* output, int dtype,
+                           int64_t numel, void* stream);
+SLC_API int slc_hip_rope_table(const int64_t* positions, const float* inv_freq,
+                               void* cosine, void* sine, int dtype, int64_t batch,
+                               int64_t tokens, int64_t pos_stride_b, int64_t head_dim,
+                               void* stream);
+SLC_API int slc_hip_kv_advance(const int64_t* lengths_in, int64_t* lengths_out,
+                               int64_t batch, int64_t delta, int64_t capacity,
+                               int* overflow, void* stream);
+SLC_API int slc_hip_argmax(const void* logits, int64_t* output, int dtype, int64_t rows,
+                           int64_t cols, int64_t row_stride, void* stream);
 
 #ifdef __cplusplus
 }

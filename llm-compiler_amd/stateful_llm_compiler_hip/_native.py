@@ -47,8 +47,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "slc_hip_last_error": (ctypes.c_char_p, []),
     "slc_hip_kv_store": (
         _I,
-        [_P, _P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _P],
+        [_P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _P],
     ),
+    "slc_hip_embedding": (_I, [_P, _P, _P, _I, _L, _L, _L, _P, _P]),
+    "slc_hip_add": (_I, [_P, _P, _P, _I, _L, _P]),
+    "slc_hip_swiglu": (_I, [_P, _P, _P, _I, _L, _P]),
+    "slc_hip_rope_table": (_I, [_P, _P, _P, _P, _I, _L, _L, _L, _L, _P]),
+    "slc_hip_kv_advance": (_I, [_P, _P, _L, _L, _L, _P, _P]),
+    "slc_hip_argmax": (_I, [_P, _P, _I, _L, _L, _L, _P]),
     "slc_hip_decode_attention_workspace_size": (
         _L,
         [_L, _L, _L, _L, _L, _I, _L],

@@ -3,11 +3,25 @@
 from .hip_attention import hip_decode_attention
 from .hip_kv import hip_kv_store
 from .hip_linear import hip_linear
+from .hip_ops import (
+    hip_add,
+    hip_argmax,
+    hip_embedding,
+    hip_kv_advance,
+    hip_rope_table,
+    hip_swiglu,
+)
 from .hip_prefill_attention import hip_prefill_attention
 from .hip_rmsnorm import hip_rms_norm
 from .hip_rope import hip_rope
 
 __all__ = [
+    "hip_add",
+    "hip_argmax",
+    "hip_embedding",
+    "hip_kv_advance",
+    "hip_rope_table",
+    "hip_swiglu",
     "hip_decode_attention",
     "hip_kv_store",
     "hip_linear",

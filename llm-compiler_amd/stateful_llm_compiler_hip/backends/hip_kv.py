@@ -18,11 +18,14 @@ def hip_kv_store(
     key: torch.Tensor,
     value: torch.Tensor,
     positions: torch.Tensor,
+    *,
+    overflow: torch.Tensor | None = None,
 ) -> None:
     """Write B x H x T x D ``key``/``value`` rows into B x Cap x H x D buffers.
 
     Row ``t`` of batch ``b`` lands at buffer row ``positions[b] + t``; rows at
-    or beyond the capacity are skipped, as in the reference kernel.
+    or beyond the capacity are skipped, as in the reference kernel, and set
+    the optional int32 ``overflow`` flag tensor.
     """
 
     if not all(
@@ -61,6 +64,7 @@ def hip_kv_store(
         key.data_ptr(),
         value.data_ptr(),
         positions.data_ptr(),
+        None if overflow is None else overflow.data_ptr(),
         _native.dtype_tag(key.dtype),
         batch,
         heads,

@@ -1,0 +1,56 @@
+"""Compile entry point: ServeIR module -> verified, lowered KernelIR.
+
+Mirrors the reference's ``compile_exported_program`` / ``CompileOptions``
+(src/stateful_llm_compiler/compiler.py:25-79) for graphs that already are
+ServeIR: optional profile-guided RMSNorm plans, the KernelIR lowering in the
+chosen numerical mode, and ``require_full_lowering`` when strict.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Any
+
+from .cost_model import RMSNormCostModel
+from .ir import Module
+from .lowering import LoweringCoverage, LowerToKernelIRPass, analyze_lowering_coverage, require_full_lowering
+from .pass_manager import PassManager, PassResult, operation_counts
+from .passes import SelectRMSNormLoweringPass
+
+
+@dataclass(frozen=True)
+class CompileOptions:
+    numerical_mode: str = "fast"
+    require_full_lowering: bool = True
+    rmsnorm_profile: str | Path | None = None
+    rmsnorm_fallback: str = "hip"
+
+
+@dataclass
+class CompileResult:
+    module: Module
+    passes: list[PassResult]
+    coverage: LoweringCoverage
+    operation_counts: dict[str, int] = field(default_factory=dict)
+
+    def statistics(self) -> dict[str, Any]:
+        return {
+            "passes": [{"name": r.name, "changed": r.changed, **r.statistics} for r in self.passes],
+            "coverage": self.coverage.to_dict(),
+            "operation_counts": self.operation_counts,
+        }
+
+
+def compile_module(module: Module, options: CompileOptions | None = None) -> CompileResult:
+    """Lower ``module`` in place and return it with pass statistics."""
+
+    options = options or CompileOptions()
+    manager = PassManager()
+    if options.rmsnorm_profile is not None:
+        manager.add(SelectRMSNormLoweringPass(RMSNormCostModel.load(options.rmsnorm_profile),
+                                              fallback=options.rmsnorm_fallback))
+    manager.add(LowerToKernelIRPass(numerical_mode=options.numerical_mode))
+    results = manager.run(module)
+    coverage = require_full_lowering(module) if options.require_full_lowering else analyze_lowering_coverage(module)
+    return CompileResult(module, results, coverage, operation_counts(module))

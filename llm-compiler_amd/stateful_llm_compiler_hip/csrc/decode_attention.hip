@@ -132,7 +132,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     float* __restrict__ part_ml, int q_heads, int kv_heads, int groups,
     int64_t capacity, int64_t mask_len, int64_t q_sb, int64_t q_sh,
     int64_t kv_sb, int kv_ss, int64_t kv_sh, int64_t m_sb, int m_ss,
-    int64_t o_sb, int64_t o_sh, float scale_log2, int chunk_tokens,
+    int64_t o_sb, int64_t o_sh, float scale, int chunk_tokens,
     int nchunks) {
   using M = Mfma<T>;
   using Layout = SharedLayout<T, D>;
@@ -272,7 +272,9 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
       for (int kk = 0; kk < KK; ++kk) st = M::run(as_vec<T>(tile.k[j][kk]), qv[kk], st);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float v = st[r] * scale_log2;
+        // q.k and its scaling are materialised in the tensor dtype, as the
+        // reference's bf16 matmul and multiply do; softmax stays fp32.
+        float v = slc::round_to<T>(slc::round_to<T>(st[r]) * scale) * kLog2e;
         if constexpr (MK != 0) v += tile.mk[4 * j + r];
         s[4 * j + r] = t0 + 16 * j + 4 * g + r < chunk_end ? v : -INFINITY;
       }
@@ -460,7 +462,7 @@ __global__ __launch_bounds__(256) void decode_attention_generic_kernel(
     T* __restrict__ output, int q_heads, int groups, int head_dim,
     int64_t capacity, int64_t mask_len, int64_t q_sb, int64_t q_sh,
     int64_t kv_sb, int64_t kv_ss, int64_t kv_sh, int64_t m_sb, int64_t m_ss,
-    int64_t o_sb, int64_t o_sh, float scale_log2) {
+    int64_t o_sb, int64_t o_sh, float scale) {
   __shared__ float sm_m[kGenericWaves];
   __shared__ float sm_l[kGenericWaves];
   __shared__ float sm_o[kGenericWaves][NI * 64];
@@ -492,7 +494,9 @@ __global__ __launch_bounds__(256) void decode_attention_generic_kernel(
       if (d < head_dim) dot += q[i] * slc::to_f32(kbase[t * kv_ss + d]);
     }
     dot = slc::wave_sum(dot);
-    float s = dot * scale_log2;
+    // 16-bit dtypes materialise q.k and its scaling like the reference's
+    // matmul and multiply; fp32 keeps them exact.
+    float s = (sizeof(T) == 2 ? slc::round_to<T>(slc::round_to<T>(dot) * scale) : dot * scale) * kLog2e;
     if (mask != nullptr) s += slc::load_as_f32(mask, b * m_sb + t * m_ss, mask_dtype) * kLog2e;
     const float m_new = fmaxf(m_run, s);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
@@ -564,7 +568,7 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
                 const void* lengths, int lengths_dtype, const void* mask,
                 int mask_dtype, void* output, void* workspace, int64_t batch,
                 int64_t q_heads, int64_t kv_heads, int64_t capacity,
-                int64_t mask_len, const int64_t* st, float scale_log2,
+                int64_t mask_len, const int64_t* st, float scale,
                 int64_t chunk, int64_t nchunks, hipStream_t stream) {
   float* part_o = nullptr;
   float* part_ml = nullptr;
@@ -584,7 +588,7 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
                      static_cast<int>(q_heads), static_cast<int>(kv_heads),   \
                      groups, capacity, mask_len, st[0], st[1], st[2],         \
                      static_cast<int>(st[3]), st[4], st[5],                   \
-                     static_cast<int>(st[6]), st[7], st[8], scale_log2,       \
+                     static_cast<int>(st[6]), st[7], st[8], scale,            \
                      static_cast<int>(chunk), static_cast<int>(nchunks))
   if (mask == nullptr) {
     SLC_MFMA(0);
@@ -613,7 +617,7 @@ int launch_generic(const void* query, const void* kb, const void* vb,
                    const void* lengths, int lengths_dtype, const void* mask,
                    int mask_dtype, void* output, int64_t batch, int64_t q_heads,
                    int64_t kv_heads, int64_t head_dim, int64_t capacity,
-                   int64_t mask_len, const int64_t* st, float scale_log2,
+                   int64_t mask_len, const int64_t* st, float scale,
                    hipStream_t stream) {
   const int groups = static_cast<int>(q_heads / kv_heads);
   const dim3 grid(static_cast<unsigned>(batch * q_heads));
@@ -625,7 +629,7 @@ int launch_generic(const void* query, const void* kb, const void* vb,
                      static_cast<T*>(output), static_cast<int>(q_heads),       \
                      groups, static_cast<int>(head_dim), capacity, mask_len,   \
                      st[0], st[1], st[2], st[3], st[4], st[5], st[6], st[7],   \
-                     st[8], scale_log2)
+                     st[8], scale)
   if (head_dim <= 64) {
     SLC_GENERIC(1);
   } else if (head_dim <= 128) {
@@ -685,7 +689,6 @@ extern "C" int slc_hip_decode_attention(
   const int64_t st[9] = {q_stride_b,    q_stride_h,    kv_stride_b,
                          kv_stride_s,   kv_stride_h,   mask_stride_b,
                          mask_stride_s, out_stride_b,  out_stride_h};
-  const float scale_log2 = scale * kLog2e;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t ml = mask_len;
 
@@ -721,24 +724,24 @@ extern "C" int slc_hip_decode_attention(
                                             lengths, lengths_dtype, mask,
                                             mask_dtype, output, workspace, batch,
                                             q_heads, kv_heads, capacity, ml, st,
-                                            scale_log2, chunk, nchunks, s);
+                                            scale, chunk, nchunks, s);
       return launch_mfma<slc::bf16_t, 128>(query, key_buffer, value_buffer,
                                            lengths, lengths_dtype, mask,
                                            mask_dtype, output, workspace, batch,
                                            q_heads, kv_heads, capacity, ml, st,
-                                           scale_log2, chunk, nchunks, s);
+                                           scale, chunk, nchunks, s);
     }
     if (head_dim == 64)
       return launch_mfma<slc::f16_t, 64>(query, key_buffer, value_buffer,
                                          lengths, lengths_dtype, mask,
                                          mask_dtype, output, workspace, batch,
                                          q_heads, kv_heads, capacity, ml, st,
-                                         scale_log2, chunk, nchunks, s);
+                                         scale, chunk, nchunks, s);
     return launch_mfma<slc::f16_t, 128>(query, key_buffer, value_buffer,
                                         lengths, lengths_dtype, mask,
                                         mask_dtype, output, workspace, batch,
                                         q_heads, kv_heads, capacity, ml, st,
-                                        scale_log2, chunk, nchunks, s);
+                                        scale, chunk, nchunks, s);
   }
   SLC_REQUIRE(batch * q_heads <= 0x7fffffff,
               "slc_hip_decode_attention: grid too large");
@@ -747,18 +750,18 @@ extern "C" int slc_hip_decode_attention(
       return launch_generic<float>(query, key_buffer, value_buffer, lengths,
                                    lengths_dtype, mask, mask_dtype, output,
                                    batch, q_heads, kv_heads, head_dim, capacity,
-                                   ml, st, scale_log2, s);
+                                   ml, st, scale, s);
     case SLC_BF16:
       return launch_generic<slc::bf16_t>(query, key_buffer, value_buffer,
                                          lengths, lengths_dtype, mask,
                                          mask_dtype, output, batch, q_heads,
                                          kv_heads, head_dim, capacity, ml, st,
-                                         scale_log2, s);
+                                         scale, s);
     default:
       return launch_generic<slc::f16_t>(query, key_buffer, value_buffer,
                                         lengths, lengths_dtype, mask, mask_dtype,
                                         output, batch, q_heads, kv_heads,
-                                        head_dim, capacity, ml, st, scale_log2,
+                                        head_dim, capacity, ml, st, scale,
                                         s);
   }
 }

@@ -15,8 +15,9 @@ template <typename U>
 __global__ __launch_bounds__(256) void kv_store_kernel(
     U* __restrict__ key_buffer, U* __restrict__ value_buffer,
     const U* __restrict__ key, const U* __restrict__ value,
-    const int64_t* __restrict__ positions, int64_t heads, int64_t tokens,
-    int64_t row_units, int64_t capacity, int64_t total, int64_t k_sb,
+    const int64_t* __restrict__ positions, int* __restrict__ overflow,
+    int64_t heads, int64_t tokens, int64_t row_units, int64_t capacity,
+    int64_t total, int64_t k_sb,
     int64_t k_sh, int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (gid >= total) return;
@@ -27,7 +28,10 @@ __global__ __launch_bounds__(256) void kv_store_kernel(
   const int64_t h = rest % heads;
   const int64_t b = rest / heads;
   const int64_t position = positions[b] + t;
-  if (position < 0 || position >= capacity) return;
+  if (position < 0 || position >= capacity) {
+    if (overflow != nullptr) *overflow = 1;
+    return;
+  }
   const int64_t dst = ((b * capacity + position) * heads + h) * row_units + unit;
   key_buffer[dst] = key[b * k_sb + h * k_sh + t * k_st + unit];
   value_buffer[dst] = value[b * v_sb + h * v_sh + t * v_st + unit];
@@ -35,7 +39,7 @@ __global__ __launch_bounds__(256) void kv_store_kernel(
 
 template <typename U>
 int launch(void* kb, void* vb, const void* k, const void* v,
-           const int64_t* pos, int64_t batch, int64_t heads, int64_t tokens,
+           const int64_t* pos, int* overflow, int64_t batch, int64_t heads, int64_t tokens,
            int64_t row_bytes, int64_t capacity, const int64_t* ks,
            const int64_t* vs, hipStream_t stream) {
   const int64_t unit = sizeof(U);
@@ -45,7 +49,7 @@ int launch(void* kb, void* vb, const void* k, const void* v,
   hipLaunchKernelGGL(kv_store_kernel<U>, dim3(static_cast<unsigned>(blocks)),
                      dim3(256), 0, stream, static_cast<U*>(kb),
                      static_cast<U*>(vb), static_cast<const U*>(k),
-                     static_cast<const U*>(v), pos, heads, tokens, row_units,
+                     static_cast<const U*>(v), pos, overflow, heads, tokens, row_units,
                      capacity, total, ks[0] / unit, ks[1] / unit, ks[2] / unit,
                      vs[0] / unit, vs[1] / unit, vs[2] / unit);
   return slc_host::check_launch("slc_hip_kv_store");
@@ -55,7 +59,8 @@ int launch(void* kb, void* vb, const void* k, const void* v,
 
 extern "C" int slc_hip_kv_store(void* key_buffer, void* value_buffer,
                                 const void* key, const void* value,
-                                const int64_t* positions, int dtype,
+                                const int64_t* positions, int* overflow,
+                                int dtype,
                                 int64_t batch, int64_t heads, int64_t tokens,
                                 int64_t head_dim, int64_t capacity,
                                 int64_t key_stride_b, int64_t key_stride_h,
@@ -88,15 +93,15 @@ extern "C" int slc_hip_kv_store(void* key_buffer, void* value_buffer,
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   if ((bits & 15) == 0)
-    return launch<uint4>(key_buffer, value_buffer, key, value, positions, batch,
+    return launch<uint4>(key_buffer, value_buffer, key, value, positions, overflow, batch,
                          heads, tokens, row_bytes, capacity, ks, vs, s);
   if ((bits & 7) == 0)
-    return launch<uint2>(key_buffer, value_buffer, key, value, positions, batch,
+    return launch<uint2>(key_buffer, value_buffer, key, value, positions, overflow, batch,
                          heads, tokens, row_bytes, capacity, ks, vs, s);
   if ((bits & 3) == 0)
-    return launch<uint32_t>(key_buffer, value_buffer, key, value, positions,
+    return launch<uint32_t>(key_buffer, value_buffer, key, value, positions, overflow,
                             batch, heads, tokens, row_bytes, capacity, ks, vs,
                             s);
   return launch<uint16_t>(key_buffer, value_buffer, key, value, positions,
-                          batch, heads, tokens, row_bytes, capacity, ks, vs, s);
+                          overflow, batch, heads, tokens, row_bytes, capacity, ks, vs, s);
 }

@@ -98,7 +98,7 @@ __global__ __launch_bounds__(256) void prefill_attention_mfma_kernel(
     int groups, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh,
     int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t m_sb,
     int64_t m_sq, int64_t m_sk, int64_t o_sb, int64_t o_sh, int64_t o_st,
-    float scale_log2) {
+    float scale) {
   using M = Mfma<T>;
   __shared__ __attribute__((aligned(16))) unsigned char smem[2][2][kTileBytes];
 
@@ -209,7 +209,9 @@ __global__ __launch_bounds__(256) void prefill_attention_mfma_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int kidx = k0 + kb * 16 + 4 * g + r;
-          float v = st[r] * scale_log2;
+          // q.k and its scaling are materialised in the tensor dtype, as the
+          // reference's matmul and multiply do; softmax stays fp32.
+          float v = slc::round_to<T>(slc::round_to<T>(st[r]) * scale) * kLog2e;
           if constexpr (MK != 0) {
             if (kidx < tokens) {
               const char* p = mrow + static_cast<int64_t>(kidx) * m_sk * kMaskBytes;
@@ -288,7 +290,7 @@ __global__ __launch_bounds__(256) void prefill_attention_generic_kernel(
     int q_heads, int groups, int head_dim, int causal, int64_t q_sb, int64_t q_sh,
     int64_t q_st, int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t v_sb,
     int64_t v_sh, int64_t v_st, int64_t m_sb, int64_t m_sq, int64_t m_sk,
-    int64_t o_sb, int64_t o_sh, int64_t o_st, float scale_log2) {
+    int64_t o_sb, int64_t o_sh, int64_t o_st, float scale) {
   const int lane = threadIdx.x & 63;
   const int qi = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int h = blockIdx.y;
@@ -312,7 +314,7 @@ __global__ __launch_bounds__(256) void prefill_attention_generic_kernel(
       if (d < head_dim) dot += q[i] * slc::to_f32(key[b * k_sb + kvh * k_sh + kidx * k_st + d]);
     }
     dot = slc::wave_sum(dot);
-    float s = dot * scale_log2;
+    float s = (sizeof(T) == 2 ? slc::round_to<T>(slc::round_to<T>(dot) * scale) : dot * scale) * kLog2e;
     if (mask != nullptr) s += slc::load_as_f32(mask, b * m_sb + qi * m_sq + kidx * m_sk, mask_dtype) * kLog2e;
     const float m_new = fmaxf(m_run, s);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
@@ -337,34 +339,34 @@ __global__ __launch_bounds__(256) void prefill_attention_generic_kernel(
 template <typename T, int MK, bool CAUSAL>
 int launch_mfma(const void* q, const void* k, const void* v, const void* mask, void* out,
                 int64_t batch, int tokens, int q_heads, int groups, const int64_t* st,
-                float scale_log2, hipStream_t stream) {
+                float scale, hipStream_t stream) {
   const dim3 grid((tokens + kQueries - 1) / kQueries, q_heads, static_cast<unsigned>(batch));
   hipLaunchKernelGGL((prefill_attention_mfma_kernel<T, MK, CAUSAL>), grid, dim3(256), 0, stream,
                      static_cast<const T*>(q), static_cast<const T*>(k),
                      static_cast<const T*>(v), mask, static_cast<T*>(out), tokens, q_heads,
                      groups, st[0], st[1], st[2], st[3], st[4], st[5], st[6], st[7], st[8],
-                     st[9], st[10], st[11], st[12], st[13], st[14], scale_log2);
+                     st[9], st[10], st[11], st[12], st[13], st[14], scale);
   return slc_host::check_launch("slc_hip_prefill_attention");
 }
 
 template <typename T, bool CAUSAL>
 int dispatch_mask(const void* q, const void* k, const void* v, const void* mask,
                   int mask_dtype, void* out, int64_t batch, int tokens, int q_heads,
-                  int groups, const int64_t* st, float scale_log2, hipStream_t s) {
+                  int groups, const int64_t* st, float scale, hipStream_t s) {
   if (mask == nullptr)
-    return launch_mfma<T, 0, CAUSAL>(q, k, v, mask, out, batch, tokens, q_heads, groups, st, scale_log2, s);
+    return launch_mfma<T, 0, CAUSAL>(q, k, v, mask, out, batch, tokens, q_heads, groups, st, scale, s);
   if (mask_dtype == SLC_BF16)
-    return launch_mfma<T, SLC_BF16 + 1, CAUSAL>(q, k, v, mask, out, batch, tokens, q_heads, groups, st, scale_log2, s);
+    return launch_mfma<T, SLC_BF16 + 1, CAUSAL>(q, k, v, mask, out, batch, tokens, q_heads, groups, st, scale, s);
   if (mask_dtype == SLC_F16)
-    return launch_mfma<T, SLC_F16 + 1, CAUSAL>(q, k, v, mask, out, batch, tokens, q_heads, groups, st, scale_log2, s);
-  return launch_mfma<T, SLC_F32 + 1, CAUSAL>(q, k, v, mask, out, batch, tokens, q_heads, groups, st, scale_log2, s);
+    return launch_mfma<T, SLC_F16 + 1, CAUSAL>(q, k, v, mask, out, batch, tokens, q_heads, groups, st, scale, s);
+  return launch_mfma<T, SLC_F32 + 1, CAUSAL>(q, k, v, mask, out, batch, tokens, q_heads, groups, st, scale, s);
 }
 
 template <typename T>
 int launch_generic(const void* q, const void* k, const void* v, const void* mask,
                    int mask_dtype, void* out, int64_t batch, int tokens, int q_heads,
                    int groups, int head_dim, int causal, const int64_t* st,
-                   float scale_log2, hipStream_t stream) {
+                   float scale, hipStream_t stream) {
   const dim3 grid((tokens + 3) / 4, q_heads, static_cast<unsigned>(batch));
 #define SLC_GEN(NI)                                                                      \
   hipLaunchKernelGGL((prefill_attention_generic_kernel<T, NI>), grid, dim3(256), 0, stream, \
@@ -372,7 +374,7 @@ int launch_generic(const void* q, const void* k, const void* v, const void* mask
                      static_cast<const T*>(v), mask, mask_dtype, static_cast<T*>(out),   \
                      tokens, q_heads, groups, head_dim, causal, st[0], st[1], st[2],     \
                      st[3], st[4], st[5], st[6], st[7], st[8], st[9], st[10], st[11],    \
-                     st[12], st[13], st[14], scale_log2)
+                     st[12], st[13], st[14], scale)
   if (head_dim <= 64) {
     SLC_GEN(1);
   } else if (head_dim <= 128) {
@@ -407,7 +409,6 @@ extern "C" int slc_hip_prefill_attention(
   const int64_t st[15] = {q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh,
                           v_st, m_sb, m_sq, m_sk, o_sb, o_sh, o_st};
   const int groups = static_cast<int>(q_heads / kv_heads);
-  const float scale_log2 = scale * kLog2e;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int T_ = static_cast<int>(tokens);
   const uint64_t bits = reinterpret_cast<uintptr_t>(query) | reinterpret_cast<uintptr_t>(key) |
@@ -419,24 +420,24 @@ extern "C" int slc_hip_prefill_attention(
                        tokens * (k_st > v_st ? k_st : v_st) * 2 < (1LL << 31);
   if (mfma_ok) {
     if (dtype == SLC_BF16) {
-      return causal ? dispatch_mask<slc::bf16_t, true>(query, key, value, mask, mask_dtype, output, batch, T_, static_cast<int>(q_heads), groups, st, scale_log2, s)
-                    : dispatch_mask<slc::bf16_t, false>(query, key, value, mask, mask_dtype, output, batch, T_, static_cast<int>(q_heads), groups, st, scale_log2, s);
+      return causal ? dispatch_mask<slc::bf16_t, true>(query, key, value, mask, mask_dtype, output, batch, T_, static_cast<int>(q_heads), groups, st, scale, s)
+                    : dispatch_mask<slc::bf16_t, false>(query, key, value, mask, mask_dtype, output, batch, T_, static_cast<int>(q_heads), groups, st, scale, s);
     }
-    return causal ? dispatch_mask<slc::f16_t, true>(query, key, value, mask, mask_dtype, output, batch, T_, static_cast<int>(q_heads), groups, st, scale_log2, s)
-                  : dispatch_mask<slc::f16_t, false>(query, key, value, mask, mask_dtype, output, batch, T_, static_cast<int>(q_heads), groups, st, scale_log2, s);
+    return causal ? dispatch_mask<slc::f16_t, true>(query, key, value, mask, mask_dtype, output, batch, T_, static_cast<int>(q_heads), groups, st, scale, s)
+                  : dispatch_mask<slc::f16_t, false>(query, key, value, mask, mask_dtype, output, batch, T_, static_cast<int>(q_heads), groups, st, scale, s);
   }
   switch (dtype) {
     case SLC_F32:
       return launch_generic<float>(query, key, value, mask, mask_dtype, output, batch, T_,
                                    static_cast<int>(q_heads), groups, static_cast<int>(head_dim),
-                                   causal, st, scale_log2, s);
+                                   causal, st, scale, s);
     case SLC_BF16:
       return launch_generic<slc::bf16_t>(query, key, value, mask, mask_dtype, output, batch, T_,
                                          static_cast<int>(q_heads), groups,
-                                         static_cast<int>(head_dim), causal, st, scale_log2, s);
+                                         static_cast<int>(head_dim), causal, st, scale, s);
     default:
       return launch_generic<slc::f16_t>(query, key, value, mask, mask_dtype, output, batch, T_,
                                         static_cast<int>(q_heads), groups,
-                                        static_cast<int>(head_dim), causal, st, scale_log2, s);
+                                        static_cast<int>(head_dim), causal, st, scale, s);
   }
 }

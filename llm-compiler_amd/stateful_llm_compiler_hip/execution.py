@@ -1,0 +1,705 @@
+"""KV runtime state and the KernelIR executor of the gfx950 backend.
+
+``PreallocatedKVCacheState`` keeps the reference's contract
+(src/stateful_llm_compiler/execution.py:98-475): per-layer physical buffers
+B x capacity x H x D (contiguous_bshd) that never move, int64 lengths per
+batch row, immutable SSA versions (``advance`` returns a new state sharing
+the buffers), validation errors as ``ExecutionError``.  Its writer / runner
+plug-ins are the HIP kernels; the capacity guard is a device-side flag (no
+host synchronisation on the hot path) read by ``check_capacity()``.
+
+``HipExecutor`` walks a lowered KernelIR function and dispatches each op by
+name (triton_executor.py:69-130 in the reference), validating every argument
+and result against its IR type like the reference executor
+(execution.py:530-579, 1094-1157).  It executes only lowered ops: an
+unlowered ``serve.*`` / ``aten.*`` op raises instead of falling back to eager
+PyTorch.
+"""
+
+from __future__ import annotations
+
+import re
+from dataclasses import dataclass, replace
+from typing import Any, Callable, Sequence
+
+import torch
+import torch.nn.functional as F
+
+from .backends import (
+    hip_add,
+    hip_decode_attention,
+    hip_embedding,
+    hip_kv_advance,
+    hip_kv_store,
+    hip_linear,
+    hip_prefill_attention,
+    hip_rms_norm,
+    hip_rope,
+    hip_rope_table,
+    hip_swiglu,
+)
+from .cost_model import resolve_lowering_plan
+from .ir import (
+    Function,
+    IRType,
+    KVStateType,
+    Module,
+    ScalarType,
+    StaticDim,
+    SymbolicDim,
+    TensorType,
+    TupleType,
+    UnknownType,
+)
+from .lowering import require_full_lowering
+
+
+class ExecutionError(RuntimeError):
+    pass
+
+
+DTYPES = {
+    "f16": torch.float16,
+    "bf16": torch.bfloat16,
+    "f32": torch.float32,
+    "f64": torch.float64,
+    "i8": torch.int8,
+    "i16": torch.int16,
+    "i32": torch.int32,
+    "i64": torch.int64,
+    "i1": torch.bool,
+}
+DTYPE_NAMES = {value: key for key, value in DTYPES.items()}
+
+
+@dataclass(frozen=True)
+class PreallocatedKVCacheState:
+    """Shared physical KV buffers plus per-version logical lengths."""
+
+    keys: tuple[torch.Tensor, ...]
+    values: tuple[torch.Tensor, ...]
+    lengths: tuple[torch.Tensor, ...]
+    capacity: int
+    generation: int = 0
+    # int32[1] device flag shared by all versions: set when a store or an
+    # advance leaves [0, capacity].
+    overflow: torch.Tensor | None = None
+    # When true, advance() updates the lengths tensors in place (stable
+    # addresses for HIP graph replay); otherwise it creates new tensors.
+    in_place_lengths: bool = False
+    # Slots whose lengths are known (on the host) to be zero, so prefill_store
+    # needs no device-to-host check; None = unknown.
+    zero_slots: frozenset[int] | None = None
+
+    def __post_init__(self) -> None:
+        if self.capacity <= 0:
+            raise ExecutionError("KV capacity must be positive")
+        if not self.keys or len(self.keys) != len(self.values) or len(self.keys) != len(self.lengths):
+            raise ExecutionError("KV key/value/length slot counts must agree")
+        for key, value, lengths in zip(self.keys, self.values, self.lengths):
+            if key.shape != value.shape or key.ndim != 4:
+                raise ExecutionError("KV buffers must be equal-shaped B x C x H x D tensors")
+            if key.shape[1] != self.capacity:
+                raise ExecutionError("KV buffer dim 1 must equal the capacity")
+            if lengths.shape != (key.shape[0],):
+                raise ExecutionError("KV lengths must be a 1-D batch tensor")
+            if lengths.dtype != torch.int64:
+                raise ExecutionError("KV lengths must be int64")
+
+    @classmethod
+    def empty_from_key_template(
+        cls, key: torch.Tensor, *, num_layers: int, capacity: int, in_place_lengths: bool = False
+    ) -> "PreallocatedKVCacheState":
+        """Zeroed buffers for every layer from a B x H x T x D key template."""
+
+        if key.ndim != 4 or num_layers <= 0 or capacity <= 0:
+            raise ExecutionError("KV init got an illegal template, layer count or capacity")
+        batch, heads, _, head_dim = key.shape
+        keys = tuple(
+            torch.zeros(batch, capacity, heads, head_dim, device=key.device, dtype=key.dtype)
+            for _ in range(num_layers)
+        )
+        values = tuple(torch.zeros_like(buffer) for buffer in keys)
+        lengths = tuple(torch.zeros(batch, device=key.device, dtype=torch.int64) for _ in range(num_layers))
+        overflow = torch.zeros(1, device=key.device, dtype=torch.int32)
+        return cls(keys, values, lengths, capacity, overflow=overflow,
+                   in_place_lengths=in_place_lengths, zero_slots=frozenset(range(num_layers)))
+
+    @classmethod
+    def from_layer_tensors(
+        cls,
+        past_key_values: Sequence[tuple[torch.Tensor, torch.Tensor]],
+        *,
+        capacity: int,
+        in_place_lengths: bool = False,
+    ) -> "PreallocatedKVCacheState":
+        """Copy logical B x H x S x D caches into preallocated slots (setup only)."""
+
+        if not past_key_values:
+            raise ExecutionError("a multi-layer KV cache needs at least one slot")
+        keys, values, lengths = [], [], []
+        structure = None
+        for slot, (key, value) in enumerate(past_key_values):
+            if key.shape != value.shape or key.ndim != 4:
+                raise ExecutionError(f"layer {slot}: initial K/V must be equal B x H x S x D tensors")
+            batch, heads, sequence, head_dim = key.shape
+            this = (batch, heads, sequence, head_dim, key.dtype, key.device)
+            if structure is None:
+                structure = this
+            elif this != structure:
+                raise ExecutionError("all layer slots need one K/V shape, dtype and device")
+            if sequence > capacity:
+                raise ExecutionError(f"layer {slot}: initial length {sequence} exceeds capacity {capacity}")
+            kb = torch.zeros(batch, capacity, heads, head_dim, device=key.device, dtype=key.dtype)
+            vb = torch.zeros_like(kb)
+            kb[:, :sequence].copy_(key.transpose(1, 2))
+            vb[:, :sequence].copy_(value.transpose(1, 2))
+            keys.append(kb)
+            values.append(vb)
+            lengths.append(torch.full((batch,), sequence, device=key.device, dtype=torch.int64))
+        overflow = torch.zeros(1, device=keys[0].device, dtype=torch.int32)
+        return cls(tuple(keys), tuple(values), tuple(lengths), capacity, overflow=overflow,
+                   in_place_lengths=in_place_lengths)
+
+    def positions(self, slot: int) -> torch.Tensor:
+        try:
+            return self.lengths[slot]
+        except IndexError as error:
+            raise ExecutionError(f"KV buffer has no slot {slot}") from error
+
+    def read(self, slot: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """Logical B x H x S x D view of the longest prefix (host sync)."""
+
+        try:
+            key, value, lengths = self.keys[slot], self.values[slot], self.lengths[slot]
+        except IndexError as error:
+            raise ExecutionError(f"KV buffer has no slot {slot}") from error
+        used = int(lengths.max().item())
+        return key[:, :used].transpose(1, 2), value[:, :used].transpose(1, 2)
+
+    def decode_attention(
+        self,
+        slot: int,
+        query: torch.Tensor,
+        attention_mask: torch.Tensor,
+        *,
+        groups: int,
+        scale: float,
+        runner: Callable[..., torch.Tensor] = hip_decode_attention,
+    ) -> torch.Tensor:
+        """Decode attention straight from the B x Capacity x H x D buffers."""
+
+        key_buffer, value_buffer, lengths = self._attention_inputs(slot, query, attention_mask, groups)
+        return runner(query, key_buffer, value_buffer, lengths, attention_mask, scale=scale)
+
+    def _attention_inputs(self, slot, query, attention_mask, groups):
+        try:
+            key_buffer, value_buffer, lengths = self.keys[slot], self.values[slot], self.lengths[slot]
+        except IndexError as error:
+            raise ExecutionError(f"KV buffer has no slot {slot}") from error
+        if query.ndim != 4 or query.shape[2] != 1:
+            raise ExecutionError("decode attention query must be B x H x 1 x D")
+        if attention_mask.ndim != 4 or attention_mask.shape[2] != 1:
+            raise ExecutionError("decode attention mask must be B x 1 x 1 x S")
+        if (
+            query.shape[0] != key_buffer.shape[0]
+            or query.shape[0] != attention_mask.shape[0]
+            or query.shape[3] != key_buffer.shape[3]
+        ):
+            raise ExecutionError("decode attention batch or head dim does not match the KV buffer")
+        if groups <= 0 or query.shape[1] != key_buffer.shape[2] * groups:
+            raise ExecutionError("decode attention GQA groups do not match")
+        if attention_mask.shape[-1] > self.capacity:
+            raise ExecutionError("decode attention mask is longer than the KV capacity")
+        return key_buffer, value_buffer, lengths
+
+    def store(
+        self,
+        slot: int,
+        key: torch.Tensor,
+        value: torch.Tensor,
+        positions: torch.Tensor,
+        *,
+        writer: Callable[..., None] = hip_kv_store,
+    ) -> "PreallocatedKVCacheState":
+        buffer_key, buffer_value = self._validate_store(slot, key, value, positions)
+        writer(buffer_key, buffer_value, key, value, positions, overflow=self.overflow)
+        # Only rows past the current logical length change: older versions'
+        # visible prefixes are untouched, so the same object is returned.
+        return self
+
+    def prefill_store(
+        self,
+        slot: int,
+        key: torch.Tensor,
+        value: torch.Tensor,
+        *,
+        writer: Callable[..., None] = hip_kv_store,
+    ) -> "PreallocatedKVCacheState":
+        """Write a layer's prompt K/V from position 0, then advance by T."""
+
+        positions = self.positions(slot)
+        if self.zero_slots is not None:
+            if slot not in self.zero_slots:
+                raise ExecutionError("prefill KV store needs the slot's length to be 0")
+        elif bool((positions != 0).any()):
+            raise ExecutionError("prefill KV store needs the slot's length to be 0")
+        self.store(slot, key, value, positions, writer=writer)
+        return self.advance(slot, delta=key.shape[2])
+
+    def advance(self, slot: int, *, delta: int) -> "PreallocatedKVCacheState":
+        if delta <= 0:
+            raise ExecutionError("KV advance delta must be positive")
+        positions = self.positions(slot)
+        out = positions if self.in_place_lengths else None
+        next_lengths = hip_kv_advance(positions, delta, self.capacity, out=out, overflow=self.overflow)
+        lengths = list(self.lengths)
+        lengths[slot] = next_lengths
+        zero = None if self.zero_slots is None else self.zero_slots - {slot}
+        return replace(self, lengths=tuple(lengths), generation=self.generation + 1, zero_slots=zero)
+
+    def check_capacity(self) -> None:
+        """Synchronise and raise if any store or advance overflowed the capacity."""
+
+        if self.overflow is not None and int(self.overflow.item()) != 0:
+            raise ExecutionError(f"KV store or advance exceeded capacity {self.capacity}")
+
+    def _validate_store(self, slot, key, value, positions):
+        try:
+            buffer_key, buffer_value = self.keys[slot], self.values[slot]
+        except IndexError as error:
+            raise ExecutionError(f"KV buffer has no slot {slot}") from error
+        if key.shape != value.shape or key.ndim != 4:
+            raise ExecutionError("KV store K/V must be equal B x H x T x D tensors")
+        batch, heads, _, head_dim = key.shape
+        if batch != buffer_key.shape[0] or heads != buffer_key.shape[2] or head_dim != buffer_key.shape[3]:
+            raise ExecutionError("KV store batch, heads or head dim does not match")
+        if positions.shape != (batch,) or positions.dtype != torch.int64:
+            raise ExecutionError("KV store positions must be a 1-D batch int64 tensor")
+        if positions.device != key.device:
+            raise ExecutionError("KV store positions and K/V must share a device")
+        return buffer_key, buffer_value
+
+
+@dataclass
+class ExecutionResult:
+    outputs: tuple[Any, ...]
+    executed_operations: tuple[str, ...]
+    symbolic_dimensions: dict[str, int]
+
+
+class HipExecutor:
+    """Executes lowered KernelIR on the gfx950 kernels."""
+
+    def __init__(self, *, strict: bool = True, validate: bool = True) -> None:
+        self.strict = strict
+        self.validate = validate
+        self.lowering_trace: list[dict[str, Any]] = []
+        self._handlers: dict[str, Callable[[list[Any], dict[str, Any]], Any]] = {
+            "kernel.hip.rms_norm": self._rms_norm,
+            "kernel.hip.linear": self._linear,
+            "kernel.hip.rope": self._rope,
+            "kernel.hip.prefill_attention": self._prefill_attention,
+            "kernel.hip.decode_attention": self._decode_attention,
+            "kernel.hip.kv_store": self._kv_store,
+            "kernel.hip.kv_prefill_store": self._kv_prefill_store,
+            "kernel.hip.embedding": self._embedding,
+            "kernel.hip.add": self._add,
+            "kernel.hip.swiglu": self._swiglu,
+            "kernel.hip.rope_table": self._rope_table,
+            "runtime.kv.init": self._kv_init,
+            "runtime.kv.length": self._kv_length,
+            "runtime.kv.advance": self._kv_advance,
+            "kernel.metadata.view": self._view,
+            "kernel.metadata.reshape": self._view,
+            "kernel.metadata.transpose": self._transpose,
+            "kernel.metadata.unsqueeze": self._unsqueeze,
+            "kernel.metadata.getitem": self._getitem,
+            "kernel.rocm_compat.rms_norm": self._compat_rms_norm,
+            "kernel.rocm_compat.linear": self._compat_linear,
+            "kernel.rocm_compat.decode_attention": self._compat_decode_attention,
+            "kernel.rocm_compat.prefill_attention": self._compat_prefill_attention,
+            "kernel.rocm_compat.rope_table": self._compat_rope_table,
+            "kernel.rocm_compat.swiglu": self._compat_swiglu,
+        }
+
+    # ------------------------------------------------------------------ run
+
+    def run(self, module: Module, arguments: Sequence[Any], *, function_name: str | None = None) -> ExecutionResult:
+        if self.strict:
+            # Check the whole graph before any op runs.
+            require_full_lowering(module)
+        function = select_function(module, function_name)
+        if len(arguments) != len(function.block.arguments):
+            raise ExecutionError(
+                f"@{function.name} takes {len(function.block.arguments)} arguments, got {len(arguments)}"
+            )
+        environment: dict[str, Any] = {}
+        symbols: dict[str, int] = {}
+        for argument, value in zip(function.block.arguments, arguments):
+            if self.validate:
+                validate_runtime_value(value, argument.type, symbols, context=f"argument {argument.name}")
+            environment[argument.name] = value
+        trace = []
+        for operation in function.block.operations:
+            handler = self._handlers.get(operation.name)
+            if handler is None:
+                raise ExecutionError(f"no gfx950 kernel for operation {operation.name}")
+            result = handler([environment[v.name] for v in operation.operands], operation.attributes)
+            values = normalize_results(result, len(operation.results), operation.name)
+            for ir_value, runtime_value in zip(operation.results, values):
+                if self.validate:
+                    validate_runtime_value(
+                        runtime_value, ir_value.type, symbols,
+                        context=f"{operation.name} result {ir_value.name}",
+                    )
+                environment[ir_value.name] = runtime_value
+            trace.append(operation.name)
+        outputs = tuple(environment[v.name] for v in function.returns)
+        return ExecutionResult(outputs, tuple(trace), dict(symbols))
+
+    # -------------------------------------------------------------- kernels
+
+    def _rms_norm(self, operands, attributes):
+        if len(operands) != 2:
+            raise ExecutionError("kernel.hip.rms_norm takes input and weight")
+        tensor, weight = operands
+        rows = tensor.numel() // tensor.shape[-1]
+        decision = resolve_lowering_plan(attributes.get("lowering_plan"), rows)
+        self.lowering_trace.append({
+            "op": "rms_norm", "backend": "hip", "plan_backend": decision.backend,
+            "source": decision.source, "rows": rows, "profile_rows": decision.profile_rows,
+            "estimated_us": decision.estimated_us,
+        })
+        return hip_rms_norm(
+            tensor, weight, epsilon=float(attributes["epsilon"]),
+            output_dtype=attributes.get("output_dtype"),
+            round_before_weight=bool(attributes.get("round_before_weight", False)),
+        )
+
+    @staticmethod
+    def _linear(operands, attributes):
+        if len(operands) not in (2, 3):
+            raise ExecutionError("kernel.hip.linear takes input, weight and an optional bias")
+        bias = operands[2] if len(operands) == 3 else None
+        if bool(attributes.get("has_bias")) != (bias is not None):
+            raise ExecutionError("kernel.hip.linear has_bias does not match its operands")
+        return hip_linear(operands[0], operands[1], bias)
+
+    @staticmethod
+    def _rope(operands, attributes):
+        if len(operands) != 4:
+            raise ExecutionError("kernel.hip.rope takes query, key, cosine and sine")
+        if operands[0].shape[-1] != int(attributes["head_dim"]):
+            raise ExecutionError("kernel.hip.rope head dim mismatch")
+        return hip_rope(*operands)
+
+    @staticmethod
+    def _prefill_attention(operands, attributes):
+        if len(operands) != 4:
+            raise ExecutionError("kernel.hip.prefill_attention takes query, key, value and mask")
+        query, key, value, mask = operands
+        groups = int(attributes["groups"])
+        if query.shape[1] != key.shape[1] * groups:
+            raise ExecutionError("kernel.hip.prefill_attention GQA groups do not match")
+        return hip_prefill_attention(
+            query, key, value, mask, scale=float(attributes["scale"]),
+            causal=attributes.get("causal") is True,
+        )
+
+    @staticmethod
+    def _decode_attention(operands, attributes):
+        if len(operands) != 3 or not isinstance(operands[0], PreallocatedKVCacheState):
+            raise ExecutionError("kernel.hip.decode_attention takes state, query and mask")
+        state, query, mask = operands
+        return state.decode_attention(
+            int(attributes.get("slot", 0)), query, mask, groups=int(attributes["groups"]),
+            scale=float(attributes["scale"]),
+        )
+
+    @staticmethod
+    def _kv_store(operands, attributes):
+        if len(operands) != 4 or not isinstance(operands[0], PreallocatedKVCacheState):
+            raise ExecutionError("kernel.hip.kv_store takes state, key, value and positions")
+        state, key, value, positions = operands
+        return state.store(int(attributes.get("slot", 0)), key, value, positions)
+
+    @staticmethod
+    def _kv_prefill_store(operands, attributes):
+        if len(operands) != 3 or not isinstance(operands[0], PreallocatedKVCacheState):
+            raise ExecutionError("kernel.hip.kv_prefill_store takes state, key and value")
+        state, key, value = operands
+        return state.prefill_store(int(attributes.get("slot", 0)), key, value)
+
+    @staticmethod
+    def _embedding(operands, attributes):
+        ids, table = operands
+        return hip_embedding(ids, table)
+
+    @staticmethod
+    def _add(operands, attributes):
+        return hip_add(*operands)
+
+    @staticmethod
+    def _swiglu(operands, attributes):
+        return hip_swiglu(*operands)
+
+    @staticmethod
+    def _rope_table(operands, attributes):
+        positions, inv_freq = operands
+        return hip_rope_table(positions, inv_freq, DTYPES[attributes["dtype"]])
+
+    @staticmethod
+    def _kv_init(operands, attributes):
+        if len(operands) != 1 or not isinstance(operands[0], torch.Tensor):
+            raise ExecutionError("runtime.kv.init takes one key template")
+        return PreallocatedKVCacheState.empty_from_key_template(
+            operands[0], num_layers=int(attributes["num_layers"]),
+            capacity=int(attributes["capacity"]),
+        )
+
+    @staticmethod
+    def _kv_length(operands, attributes):
+        if len(operands) != 1 or not isinstance(operands[0], PreallocatedKVCacheState):
+            raise ExecutionError("runtime.kv.length takes a KV state")
+        return operands[0].positions(int(attributes.get("slot", 0)))
+
+    @staticmethod
+    def _kv_advance(operands, attributes):
+        if len(operands) != 1 or not isinstance(operands[0], PreallocatedKVCacheState):
+            raise ExecutionError("runtime.kv.advance takes a KV state")
+        return operands[0].advance(int(attributes.get("slot", 0)), delta=int(attributes.get("delta", 1)))
+
+    # -------------------------------------------------------------- metadata
+
+    @staticmethod
+    def _view(operands, attributes):
+        (tensor,) = operands
+        shape = resolve_shape(attributes["shape"], tensor)
+        try:
+            return tensor.view(shape)
+        except RuntimeError as error:
+            raise ExecutionError(
+                f"metadata view {tuple(tensor.shape)} -> {shape} would need a copy"
+            ) from error
+
+    @staticmethod
+    def _transpose(operands, attributes):
+        (tensor,) = operands
+        return tensor.transpose(int(attributes["dim0"]), int(attributes["dim1"]))
+
+    @staticmethod
+    def _unsqueeze(operands, attributes):
+        (tensor,) = operands
+        return tensor.unsqueeze(int(attributes["dim"]))
+
+    @staticmethod
+    def _getitem(operands, attributes):
+        (value,) = operands
+        return value[int(attributes["index"])]
+
+    # --------------------------------------------------------------- compat
+
+    @staticmethod
+    def _compat_rms_norm(operands, attributes):
+        """PyTorch-ROCm composite with the reference executor's rounding order
+        (execution.py:674-692)."""
+
+        _require_gpu(operands, "kernel.rocm_compat.rms_norm")
+        tensor, weight = operands
+        epsilon = float(attributes["epsilon"])
+        variance = tensor.float().pow(2).mean(dim=-1, keepdim=True)
+        normalized = tensor.float() * torch.rsqrt(variance + epsilon)
+        dtype = DTYPES.get(attributes.get("output_dtype"), tensor.dtype)
+        if bool(attributes.get("round_before_weight", False)):
+            return weight * normalized.to(dtype)
+        return (normalized * weight.float()).to(dtype)
+
+    @staticmethod
+    def _compat_linear(operands, attributes):
+        """PyTorch's ROCm BLAS GEMM (the reference's kernel.cublas.linear)."""
+
+        _require_gpu(operands, "kernel.rocm_compat.linear")
+        bias = operands[2] if len(operands) == 3 else None
+        if bool(attributes.get("has_bias")) != (bias is not None):
+            raise ExecutionError("kernel.rocm_compat.linear has_bias does not match its operands")
+        return F.linear(operands[0], operands[1], bias)
+
+    @staticmethod
+    def _compat_decode_attention(operands, attributes):
+        """Eager composite of the original graph's GQA attention
+        (triton_executor.py:419-463 in the reference)."""
+
+        if len(operands) != 3 or not isinstance(operands[0], PreallocatedKVCacheState):
+            raise ExecutionError("kernel.rocm_compat.decode_attention takes state, query and mask")
+        state, query, mask = operands
+        _require_gpu([query, mask], "kernel.rocm_compat.decode_attention")
+        groups = int(attributes["groups"])
+        key_buffer, value_buffer, lengths = state._attention_inputs(int(attributes.get("slot", 0)), query, mask, groups)
+        sequence = mask.shape[-1]
+        key = key_buffer[:, :sequence].permute(0, 2, 1, 3).repeat_interleave(groups, dim=1)
+        value = value_buffer[:, :sequence].permute(0, 2, 1, 3).repeat_interleave(groups, dim=1)
+        scores = torch.matmul(query, key.transpose(-2, -1)) * float(attributes["scale"])
+        scores = scores.float() + mask.float()
+        valid = torch.arange(sequence, device=query.device).view(1, 1, 1, sequence) < lengths.view(-1, 1, 1, 1)
+        scores = scores.masked_fill(~valid, float("-inf"))
+        return torch.matmul(torch.softmax(scores, dim=-1).to(query.dtype), value)
+
+    @staticmethod
+    def _compat_prefill_attention(operands, attributes):
+        """Eager composite of the original prefill attention (execution.py:707-739)."""
+
+        _require_gpu(operands, "kernel.rocm_compat.prefill_attention")
+        query, key, value, mask = operands
+        groups = int(attributes["groups"])
+        expanded_key = key.repeat_interleave(groups, dim=1)
+        expanded_value = value.repeat_interleave(groups, dim=1)
+        scores = torch.matmul(query, expanded_key.transpose(-2, -1)) * float(attributes["scale"])
+        scores = scores.float() + mask.float()
+        if attributes.get("causal") is True:
+            tokens = query.shape[2]
+            future = torch.triu(torch.ones(tokens, tokens, dtype=torch.bool, device=query.device), diagonal=1)
+            scores = scores.masked_fill(future, float("-inf"))
+        context = torch.matmul(torch.softmax(scores, dim=-1).to(query.dtype), expanded_value)
+        # Same bytes in the [B, T, H, D] layout the head merge views (the eager
+        # model makes this copy with .transpose(1, 2).contiguous()).
+        return context.transpose(1, 2).contiguous().transpose(1, 2)
+
+
+    @staticmethod
+    def _compat_rope_table(operands, attributes):
+        """cos/sin of cat(f, f), f = pos * inv_freq, with PyTorch's kernels
+        (qwen2.py:136-149)."""
+
+        _require_gpu(operands, "kernel.rocm_compat.rope_table")
+        positions, inv_freq = operands
+        freqs = positions.float().unsqueeze(-1) * inv_freq.float().view(1, 1, -1)
+        emb = torch.cat((freqs, freqs), dim=-1)
+        dtype = DTYPES[attributes["dtype"]]
+        return emb.cos().to(dtype), emb.sin().to(dtype)
+
+    @staticmethod
+    def _compat_swiglu(operands, attributes):
+        """silu(gate) * up with PyTorch's SiLU (qwen2.py:253-256)."""
+
+        _require_gpu(operands, "kernel.rocm_compat.swiglu")
+        return F.silu(operands[0]) * operands[1]
+
+
+def _require_gpu(operands: Sequence[Any], what: str) -> None:
+    tensors = [o for o in operands if isinstance(o, torch.Tensor)]
+    if not tensors or not all(t.is_cuda for t in tensors):
+        raise ExecutionError(f"{what}: every tensor must be on the GPU")
+
+
+def resolve_shape(spec: Sequence[Any], tensor: torch.Tensor) -> list[int]:
+    """View shapes: ints, -1, or {"dim": i} for the input's size at axis i."""
+
+    shape = []
+    for item in spec:
+        if isinstance(item, dict) and "dim" in item:
+            shape.append(int(tensor.shape[int(item["dim"])]))
+        else:
+            shape.append(int(item))
+    return shape
+
+
+def select_function(module: Module, function_name: str | None) -> Function:
+    if function_name is None:
+        if len(module.functions) != 1:
+            raise ExecutionError("the module has several functions; pass function_name")
+        return module.functions[0]
+    for function in module.functions:
+        if function.name == function_name:
+            return function
+    raise ExecutionError(f"no function @{function_name}")
+
+
+def normalize_results(result: Any, expected: int, name: str) -> tuple[Any, ...]:
+    if expected == 0:
+        if result is not None:
+            raise ExecutionError(f"{name} must not produce a result")
+        return ()
+    if expected == 1:
+        return (result,)
+    if not isinstance(result, (tuple, list)) or len(result) != expected:
+        raise ExecutionError(f"{name} must produce {expected} results")
+    return tuple(result)
+
+
+def validate_runtime_value(value: Any, type_: IRType, symbols: dict[str, int], *, context: str) -> None:
+    """Type / shape / device / symbol guard (execution.py:1094-1157)."""
+
+    if isinstance(type_, UnknownType):
+        return
+    if isinstance(type_, TensorType):
+        if not isinstance(value, torch.Tensor):
+            raise ExecutionError(f"{context} must be a tensor")
+        expected = DTYPES.get(type_.dtype)
+        if expected is not None and value.dtype != expected:
+            raise ExecutionError(f"{context} dtype must be {expected}, got {value.dtype}")
+        if str(value.device) != type_.device:
+            raise ExecutionError(f"{context} device must be {type_.device}, got {value.device}")
+        if value.ndim != len(type_.shape):
+            raise ExecutionError(f"{context} rank must be {len(type_.shape)}, got {value.ndim}")
+        for index, (actual, dimension) in enumerate(zip(value.shape, type_.shape)):
+            if isinstance(dimension, StaticDim):
+                if actual != dimension.value:
+                    raise ExecutionError(f"{context} dim {index} must be {dimension.value}, got {actual}")
+            elif isinstance(dimension, SymbolicDim):
+                _bind_symbol(dimension, int(actual), symbols, context, index)
+        return
+    if isinstance(type_, KVStateType):
+        _validate_kv_state(value, type_, context)
+        return
+    if isinstance(type_, TupleType):
+        if not isinstance(value, (tuple, list)) or len(value) != len(type_.elements):
+            raise ExecutionError(f"{context} must be a tuple of {len(type_.elements)}")
+        for index, (item, item_type) in enumerate(zip(value, type_.elements)):
+            validate_runtime_value(item, item_type, symbols, context=f"{context}[{index}]")
+        return
+    if isinstance(type_, ScalarType):
+        if type_.dtype in {"index", "symint"} and not isinstance(value, int):
+            raise ExecutionError(f"{context} must be an integer scalar")
+        return
+    raise ExecutionError(f"{context} has a type that cannot execute: {type_}")
+
+
+def _validate_kv_state(value: Any, type_: KVStateType, context: str) -> None:
+    if not isinstance(value, PreallocatedKVCacheState):
+        raise ExecutionError(f"{context} must be a preallocated KV runtime state")
+    if type_.layout != "contiguous_bshd":
+        raise ExecutionError(f"{context}: layout {type_.layout} is not supported by the runtime")
+    if type_.capacity is not None and value.capacity != type_.capacity:
+        raise ExecutionError(f"{context} capacity must be {type_.capacity}, got {value.capacity}")
+    if len(value.keys) != type_.num_layers:
+        raise ExecutionError(f"{context} must hold {type_.num_layers} layer slots")
+    expected = DTYPES.get(type_.dtype)
+    for slot, key in enumerate(value.keys):
+        if key.shape[2] != type_.num_kv_heads or key.shape[3] != type_.head_dim:
+            raise ExecutionError(f"{context} slot {slot} heads/head dim do not match")
+        if expected is not None and key.dtype != expected:
+            raise ExecutionError(f"{context} slot {slot} dtype must be {expected}")
+
+
+def _bind_symbol(dimension: SymbolicDim, actual: int, symbols: dict[str, int], context: str, index: int) -> None:
+    existing = symbols.get(dimension.name)
+    if existing is not None and existing != actual:
+        raise ExecutionError(
+            f"{context} dim {index} breaks symbol {dimension.name}: bound to {existing}, got {actual}"
+        )
+    lower, upper = _parse_bounds(dimension.bounds)
+    if lower is not None and actual < lower:
+        raise ExecutionError(f"{context} dim {index}: {dimension.name}={actual} below {lower}")
+    if upper is not None and actual > upper:
+        raise ExecutionError(f"{context} dim {index}: {dimension.name}={actual} above {upper}")
+    symbols[dimension.name] = actual
+
+
+def _parse_bounds(bounds: str | None) -> tuple[int | None, int | None]:
+    if not bounds:
+        return None, None
+    match = re.fullmatch(r"VR\[(-?\d+),\s*(-?\d+|int_oo)\]", bounds)
+    if match is None:
+        return None, None
+    return int(match.group(1)), None if match.group(2) == "int_oo" else int(match.group(2))
