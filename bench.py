@@ -143,6 +143,57 @@ def bench_decode_attention(steps: int, warmup: int, split_tokens: int) -> dict:
     }
 
 
+MODEL_BATCH, PROMPT, CAPACITY, DECODE_STEPS = 8, 512, 2048, 128
+
+
+def bench_decode_tokens(seed: int = 5) -> dict:
+    """Config 5: 24-layer Qwen2-0.5B-shape CausalLM (bf16, random init, tied
+    embeddings), stateful prefill of 512 random tokens at batch 8 into a KV
+    state of capacity 2048, then 128 greedy decode steps on the same buffers.
+    The decode step (all 24 layers + LM head + argmax) is one HIP-graph replay
+    of the fully lowered KernelIR function."""
+
+    from oracle.qwen2_model import causal_mask  # only builds the input mask
+    from stateful_llm_compiler_hip.qwen2 import Qwen2Config, init_weights
+    from stateful_llm_compiler_hip.runtime import Qwen2Runtime
+
+    device = torch.device("cuda:0")
+    config = Qwen2Config()
+    weights = init_weights(config, seed=seed, dtype=torch.bfloat16, device=device, draw_on_device=True)
+    runtime = Qwen2Runtime(config, weights, capacity=CAPACITY, dtype=torch.bfloat16,
+                           device="cuda:0", validate=False)
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    ids = torch.randint(0, config.vocab_size, (MODEL_BATCH, PROMPT), generator=g).to(device)
+    mask = causal_mask(MODEL_BATCH, PROMPT).to(device)
+    pos = torch.arange(PROMPT, device=device).view(1, -1).expand(MODEL_BATCH, -1).contiguous()
+
+    runtime.prefill(ids, mask, pos)  # warm-up (kernel loading, allocator)
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    logits, state = runtime.prefill(ids, mask, pos)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - start
+
+    decoder = runtime.graph_decoder(state, logits[:, -1].argmax(-1))
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(DECODE_STEPS):
+        decoder.step()
+    torch.cuda.synchronize()
+    decode_s = time.perf_counter() - start
+    lengths = state.lengths[0].tolist()
+    state.check_capacity()
+    return {
+        "decode_tok_s": MODEL_BATCH * DECODE_STEPS / decode_s,
+        "decode_ms_per_step": decode_s * 1e3 / DECODE_STEPS,
+        "prefill_tok_s": MODEL_BATCH * PROMPT / prefill_s,
+        "prefill_ms": prefill_s * 1e3,
+        "final_lengths": sorted(set(lengths)),
+        "decode_ops_per_step": len(runtime.decode_result.module.functions[0].block.operations),
+        "coverage": runtime.decode_result.coverage.coverage,
+    }
+
+
 def main() -> None:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -150,6 +201,7 @@ def main() -> None:
     parser.add_argument("--warmup", type=int, default=50)
     parser.add_argument("--split-tokens", type=int, default=0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-model", action="store_true", help="skip the decode tok/s leg")
     args = parser.parse_args()
     if args.gpus != 1:
         print(
@@ -194,6 +246,18 @@ def main() -> None:
             "algorithmic_bytes": result["bytes"],
         },
     }
+    if not args.no_model:
+        tok = bench_decode_tokens()
+        line["decode_tok_s"] = round(tok["decode_tok_s"], 1)
+        line["decode"] = {
+            "workload": "24-layer Qwen2-0.5B-shape CausalLM bf16 random init, batch 8, prefill 512 into capacity 2048, 128 greedy steps, fast mode, full lowering, HIP-graph decode step",
+            "ms_per_step": round(tok["decode_ms_per_step"], 4),
+            "prefill_tok_s": round(tok["prefill_tok_s"], 1),
+            "prefill_ms": round(tok["prefill_ms"], 2),
+            "ops_per_step": tok["decode_ops_per_step"],
+            "lowering_coverage": tok["coverage"],
+            "final_lengths": tok["final_lengths"],
+        }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line))

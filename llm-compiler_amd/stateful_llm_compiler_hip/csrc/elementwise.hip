@@ -141,22 +141,58 @@ __global__ void kv_advance_kernel(const int64_t* __restrict__ in, int64_t* __res
   if (overflow != nullptr && (next > capacity || next < 0)) *overflow = 1;
 }
 
-// One workgroup per row: (max, first index) reduction; ties keep the lowest
-// index, as torch.argmax does.
+// One 1024-thread workgroup per row: 16-byte vector loads, four in flight per
+// thread, then a (max, first index) reduction.  NaN ranks above every number
+// and ties keep the lowest index, as torch.argmax does.
+__device__ __forceinline__ bool argmax_better(float v, int64_t i, float best, int64_t best_i) {
+  const bool v_nan = v != v, b_nan = best != best;
+  if (v_nan != b_nan) return v_nan;
+  if (!v_nan && v != best) return v > best;
+  return i < best_i;
+}
+
 template <typename T>
-__global__ __launch_bounds__(256) void argmax_kernel(const T* __restrict__ logits,
-                                                     int64_t* __restrict__ out, int64_t cols,
-                                                     int64_t row_stride) {
-  __shared__ float sv[4];
-  __shared__ int64_t si[4];
+__global__ __launch_bounds__(1024) void argmax_kernel(const T* __restrict__ logits,
+                                                      int64_t* __restrict__ out, int64_t cols,
+                                                      int64_t row_stride, int vector_ok) {
+  __shared__ float sv[16];
+  __shared__ int64_t si[16];
+  constexpr int VEC = 16 / sizeof(T);
   const int64_t r = blockIdx.x;
   const T* row = logits + r * row_stride;
   float best = -INFINITY;
-  int64_t best_i = cols;  // sentinel: larger than every index
-  for (int64_t i = threadIdx.x; i < cols; i += 256) {
+  int64_t best_i = INT64_MAX;
+  int64_t done = 0;
+  if (vector_ok) {
+    const int64_t nvec = cols / VEC;
+    const uint4* vrow = reinterpret_cast<const uint4*>(row);
+    for (int64_t base = threadIdx.x; base < nvec; base += 4 * 1024) {
+      uint4 raw[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t j = base + u * 1024;
+        raw[u] = j < nvec ? vrow[j] : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t j = base + u * 1024;
+        if (j >= nvec) break;
+        const T* e = reinterpret_cast<const T*>(&raw[u]);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+          const float v = slc::to_f32(e[k]);
+          if (argmax_better(v, j * VEC + k, best, best_i)) {
+            best = v;
+            best_i = j * VEC + k;
+          }
+        }
+      }
+    }
+    done = nvec * VEC;
+  }
+  for (int64_t i = done + threadIdx.x; i < cols; i += 1024) {
     const float v = slc::to_f32(row[i]);
-    // NaN compares as the maximum, like torch.argmax.
-    if (v > best || (v != v && best == best)) {
+    if (argmax_better(v, i, best, best_i)) {
       best = v;
       best_i = i;
     }
@@ -164,9 +200,7 @@ __global__ __launch_bounds__(256) void argmax_kernel(const T* __restrict__ logit
   for (int off = 32; off > 0; off >>= 1) {
     const float ov = __shfl_xor(best, off, 64);
     const int64_t oi = __shfl_xor(best_i, off, 64);
-    const bool take = (ov > best) || (ov != ov && best == best) ||
-                      ((ov == best || (ov != ov && best != best)) && oi < best_i);
-    if (take) {
+    if (argmax_better(ov, oi, best, best_i)) {
       best = ov;
       best_i = oi;
     }
@@ -177,14 +211,10 @@ __global__ __launch_bounds__(256) void argmax_kernel(const T* __restrict__ logit
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < 4; ++w) {
-      const float ov = sv[w];
-      const int64_t oi = si[w];
-      const bool take = (ov > best) || (ov != ov && best == best) ||
-                        ((ov == best || (ov != ov && best != best)) && oi < best_i);
-      if (take) {
-        best = ov;
-        best_i = oi;
+    for (int w = 1; w < 16; ++w) {
+      if (argmax_better(sv[w], si[w], best, best_i)) {
+        best = sv[w];
+        best_i = si[w];
       }
     }
     out[r] = best_i < cols ? best_i : 0;
@@ -326,18 +356,20 @@ extern "C" int slc_hip_argmax(const void* logits, int64_t* output, int dtype, in
   SLC_REQUIRE(logits && output, "slc_hip_argmax: null pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(rows));
+  const int64_t es = slc_host::dtype_size(dtype);
+  const int vector_ok = (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (row_stride * es) % 16 == 0;
   switch (dtype) {
     case SLC_BF16:
-      hipLaunchKernelGGL((argmax_kernel<slc::bf16_t>), grid, dim3(256), 0, s,
-                         static_cast<const slc::bf16_t*>(logits), output, cols, row_stride);
+      hipLaunchKernelGGL((argmax_kernel<slc::bf16_t>), grid, dim3(1024), 0, s,
+                         static_cast<const slc::bf16_t*>(logits), output, cols, row_stride, vector_ok);
       break;
     case SLC_F16:
-      hipLaunchKernelGGL((argmax_kernel<slc::f16_t>), grid, dim3(256), 0, s,
-                         static_cast<const slc::f16_t*>(logits), output, cols, row_stride);
+      hipLaunchKernelGGL((argmax_kernel<slc::f16_t>), grid, dim3(1024), 0, s,
+                         static_cast<const slc::f16_t*>(logits), output, cols, row_stride, vector_ok);
       break;
     default:
-      hipLaunchKernelGGL((argmax_kernel<float>), grid, dim3(256), 0, s,
-                         static_cast<const float*>(logits), output, cols, row_stride);
+      hipLaunchKernelGGL((argmax_kernel<float>), grid, dim3(1024), 0, s,
+                         static_cast<const float*>(logits), output, cols, row_stride, vector_ok);
   }
   return slc_host::check_launch("slc_hip_argmax");
 }

@@ -14,9 +14,9 @@
 //    chunks so the 16-row MFMA operand reads (ds_read_b128) are free of bank
 //    conflicts.  Two LDS buffers: tile k+1 is fetched into registers while
 //    tile k is multiplied.
-//  * The tile shape follows M: decode-sized M (<= 64) streams W with narrow
-//    M tiles and many workgroups along N (HBM-bound), prefill-sized M uses
-//    128 x 128 tiles (MFMA-bound).
+//  * Decode-sized M (<= 64) takes a dedicated weight-streaming kernel (split-K
+//    across the waves of a workgroup, see linear_skinny_kernel); prefill-sized
+//    M uses 128 x 128 tiles (MFMA-bound).
 // fp32 (and shapes the vector path cannot take) use a classic LDS-tiled
 // FMA kernel.
 #include "common.hpp"
@@ -191,6 +191,115 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(
   }
 }
 
+
+// Decode-sized M (<= 64): Y is a handful of rows, W streams from HBM once.
+// One workgroup owns 16 output features and all M rows; its KW waves split K
+// between them (partial sums meet in LDS at the end), so even a 896-wide
+// projection launches N/16 workgroups x KW waves.  Operands are loaded
+// straight into MFMA registers -- lane (row c, k-slice g) takes 16 bytes of
+// one W row per k-step -- U k-steps per batch, the next batch in flight while
+// the current one is multiplied.
+template <typename T, int MB, int KW, int U>
+__global__ __launch_bounds__(KW * 64) void linear_skinny_kernel(
+    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
+    T* __restrict__ y, int M, int N, int K, int64_t x_rs, int64_t y_rs) {
+  using MF = Mfma<T>;
+  __shared__ float partial[KW][MB][64][4];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+
+  const int steps = (K + 31) / 32;               // 32-wide MFMA k-steps
+  const int per_wave = (steps + KW - 1) / KW;
+  const int s_begin = wave * per_wave;
+  const int s_end = min(s_begin + per_wave, steps);
+
+  const int w_rows = min(16, N - n0);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w + static_cast<int64_t>(n0) * K,
+                                              static_cast<int64_t>(w_rows) * K * 2);
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(x, (static_cast<int64_t>(M) - 1) * x_rs * 2 + static_cast<int64_t>(K) * 2);
+  // Per-lane byte offsets of k-step 0; rows past N / M read zero.
+  const int w_off = c * K * 2 + g * 16;
+  int x_off[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) x_off[i] = static_cast<int>((i * 16 + c) * x_rs * 2) + g * 16;
+
+  f32x4_t acc[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  uint4 wa[U], xa[U][MB], wb[U], xb[U][MB];
+  auto fetch = [&](int s0, uint4 (&wr)[U], uint4 (&xr)[U][MB]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = s0 + u;
+      const int k = s * 32 + g * 8;
+      // k past K (or past this wave's range) contributes zeros; within a row
+      // the buffer range check cannot see the end, so this lane test does.
+      const bool ok = s < s_end && k < K;
+      wr[u] = ok ? buffer_load16(rw, w_off + s * 64) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+        xr[u][i] = ok ? buffer_load16(rx, x_off[i] + s * 64) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto multiply = [&](const uint4 (&wr)[U], const uint4 (&xr)[U][MB]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const auto b = __builtin_bit_cast(typename MF::vec, wr[u]);
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+        acc[i] = MF::run(__builtin_bit_cast(typename MF::vec, xr[u][i]), b, acc[i]);
+    }
+  };
+
+  int s0 = s_begin;
+  fetch(s0, wa, xa);
+  while (s0 < s_end) {
+    fetch(s0 + U, wb, xb);
+    multiply(wa, xa);
+    s0 += U;
+    if (s0 >= s_end) break;
+    fetch(s0 + U, wa, xa);
+    multiply(wb, xb);
+    s0 += U;
+  }
+
+  // C layout: lane (col c = feature, rows 4g..4g+3 = batch rows of block i).
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) partial[wave][i][lane][r] = acc[i][r];
+  __syncthreads();
+  for (int idx = tid; idx < MB * 64 * 4; idx += KW * 64) {
+    const int i = idx / 256, l = (idx / 4) % 64, r = idx % 4;
+    float sum = 0.0f;
+#pragma unroll
+    for (int v = 0; v < KW; ++v) sum += partial[v][i][l][r];
+    const int n = n0 + (l & 15);
+    const int m = i * 16 + 4 * (l >> 4) + r;
+    if (n < N && m < M) {
+      if (bias != nullptr) sum += slc::to_f32(bias[n]);
+      y[m * y_rs + n] = slc::from_f32<T>(sum);
+    }
+  }
+}
+
+template <typename T, int MB>
+int launch_skinny(const void* x, const void* w, const void* bias, void* y, int M, int N,
+                  int K, int64_t x_rs, int64_t y_rs, hipStream_t stream) {
+  // k-steps per prefetch batch: as deep as the registers allow.
+  constexpr int KW = 8, U = MB == 1 ? 8 : (MB == 2 ? 4 : 2);
+  hipLaunchKernelGGL((linear_skinny_kernel<T, MB, KW, U>), dim3((N + 15) / 16), dim3(KW * 64), 0,
+                     stream, static_cast<const T*>(x), static_cast<const T*>(w),
+                     static_cast<const T*>(bias), static_cast<T*>(y), M, N, K, x_rs, y_rs);
+  return slc_host::check_launch("slc_hip_linear(skinny)");
+}
+
 // Classic 16 x 16 LDS-tiled FMA GEMM for fp32 and unaligned shapes.
 template <typename T>
 __global__ __launch_bounds__(256) void linear_generic_kernel(
@@ -233,9 +342,9 @@ int launch_mfma(const void* x, const void* w, const void* bias, void* y, int M,
 template <typename T>
 int dispatch_mfma(const void* x, const void* w, const void* bias, void* y, int M,
                   int N, int K, int64_t x_rs, int64_t y_rs, hipStream_t s) {
-  if (M <= 16) return launch_mfma<T, 16, 64, 1, 4>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
-  if (M <= 32) return launch_mfma<T, 32, 64, 2, 2>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
-  if (M <= 64) return launch_mfma<T, 64, 64, 2, 2>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
+  if (M <= 16) return launch_skinny<T, 1>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
+  if (M <= 32) return launch_skinny<T, 2>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
+  if (M <= 64) return launch_skinny<T, 4>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
   return launch_mfma<T, 128, 128, 2, 2>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
 }
 

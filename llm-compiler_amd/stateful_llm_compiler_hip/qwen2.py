@@ -105,12 +105,17 @@ def init_weights(
     dtype: torch.dtype = torch.bfloat16,
     device: torch.device | str = "cpu",
     std: float = 0.02,
+    draw_on_device: bool = False,
 ) -> dict[str, torch.Tensor]:
     """Seeded random weights: projections, biases and embeddings N(0, std),
     norm weights 1 + N(0, std).  Generated in fp32 on the CPU, then cast and
     moved, so every device and dtype sees the same draw."""
 
-    g = torch.Generator(device="cpu").manual_seed(seed)
+    # Drawn on the CPU by default so every device sees the same values; a
+    # CUDA ``device`` with ``draw_on_device=True`` draws there instead (much
+    # faster for the 0.5B-parameter model, reproducible on that device).
+    draw = torch.device(device) if draw_on_device else torch.device("cpu")
+    g = torch.Generator(device=draw).manual_seed(seed)
     H, I, V = config.hidden_size, config.intermediate_size, config.vocab_size
     kv = config.num_kv_heads * config.head_dim
     shapes: dict[str, tuple[int, ...]] = {"embed_tokens.weight": (V, H)}
@@ -131,10 +136,11 @@ def init_weights(
         shapes["lm_head.weight"] = (V, H)
     weights: dict[str, torch.Tensor] = {}
     for name, shape in shapes.items():
-        t = torch.randn(*shape, generator=g) * std
+        t = torch.randn(*shape, generator=g, device=draw) * std
         if name.endswith("norm.weight"):
             t = t + 1.0
         weights[name] = t.to(dtype).to(device)
+        del t
     weights["rotary_emb.inv_freq"] = inverse_frequency(config, device)
     return weights
 
