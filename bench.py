@@ -87,6 +87,44 @@ def cpu_baseline(seconds_budget: float = 20.0) -> dict:
     }
 
 
+TRAFFIC_PROFILE = ROOT / "profiles" / "decode_attention_b32_l8192.md"
+
+
+def profiled_traffic() -> int | None:
+    """HBM bytes per launch of the dominant kernel, from the committed
+    FETCH_SIZE/WRITE_SIZE counter runs (calibrated against a plain copy)."""
+
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def dominant_kernel_us(call, reps: int) -> float:
+    """Mean duration of the dominant kernel of ``call()`` over ``reps`` eager
+    calls, from HIP events the library records around that kernel."""
+
+    from stateful_llm_compiler_hip import _native
+
+    lib = _native.library()
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for b, e in pairs:  # creates the underlying hipEvent_t handles
+        b.record()
+        e.record()
+    torch.cuda.synchronize()
+    try:
+        for b, e in pairs:
+            lib.slc_hip_set_timing_events(b.cuda_event, e.cuda_event)
+            call()
+    finally:
+        lib.slc_hip_set_timing_events(None, None)
+    torch.cuda.synchronize()
+    return 1e3 * sum(b.elapsed_time(e) for b, e in pairs) / reps
+
+
 def bench_decode_attention(steps: int, warmup: int, split_tokens: int) -> dict:
     from stateful_llm_compiler_hip.backends import hip_decode_attention
 
@@ -116,15 +154,19 @@ def bench_decode_attention(steps: int, warmup: int, split_tokens: int) -> dict:
         graph.replay()
     torch.cuda.synchronize()
 
-    # Per-launch durations with events on the replay stream.
+    # Per-step durations of the whole graph (split + merge kernels) with
+    # events on the replay stream.
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(min(steps, 200))]
     for s, e in events:
         s.record()
         graph.replay()
         e.record()
     torch.cuda.synchronize()
-    durations_ms = [s.elapsed_time(e) for s, e in events]
-    kernel_us = 1e3 * sum(durations_ms) / len(durations_ms)
+    step_us = 1e3 * sum(s.elapsed_time(e) for s, e in events) / len(events)
+
+    # Duration of the dominant (split-sequence) kernel alone: the library
+    # records the armed events right before and after it on the launch stream.
+    kernel_us = dominant_kernel_us(step, len(events))
 
     torch.cuda.synchronize()
     start = time.perf_counter()
@@ -138,6 +180,7 @@ def bench_decode_attention(steps: int, warmup: int, split_tokens: int) -> dict:
         "elapsed": elapsed,
         "bytes": nbytes,
         "kernel_us": kernel_us,
+        "step_us": step_us,
         "achieved_gbs": achieved,
         "tokens": int(lengths.sum().item()),
     }
@@ -202,6 +245,10 @@ def main() -> None:
     parser.add_argument("--split-tokens", type=int, default=0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-model", action="store_true", help="skip the decode tok/s leg")
+    parser.add_argument(
+        "--calibrate-copy", type=int, default=0, metavar="MIB",
+        help="only run 5 plain device-to-device copies of MIB MiB (counter calibration)",
+    )
     args = parser.parse_args()
     if args.gpus != 1:
         print(
@@ -213,6 +260,14 @@ def main() -> None:
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X (torch.cuda.is_available() is False)", file=sys.stderr)
         sys.exit(2)
+    if args.calibrate_copy:
+        src = torch.ones(args.calibrate_copy << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration_copy_bytes": src.numel()}))
+        return
 
     result = bench_decode_attention(args.steps, args.warmup, args.split_tokens)
     value = result["bytes"] * args.steps / result["elapsed"] / 1e9
@@ -241,8 +296,10 @@ def main() -> None:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(result["achieved_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(),
+            "kernel": "decode_attention_mfma_kernel (split-sequence); merge kernel separate",
             "kernel_us": round(result["kernel_us"], 3),
+            "step_us_graph": round(result["step_us"], 3),
             "algorithmic_bytes": result["bytes"],
         },
     }

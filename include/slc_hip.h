@@ -61,6 +61,15 @@ SLC_API int slc_hip_version(void);
 SLC_API const char* slc_hip_last_error(void);
 
 /*
+ * Measurement hook (no counterpart in the reference, which times whole calls
+ * with torch events): arm two hipEvent_t handles for the calling thread; each
+ * later entry point with a multi-kernel launch sequence records `begin` just
+ * before and `end` just after its dominant kernel on the launch stream, so a
+ * benchmark can time that kernel alone.  Pass (NULL, NULL) to disarm.
+ */
+SLC_API void slc_hip_set_timing_events(void* begin, void* end);
+
+/*
  * kv_store: scatter the current step's K/V rows into the preallocated
  * B x capacity x H x D buffers.
  *   key_buffer/value_buffer : [batch, capacity, heads, head_dim], contiguous

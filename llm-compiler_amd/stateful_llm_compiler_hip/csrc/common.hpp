@@ -100,6 +100,12 @@ namespace slc_host {
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
 
+// Measurement hook: when the caller armed a pair of events on this thread
+// (slc_hip_set_timing_events), the entry point brackets its dominant kernel
+// with them on the launch stream.  Both are no-ops otherwise.
+void mark_kernel_begin(hipStream_t stream);
+void mark_kernel_end(hipStream_t stream);
+
 inline int dtype_size(int dtype) {
   switch (dtype) {
     case SLC_F32:

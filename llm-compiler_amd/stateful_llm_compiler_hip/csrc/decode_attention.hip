@@ -579,6 +579,7 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
   const int groups = static_cast<int>(q_heads / kv_heads);
   const dim3 grid(static_cast<unsigned>(nchunks), static_cast<unsigned>(kv_heads),
                   static_cast<unsigned>(batch));
+  slc_host::mark_kernel_begin(stream);
 #define SLC_MFMA(MK)                                                          \
   hipLaunchKernelGGL((decode_attention_mfma_kernel<T, D, MK>), grid, dim3(kThreads), \
                      0, stream, static_cast<const T*>(query),                 \
@@ -600,6 +601,7 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
     SLC_MFMA(SLC_F32 + 1);
   }
 #undef SLC_MFMA
+  slc_host::mark_kernel_end(stream);
   int rc = slc_host::check_launch("slc_hip_decode_attention");
   if (rc != SLC_OK || nchunks == 1) return rc;
   hipLaunchKernelGGL((decode_attention_merge_kernel<T, D>),

@@ -6,6 +6,8 @@
 
 namespace {
 thread_local char g_last_error[512] = "";
+thread_local hipEvent_t g_begin = nullptr;
+thread_local hipEvent_t g_end = nullptr;
 }
 
 namespace slc_host {
@@ -27,8 +29,21 @@ int check_launch(const char* what) {
   return SLC_OK;
 }
 
+void mark_kernel_begin(hipStream_t stream) {
+  if (g_begin != nullptr) hipEventRecord(g_begin, stream);
+}
+
+void mark_kernel_end(hipStream_t stream) {
+  if (g_end != nullptr) hipEventRecord(g_end, stream);
+}
+
 }  // namespace slc_host
 
 extern "C" int slc_hip_version(void) { return 100; }
 
 extern "C" const char* slc_hip_last_error(void) { return g_last_error; }
+
+extern "C" void slc_hip_set_timing_events(void* begin, void* end) {
+  g_begin = static_cast<hipEvent_t>(begin);
+  g_end = static_cast<hipEvent_t>(end);
+}
