@@ -159,14 +159,13 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   const int end = static_cast<int>(end64);  // host guarantees capacity < 2^30
   const int chunk_start = chunk * chunk_tokens;
   if (nchunks > 1 && chunk_start >= end) {
-    // Nothing of this batch in the chunk.  An empty sequence has no partial to
-    // merge, so chunk 0 writes its result (0/0 = NaN, like the reference's
-    // softmax over an all -inf row).
-    if (chunk == 0 && end == 0) {
-      for (int idx = tid; idx < groups * D; idx += kThreads) {
-        const int qh = kvh * groups + idx / D;
-        output[b * o_sb + qh * o_sh + idx % D] = slc::from_f32<T>(0.0f / 0.0f);
-      }
+    // Nothing of this batch in the chunk: an empty partial (max -inf, sum 0),
+    // which the merge weighs by zero.  A sequence with no token at all thus
+    // merges to 0/0 = NaN, like the reference's softmax over an all -inf row.
+    if (tid < groups) {
+      const int64_t p = (b * q_heads + kvh * groups + tid) * nchunks + chunk;
+      part_ml[2 * p] = -INFINITY;
+      part_ml[2 * p + 1] = 0.0f;
     }
     return;
   }
@@ -390,45 +389,45 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
 }
 
 // Merge the split-sequence partials: one workgroup per (batch, kv-head).
-// Per-chunk weights exp2(m_i - M) / L go to LDS first; each output element is
-// then an independent weighted sum over the chunks.
+// Two rounds of independent loads and no length read: every chunk wrote a
+// partial (an empty chunk writes max -inf, sum 0).  Round 1 loads every
+// (head, chunk) (max, sum) pair at once into LDS; one thread per head turns
+// them into weights; round 2 loads each output's values of the chunks with a
+// non-zero weight, kMergeUnroll at a time.
+constexpr int kMergeUnroll = 8;
 template <typename T, int D>
 __global__ __launch_bounds__(256) void decode_attention_merge_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
-    const void* __restrict__ lengths, int lengths_dtype, T* __restrict__ output,
-    int q_heads, int kv_heads, int groups, int64_t capacity, int64_t mask_len,
-    int64_t o_sb, int64_t o_sh, int chunk_tokens, int nchunks) {
+    T* __restrict__ output, int q_heads, int kv_heads, int groups, int64_t o_sb,
+    int64_t o_sh, int nchunks) {
   __shared__ float sm_w[kMaxGroups * kMaxChunks];
+  __shared__ float sm_l[kMaxGroups * kMaxChunks];
   __shared__ float sm_inv[kMaxGroups];
   const int kvh = blockIdx.x % kv_heads;
   const int64_t b = blockIdx.x / kv_heads;
   const int tid = threadIdx.x;
-  int64_t end = slc::load_length(lengths, b, lengths_dtype);
-  end = end < 0 ? 0 : end;
-  end = end < mask_len ? end : mask_len;
-  end = end < capacity ? end : capacity;
-  if (end == 0) return;  // written (NaN) by the split kernel's chunk 0
-  const int nvalid = static_cast<int>((end + chunk_tokens - 1) / chunk_tokens);
   const int64_t head0 = b * q_heads + kvh * groups;
-  for (int idx = tid; idx < groups * nvalid; idx += 256) {
-    const int head = idx / nvalid;
-    const int i = idx % nvalid;
-    sm_w[head * kMaxChunks + i] = part_ml[2 * ((head0 + head) * nchunks + i)];
+  for (int idx = tid; idx < groups * nchunks; idx += 256) {
+    const int head = idx / nchunks;
+    const int i = idx % nchunks;
+    const int64_t p = (head0 + head) * nchunks + i;
+    sm_w[head * kMaxChunks + i] = part_ml[2 * p];
+    sm_l[head * kMaxChunks + i] = part_ml[2 * p + 1];
   }
   __syncthreads();
   if (tid < groups) {
-    const int head = tid;
-    const int64_t base = (head0 + head) * nchunks;
+    float* w = sm_w + tid * kMaxChunks;
+    const float* l = sm_l + tid * kMaxChunks;
     float mmax = -INFINITY;
-    for (int i = 0; i < nvalid; ++i) mmax = fmaxf(mmax, sm_w[head * kMaxChunks + i]);
+    for (int i = 0; i < nchunks; ++i) mmax = fmaxf(mmax, w[i]);
     const float mu = mmax == -INFINITY ? 0.0f : mmax;
     float lsum = 0.0f;
-    for (int i = 0; i < nvalid; ++i) {
-      const float f = fast_exp2(sm_w[head * kMaxChunks + i] - mu);
-      sm_w[head * kMaxChunks + i] = f;
-      lsum += f * part_ml[2 * (base + i) + 1];
+    for (int i = 0; i < nchunks; ++i) {
+      const float f = fast_exp2(w[i] - mu);  // exp2(-inf) = 0 for empty chunks
+      w[i] = f;
+      lsum += f * l[i];
     }
-    sm_inv[head] = 1.0f / lsum;
+    sm_inv[tid] = 1.0f / lsum;
   }
   __syncthreads();
   for (int idx = tid; idx < groups * D; idx += 256) {
@@ -436,18 +435,20 @@ __global__ __launch_bounds__(256) void decode_attention_merge_kernel(
     const int d = idx % D;
     const float* po = part_o + (head0 + head) * nchunks * D + d;
     const float* w = sm_w + head * kMaxChunks;
-    float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
-    int i = 0;
-    for (; i + 4 <= nvalid; i += 4) {
-      o0 += w[i] * po[(i + 0) * D];
-      o1 += w[i + 1] * po[(i + 1) * D];
-      o2 += w[i + 2] * po[(i + 2) * D];
-      o3 += w[i + 3] * po[(i + 3) * D];
+    float acc = 0.0f;
+    for (int i0 = 0; i0 < nchunks; i0 += kMergeUnroll) {
+      float v[kMergeUnroll];
+#pragma unroll
+      for (int k = 0; k < kMergeUnroll; ++k) {
+        const int i = i0 + k;
+        v[k] = i < nchunks && w[i] != 0.0f ? po[i * D] : 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < kMergeUnroll; ++k)
+        if (i0 + k < nchunks) acc += w[i0 + k] * v[k];
     }
-    for (; i < nvalid; ++i) o0 += w[i] * po[i * D];
     const int qh = kvh * groups + head;
-    output[b * o_sb + qh * o_sh + d] =
-        slc::from_f32<T>(((o0 + o1) + (o2 + o3)) * sm_inv[head]);
+    output[b * o_sb + qh * o_sh + d] = slc::from_f32<T>(acc * sm_inv[head]);
   }
 }
 
@@ -606,11 +607,9 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
   if (rc != SLC_OK || nchunks == 1) return rc;
   hipLaunchKernelGGL((decode_attention_merge_kernel<T, D>),
                      dim3(static_cast<unsigned>(batch * kv_heads)), dim3(256), 0,
-                     stream, part_o, part_ml, lengths, lengths_dtype,
-                     static_cast<T*>(output), static_cast<int>(q_heads),
-                     static_cast<int>(kv_heads), groups, capacity, mask_len,
-                     st[7], st[8], static_cast<int>(chunk),
-                     static_cast<int>(nchunks));
+                     stream, part_o, part_ml, static_cast<T*>(output),
+                     static_cast<int>(q_heads), static_cast<int>(kv_heads), groups,
+                     st[7], st[8], static_cast<int>(nchunks));
   return slc_host::check_launch("slc_hip_decode_attention(merge)");
 }
 

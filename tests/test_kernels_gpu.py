@@ -103,6 +103,7 @@ def _decode_case(
     layout="bshd",
     length_dtype=torch.int64,
     split_tokens=0,
+    mask_dtype=None,
 ):
     from stateful_llm_compiler_hip.backends import hip_decode_attention
 
@@ -111,10 +112,11 @@ def _decode_case(
     query = torch.randn(batch, q_heads, 1, head_dim, generator=g).to(dtype)
     key_buffer = torch.randn(batch, capacity, kv_heads, head_dim, generator=g).to(dtype)
     value_buffer = torch.randn(batch, capacity, kv_heads, head_dim, generator=g).to(dtype)
+    mask_dtype = dtype if mask_dtype is None else mask_dtype
     if mask_kind == "zeros":
-        mask = torch.zeros(batch, 1, 1, mask_len, dtype=dtype)
+        mask = torch.zeros(batch, 1, 1, mask_len, dtype=mask_dtype)
     else:
-        mask = (torch.randn(batch, 1, 1, mask_len, generator=g) * 2.0).to(dtype)
+        mask = (torch.randn(batch, 1, 1, mask_len, generator=g) * 2.0).to(mask_dtype)
     lengths_t = torch.tensor(lengths, dtype=torch.int64)
     expected = ref.decode_attention(
         query,
@@ -187,6 +189,19 @@ def test_decode_attention_forced_split(gpu, split):
     announce(f"decode bf16 split_tokens={split}")
     actual, expected = _decode_case(
         gpu, 3, 14, 2, 64, 2048, [2048, 1, 1500], torch.bfloat16, 31, split_tokens=split, mask_kind="random",
+    )
+    assert_bf16_close(actual, expected)
+
+
+@pytest.mark.parametrize("mask_dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("mask_len", [1000, 1001])
+def test_decode_attention_mask_dtype_and_length(gpu, mask_dtype, mask_len):
+    # A mask length that is a multiple of 4 takes the MFMA kernel (the mask is
+    # staged 4 tokens at a time); 1001 takes the generic kernel.
+    announce(f"decode bf16 mask {mask_dtype} mask_len={mask_len}")
+    actual, expected = _decode_case(
+        gpu, 4, 14, 2, 64, 1024, [1001, 999, 3, 640], torch.bfloat16, 43,
+        mask_len=mask_len, mask_kind="random", mask_dtype=mask_dtype,
     )
     assert_bf16_close(actual, expected)
 
