@@ -186,6 +186,113 @@ def bench_decode_attention(steps: int, warmup: int, split_tokens: int) -> dict:
     }
 
 
+MFMA_PEAK_TFLOPS = 2500.0  # dense bf16
+
+
+def _time_graph(fn, reps: int = 20, outer: int = 5) -> float:
+    """Mean microseconds per call of ``fn`` from replays of a HIP graph that
+    holds ``reps`` back-to-back calls (launch gaps included, host overhead
+    not)."""
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(outer):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return 1e3 * start.elapsed_time(end) / (reps * outer)
+
+
+def bench_kernels() -> dict:
+    """The other hot-path ops at their SURVEY config-3/4 shapes, each against
+    the roofline that bounds it (bf16; synthetic N(0,1) data)."""
+
+    from stateful_llm_compiler_hip.backends import (
+        hip_kv_store, hip_linear, hip_prefill_attention, hip_rms_norm, hip_rope,
+    )
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cuda:0").manual_seed(7)
+    bf = torch.bfloat16
+    out: dict[str, dict] = {}
+
+    def mfma(name, us, flops, shape):
+        tf = flops / (us * 1e-6) / 1e12
+        out[name] = {"shape": shape, "us": round(us, 2), "TFLOP/s": round(tf, 1),
+                     "frac_of_mfma_peak": round(tf / MFMA_PEAK_TFLOPS, 4)}
+
+    def hbm(name, us, nbytes, shape):
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"shape": shape, "us": round(us, 2), "GB/s": round(gbs, 1),
+                     "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+    # prefill attention, causal, config 4's largest case (B=8, T=4096)
+    B, T = 8, 4096
+    q = torch.randn(B, QH, T, D, device=dev, generator=g, dtype=bf)
+    k = torch.randn(B, KVH, T, D, device=dev, generator=g, dtype=bf)
+    v = torch.randn(B, KVH, T, D, device=dev, generator=g, dtype=bf)
+    flops = 4 * B * QH * D * T * (T + 1) // 2
+    us = _time_graph(lambda: hip_prefill_attention(q, k, v, None, scale=D**-0.5, causal=True), reps=5)
+    mfma("prefill_attention_causal", us, flops, "B8 QH14 KVH2 T4096 D64")
+    mask = torch.zeros(T, T, device=dev, dtype=bf).masked_fill(
+        torch.ones(T, T, device=dev, dtype=torch.bool).triu(1), float("-inf")).expand(B, 1, T, T)
+    us = _time_graph(lambda: hip_prefill_attention(q, k, v, mask, scale=D**-0.5), reps=5)
+    mfma("prefill_attention_mask", us, flops, "B8 QH14 KVH2 T4096 D64, explicit [B,1,T,T] causal mask")
+    del q, k, v, mask
+
+    # linear: the four projection shapes at M = 4096 and the MLP at M = 32768
+    for m, n, kk in ((4096, 896, 896), (4096, 128, 896), (4096, 4864, 896), (4096, 896, 4864),
+                     (32768, 4864, 896)):
+        x = torch.randn(m, kk, device=dev, generator=g, dtype=bf)
+        w = torch.randn(n, kk, device=dev, generator=g, dtype=bf) * 0.02
+        us = _time_graph(lambda: hip_linear(x, w), reps=10)
+        mfma(f"linear_m{m}_n{n}_k{kk}", us, 2 * m * n * kk, f"M{m} N{n} K{kk}")
+    # decode-shaped linears (M = 8): weight streaming
+    for n, kk in ((4864, 896), (896, 4864), (151936, 896)):
+        x = torch.randn(8, kk, device=dev, generator=g, dtype=bf)
+        w = torch.randn(n, kk, device=dev, generator=g, dtype=bf) * 0.02
+        us = _time_graph(lambda: hip_linear(x, w), reps=10)
+        hbm(f"linear_m8_n{n}_k{kk}", us, (n * kk + 8 * kk + 8 * n) * 2, f"M8 N{n} K{kk}")
+
+    # rms_norm 32768 x 896
+    x = torch.randn(32768, 896, device=dev, generator=g, dtype=bf)
+    wn = torch.randn(896, device=dev, generator=g, dtype=bf)
+    us = _time_graph(lambda: hip_rms_norm(x, wn, epsilon=1e-6, round_before_weight=True))
+    hbm("rms_norm", us, (2 * x.numel() + 896) * 2, "rows 32768 hidden 896")
+
+    # rope B=64 T=512
+    B, T = 64, 512
+    q = torch.randn(B, QH, T, D, device=dev, generator=g, dtype=bf)
+    k = torch.randn(B, KVH, T, D, device=dev, generator=g, dtype=bf)
+    cos = torch.randn(B, T, D, device=dev, generator=g, dtype=bf)
+    sin = torch.randn(B, T, D, device=dev, generator=g, dtype=bf)
+    us = _time_graph(lambda: hip_rope(q, k, cos, sin))
+    hbm("rope", us, (2 * (q.numel() + k.numel()) + 2 * B * T * D) * 2, "B64 QH14 KVH2 T512 D64")
+    del q, cos, sin
+
+    # kv_store B=64 T=512 into a [64, 8192, 2, 64] buffer pair
+    kb = torch.zeros(B, 8192, KVH, D, device=dev, dtype=bf)
+    vb = torch.zeros_like(kb)
+    vv = torch.randn(B, KVH, T, D, device=dev, generator=g, dtype=bf)
+    pos = torch.randint(0, 4096, (B,), device=dev, generator=g)
+    us = _time_graph(lambda: hip_kv_store(kb, vb, k, vv, pos))
+    hbm("kv_store", us, 2 * (k.numel() + vv.numel()) * 2 + B * 8, "B64 H2 T512 D64 -> cap 8192")
+    return out
+
+
 MODEL_BATCH, PROMPT, CAPACITY, DECODE_STEPS = 8, 512, 2048, 128
 
 
@@ -245,6 +352,7 @@ def main() -> None:
     parser.add_argument("--split-tokens", type=int, default=0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-model", action="store_true", help="skip the decode tok/s leg")
+    parser.add_argument("--no-kernels", action="store_true", help="skip the other-op roofline table")
     parser.add_argument(
         "--calibrate-copy", type=int, default=0, metavar="MIB",
         help="only run 5 plain device-to-device copies of MIB MiB (counter calibration)",
@@ -315,6 +423,8 @@ def main() -> None:
             "lowering_coverage": tok["coverage"],
             "final_lengths": tok["final_lengths"],
         }
+    if not args.no_kernels:
+        line["kernels"] = bench_kernels()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line))
