@@ -223,6 +223,55 @@ SLC_API int slc_hip_kv_advance(const int64_t* lengths_in, int64_t* lengths_out,
 SLC_API int slc_hip_argmax(const void* logits, int64_t* output, int dtype, int64_t rows,
                            int64_t cols, int64_t row_stride, void* stream);
 
+/*
+ * Fused decode-step ops (no single counterpart in the reference: each one
+ * replaces a short sequence of the reference's KernelIR ops, and produces
+ * bit-identically what that sequence of this library's kernels produces).
+ * rows <= 32 (decode-sized), dtype bf16 or fp16, 16-byte aligned rows; larger
+ * or other inputs are rejected with SLC_ERR_INVALID_ARGUMENT and the caller
+ * runs the unfused sequence.
+ *
+ *   norm_linear_group : y_j = linear(rms_norm(x, norm_weight), w_j, b_j) for
+ *                       count = 1..3 matrices [n_j, hidden] (Q/K/V); no norm
+ *                       when norm_weight is NULL.  Replaces
+ *                       kernel.triton.rms_norm (round_before_weight=1) plus
+ *                       one kernel.triton.linear per matrix
+ *                       (triton_rmsnorm.py:205-443, triton_linear.py:87-148).
+ *   norm_linear_swiglu: y = round(silu(round(x_n . w_gate^T))) *
+ *                       round(x_n . w_up^T), x_n = rms_norm(x, norm_weight)
+ *                       (the Qwen2 MLP front, qwen2.py:253-256).
+ *   linear_residual   : y = residual + round(x . w^T + bias) (O / down
+ *                       projection and the residual add, qwen2.py:288-294).
+ *   rope_kv_store     : q_out = rope(q); key_buffer[b, positions[b] + t] =
+ *                       rope(k)[b, :, t]; value_buffer[...] = v[b, :, t]; rows
+ *                       at or past the capacity are skipped and set *overflow
+ *                       (triton_rope.py:299-390 then triton_kv.py:71-129).
+ *                       Buffers are contiguous [B, capacity, kv_heads, D].
+ */
+SLC_API int slc_hip_norm_linear_group(
+    const void* x, int64_t x_rs, const void* norm_weight, float epsilon, int64_t rows,
+    int64_t hidden, int count, const void* w0, const void* b0, void* y0, int64_t n0,
+    int64_t y0_rs, const void* w1, const void* b1, void* y1, int64_t n1, int64_t y1_rs,
+    const void* w2, const void* b2, void* y2, int64_t n2, int64_t y2_rs, int dtype,
+    void* stream);
+SLC_API int slc_hip_norm_linear_swiglu(const void* x, int64_t x_rs, const void* norm_weight,
+                                       float epsilon, int64_t rows, int64_t hidden,
+                                       int64_t features, const void* w_gate, const void* w_up,
+                                       void* y, int64_t y_rs, int dtype, void* stream);
+SLC_API int slc_hip_linear_residual(const void* x, int64_t x_rs, int64_t rows,
+                                    int64_t in_features, int64_t out_features,
+                                    const void* weight, const void* bias,
+                                    const void* residual, int64_t residual_rs, void* y,
+                                    int64_t y_rs, int dtype, void* stream);
+SLC_API int slc_hip_rope_kv_store(
+    const void* query, const void* key, const void* value, const void* cosine,
+    const void* sine, void* query_out, void* key_buffer, void* value_buffer,
+    const int64_t* positions, int* overflow, int dtype, int64_t batch, int64_t q_heads,
+    int64_t kv_heads, int64_t tokens, int64_t head_dim, int64_t capacity, int64_t q_sb,
+    int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t v_sb,
+    int64_t v_sh, int64_t v_st, int64_t cos_sb, int64_t cos_st, int64_t sin_sb,
+    int64_t sin_st, int64_t qo_sb, int64_t qo_sh, int64_t qo_st, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

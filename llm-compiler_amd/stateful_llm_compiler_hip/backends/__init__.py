@@ -1,6 +1,12 @@
 """gfx950 kernel wrappers (drop-ins for the reference's backends/triton_*)."""
 
 from .hip_attention import hip_decode_attention
+from .hip_fused import (
+    hip_linear_residual,
+    hip_norm_linear_group,
+    hip_norm_linear_swiglu,
+    hip_rope_kv_store,
+)
 from .hip_kv import hip_kv_store
 from .hip_linear import hip_linear
 from .hip_ops import (
@@ -23,6 +29,10 @@ __all__ = [
     "hip_rope_table",
     "hip_swiglu",
     "hip_decode_attention",
+    "hip_linear_residual",
+    "hip_norm_linear_group",
+    "hip_norm_linear_swiglu",
+    "hip_rope_kv_store",
     "hip_kv_store",
     "hip_linear",
     "hip_prefill_attention",

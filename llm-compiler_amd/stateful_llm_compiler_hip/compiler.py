@@ -16,7 +16,7 @@ from .cost_model import RMSNormCostModel
 from .ir import Module
 from .lowering import LoweringCoverage, LowerToKernelIRPass, analyze_lowering_coverage, require_full_lowering
 from .pass_manager import PassManager, PassResult, operation_counts
-from .passes import SelectRMSNormLoweringPass
+from .passes import FuseDecodeKernelsPass, SelectRMSNormLoweringPass
 
 
 @dataclass(frozen=True)
@@ -25,6 +25,9 @@ class CompileOptions:
     require_full_lowering: bool = True
     rmsnorm_profile: str | Path | None = None
     rmsnorm_fallback: str = "hip"
+    # Fuse decode-step op chains into single kernels (fast mode only; the
+    # fused kernels are bit-identical to the chains they replace).
+    fuse: bool = True
 
 
 @dataclass
@@ -51,6 +54,8 @@ def compile_module(module: Module, options: CompileOptions | None = None) -> Com
         manager.add(SelectRMSNormLoweringPass(RMSNormCostModel.load(options.rmsnorm_profile),
                                               fallback=options.rmsnorm_fallback))
     manager.add(LowerToKernelIRPass(numerical_mode=options.numerical_mode))
+    if options.fuse and options.numerical_mode == "fast":
+        manager.add(FuseDecodeKernelsPass())
     results = manager.run(module)
     coverage = require_full_lowering(module) if options.require_full_lowering else analyze_lowering_coverage(module)
     return CompileResult(module, results, coverage, operation_counts(module))

@@ -1,0 +1,513 @@
+// Fused decode-step kernels (fast numerical mode, decode-sized row counts).
+//
+// A Qwen2 decode step spends most of its time in launch latency: every layer
+// is ~17 small kernels.  These kernels merge neighbours of the KernelIR op
+// graph without changing a single rounding step, so each is bit-identical to
+// the ops it replaces (the compiler's fusion pass swaps them in):
+//
+//  * norm_linear_group   rms_norm -> up to three linears reading its output
+//                        (Q/K/V).  Every workgroup normalises the <= 32 input
+//                        rows into LDS with the rms_norm kernel's own row
+//                        routine, then streams its 16 weight rows.
+//  * norm_linear_swiglu  rms_norm -> gate and up linears -> swiglu.  A
+//                        workgroup owns 16 features of both projections and
+//                        applies SwiGLU to the rounded results.
+//  * linear_residual     linear -> residual add (O and down projections).
+//  * rope_kv_store       rope -> kv_store of the rotated keys and the values;
+//                        the rotated queries are written out.
+//
+// The weight-streaming loop is the decode linear kernel's (linear.hip,
+// linear_skinny_kernel): the same K split over the same 8 waves, the same
+// MFMA order and the same partial-sum order, hence the same bits.
+// Semantics: src/stateful_llm_compiler/execution.py:674-692 (rms_norm),
+// triton_executor.py:159-176 (linear), :741-767 (rope), :743-781 (kv store).
+#include "common.hpp"
+#include "op_math.hpp"
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct Mfma;
+template <>
+struct Mfma<slc::bf16_t> {
+  using vec = bf16x8_t;
+  static __device__ __forceinline__ f32x4_t run(vec a, vec b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma<slc::f16_t> {
+  using vec = f16x8_t;
+  static __device__ __forceinline__ f32x4_t run(vec a, vec b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const uint64_t address = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(address));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(address >> 32));
+  void* uniform = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+  const int clamped = bytes > 0x7fffffff ? 0x7fffffff : static_cast<int>(bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(uniform, 0, __builtin_amdgcn_readfirstlane(clamped),
+                                           0x00020000);
+}
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int offset) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 0));
+}
+
+enum Epilogue { kStore = 0, kResidual = 1, kSwiglu = 2 };
+
+constexpr int kWaves = 8;        // K split of the decode linear kernel
+constexpr int kMaxRows = 32;     // rows (batch x tokens) the fused kernels take
+constexpr int kMaxMatrices = 3;
+
+struct FusedArgs {
+  const void* x;          // [rows, hidden] input (before the norm when norm_w)
+  int64_t x_rs;
+  const void* norm_w;     // [hidden] or null
+  float eps;
+  int rows, hidden;
+  const void* w[kMaxMatrices];     // [n_j, hidden] row-major
+  const void* bias[kMaxMatrices];  // [n_j] or null
+  void* y[kMaxMatrices];           // [rows, n_j] with row stride y_rs_j
+  int n[kMaxMatrices];
+  int64_t y_rs[kMaxMatrices];
+  int block_end[kMaxMatrices];     // cumulative 16-feature blocks
+  const void* residual;            // [rows, n_0] with row stride r_rs
+  int64_t r_rs;
+};
+
+// LDS row stride of the normalised input, in elements: 8 extra elements move
+// consecutive rows 4 banks apart, so the 16-row operand reads do not collide.
+__host__ __device__ constexpr int norm_row(int hidden) { return hidden + 8; }
+
+// NV: 16-byte vectors per lane of the norm prologue (0 = no norm, the input
+// rows are read from global memory like the decode linear kernel does).
+template <typename T, int MB, int U, int NV, int EPI>
+__global__ __launch_bounds__(kWaves * 64) void fused_rows_kernel(FusedArgs p) {
+  using MF = Mfma<T>;
+  constexpr int NW = EPI == kSwiglu ? 2 : 1;  // weight streams per workgroup
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int K = p.hidden;
+  const int M = p.rows;
+
+  // The matrix and feature block of this workgroup.
+  const int blk = blockIdx.x;
+  const int j = blk < p.block_end[0] ? 0 : (blk < p.block_end[1] ? 1 : 2);
+  const int n0 = (blk - (j == 0 ? 0 : p.block_end[j - 1])) * 16;
+  const int N = p.n[j];
+
+  const int xs_bytes = NV > 0 ? MB * 16 * norm_row(K) * 2 : 0;
+  unsigned char* xs = smem;
+  float* partial = reinterpret_cast<float*>(smem + xs_bytes);  // [NW][kWaves][MB][64][4]
+
+  if constexpr (NV > 0) {
+    // Normalised input rows, exactly as the rms_norm kernel computes them.
+    constexpr int VEC = 16 / sizeof(T);
+    const T* x = static_cast<const T*>(p.x);
+    const T* nw = static_cast<const T*>(p.norm_w);
+    for (int m = wave; m < MB * 16; m += kWaves) {
+      uint4 out[NV];
+      if (m < M) {
+        slc::rms_norm_row<T, NV, true>(x + m * p.x_rs, nw, K, p.eps, lane, out);
+      } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) out[i] = make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int idx = lane + 64 * i;
+        if (idx < K / VEC)
+          *reinterpret_cast<uint4*>(xs + (m * norm_row(K) + idx * VEC) * 2) = out[i];
+      }
+    }
+    __syncthreads();
+  }
+
+  const int steps = (K + 31) / 32;               // 32-wide MFMA k-steps
+  const int per_wave = (steps + kWaves - 1) / kWaves;
+  const int s_begin = wave * per_wave;
+  const int s_end = min(s_begin + per_wave, steps);
+
+  const int w_rows = min(16, N - n0);
+  __amdgpu_buffer_rsrc_t rw[NW];
+  rw[0] = make_rsrc(static_cast<const T*>(p.w[j]) + static_cast<int64_t>(n0) * K,
+                    static_cast<int64_t>(w_rows) * K * 2);
+  if constexpr (NW == 2)
+    rw[1] = make_rsrc(static_cast<const T*>(p.w[1]) + static_cast<int64_t>(n0) * K,
+                      static_cast<int64_t>(w_rows) * K * 2);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(
+      p.x, (static_cast<int64_t>(M) - 1) * p.x_rs * 2 + static_cast<int64_t>(K) * 2);
+  const int w_off = c * K * 2 + g * 16;
+  int x_off[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) {
+    x_off[i] = NV > 0 ? ((i * 16 + c) * norm_row(K) + g * 8) * 2
+                      : static_cast<int>((i * 16 + c) * p.x_rs * 2) + g * 16;
+  }
+
+  f32x4_t acc[NW][MB];
+#pragma unroll
+  for (int h = 0; h < NW; ++h)
+#pragma unroll
+    for (int i = 0; i < MB; ++i) acc[h][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // Weight (and, without the norm, input) operands U k-steps at a time, the
+  // next batch in flight while the current one is multiplied.
+  uint4 wa[U][NW], wb[U][NW], xa[U][NV > 0 ? 1 : MB], xb[U][NV > 0 ? 1 : MB];
+  auto fetch = [&](int s0, uint4 (&wr)[U][NW], uint4 (&xr)[U][NV > 0 ? 1 : MB]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = s0 + u;
+      const bool ok = s < s_end && s * 32 + g * 8 < K;
+#pragma unroll
+      for (int h = 0; h < NW; ++h)
+        wr[u][h] = ok ? buffer_load16(rw[h], w_off + s * 64) : make_uint4(0, 0, 0, 0);
+      if constexpr (NV == 0) {
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+          xr[u][i] = ok ? buffer_load16(rx, x_off[i] + s * 64) : make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  auto multiply = [&](int s0, const uint4 (&wr)[U][NW], const uint4 (&xr)[U][NV > 0 ? 1 : MB]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = s0 + u;
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+        uint4 xv;
+        if constexpr (NV > 0) {
+          const bool ok = s < s_end && s * 32 + g * 8 < K;
+          xv = ok ? *reinterpret_cast<const uint4*>(xs + x_off[i] + s * 64) : make_uint4(0, 0, 0, 0);
+        } else {
+          xv = xr[u][i];
+        }
+        const auto a = __builtin_bit_cast(typename MF::vec, xv);
+#pragma unroll
+        for (int h = 0; h < NW; ++h)
+          acc[h][i] = MF::run(a, __builtin_bit_cast(typename MF::vec, wr[u][h]), acc[h][i]);
+      }
+    }
+  };
+
+  int s0 = s_begin;
+  fetch(s0, wa, xa);
+  while (s0 < s_end) {
+    fetch(s0 + U, wb, xb);
+    multiply(s0, wa, xa);
+    s0 += U;
+    if (s0 >= s_end) break;
+    fetch(s0 + U, wa, xa);
+    multiply(s0, wb, xb);
+    s0 += U;
+  }
+
+  // C layout: lane (col c = feature, rows 4g..4g+3 = input rows of block i).
+  auto part = [&](int h, int v, int i, int l, int r) -> float& {
+    return partial[((((h * kWaves + v) * MB + i) * 64 + l) * 4) + r];
+  };
+#pragma unroll
+  for (int h = 0; h < NW; ++h)
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) part(h, wave, i, lane, r) = acc[h][i][r];
+  __syncthreads();
+  for (int idx = tid; idx < MB * 64 * 4; idx += kWaves * 64) {
+    const int i = idx / 256, l = (idx / 4) % 64, r = idx % 4;
+    const int n = n0 + (l & 15);
+    const int m = i * 16 + 4 * (l >> 4) + r;
+    if (n >= N || m >= M) continue;
+    float sum = 0.0f;
+#pragma unroll
+    for (int v = 0; v < kWaves; ++v) sum += part(0, v, i, l, r);
+    if constexpr (EPI == kSwiglu) {
+      float up = 0.0f;
+#pragma unroll
+      for (int v = 0; v < kWaves; ++v) up += part(1, v, i, l, r);
+      const float gate = slc::round_to<T>(sum);
+      static_cast<T*>(p.y[0])[m * p.y_rs[0] + n] =
+          slc::from_f32<T>(slc::swiglu_value<T>(gate, slc::round_to<T>(up)));
+    } else {
+      if (p.bias[j] != nullptr) sum += slc::to_f32(static_cast<const T*>(p.bias[j])[n]);
+      if constexpr (EPI == kResidual) {
+        const float res = slc::to_f32(static_cast<const T*>(p.residual)[m * p.r_rs + n]);
+        sum = res + slc::round_to<T>(sum);
+      }
+      static_cast<T*>(p.y[j])[m * p.y_rs[j] + n] = slc::from_f32<T>(sum);
+    }
+  }
+}
+
+template <typename T, int NV, int EPI>
+int launch_rows(FusedArgs& a, hipStream_t stream) {
+  const int blocks = a.block_end[kMaxMatrices - 1];
+  const int nw = EPI == kSwiglu ? 2 : 1;
+  auto go = [&](auto kernel, int mb) {
+    const int xs_bytes = NV > 0 ? mb * 16 * norm_row(a.hidden) * 2 : 0;
+    const int bytes = xs_bytes + nw * kWaves * mb * 64 * 4 * 4;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess) {
+      slc_host::set_error("fused decode kernel: LDS size %d rejected: %s", bytes,
+                          hipGetErrorString(e));
+      return static_cast<int>(e);
+    }
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kWaves * 64),
+                       static_cast<unsigned>(bytes), stream, a);
+    return slc_host::check_launch("fused decode kernel");
+  };
+  // Prefetch depth: as deep as the registers allow (two weight streams for
+  // SwiGLU halve it).
+  if (a.rows <= 16) return go(fused_rows_kernel<T, 1, EPI == kSwiglu ? 4 : 8, NV, EPI>, 1);
+  return go(fused_rows_kernel<T, 2, EPI == kSwiglu ? 2 : 4, NV, EPI>, 2);
+}
+
+template <int EPI>
+int dispatch_rows(FusedArgs& a, int dtype, hipStream_t stream) {
+  const bool norm = a.norm_w != nullptr;
+  const int nv = (a.hidden / 8 + 63) / 64;  // 16-byte vectors per lane
+#define SLC_ROWS(T)                                             \
+  do {                                                          \
+    if (!norm) return launch_rows<T, 0, EPI>(a, stream);        \
+    if (nv <= 1) return launch_rows<T, 1, EPI>(a, stream);      \
+    if (nv <= 2) return launch_rows<T, 2, EPI>(a, stream);      \
+    return launch_rows<T, 4, EPI>(a, stream);                   \
+  } while (0)
+  if (dtype == SLC_BF16) SLC_ROWS(slc::bf16_t);
+  SLC_ROWS(slc::f16_t);
+#undef SLC_ROWS
+}
+
+// Shared argument checks: decode-sized rows, 16-byte aligned contiguous rows.
+int check_rows(const char* what, const void* x, int64_t x_rs, int64_t rows, int64_t hidden,
+               int dtype, bool norm) {
+  SLC_REQUIRE(dtype == SLC_BF16 || dtype == SLC_F16, "%s: dtype must be bf16 or fp16", what);
+  SLC_REQUIRE(rows >= 1 && rows <= kMaxRows, "%s: rows must be 1..%d", what, kMaxRows);
+  SLC_REQUIRE(hidden >= 8 && hidden % 8 == 0, "%s: hidden must be a positive multiple of 8",
+              what);
+  SLC_REQUIRE(!norm || hidden <= 64 * 8 * 4, "%s: hidden above 2048 with a norm", what);
+  SLC_REQUIRE(x != nullptr && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && x_rs >= hidden &&
+                  x_rs % 8 == 0,
+              "%s: input rows must be 16-byte aligned", what);
+  return SLC_OK;
+}
+
+// ---- rope + kv_store ---------------------------------------------------------
+
+struct RopeStoreArgs {
+  int64_t q_heads, kv_heads, tokens, half, capacity;
+  int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st;
+  int64_t c_sb, c_st, s_sb, s_st;
+  int64_t qo_sb, qo_sh, qo_st;
+};
+
+// One thread owns dims [d, d + VEC) of the first half and the matching dims of
+// the second half of one (batch, head, token) row.  Heads [0, QH) are query
+// heads (rotated into q_out), [QH, QH + KVH) key heads (rotated into the key
+// buffer row positions[b] + t), [QH + KVH, QH + 2 KVH) value heads (copied
+// into the value buffer).  Rows past the capacity are skipped and flagged.
+template <typename T, int VEC>
+__global__ __launch_bounds__(256) void rope_kv_store_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const T* __restrict__ cosine, const T* __restrict__ sine, T* __restrict__ q_out,
+    T* __restrict__ key_buffer, T* __restrict__ value_buffer,
+    const int64_t* __restrict__ positions, int* __restrict__ overflow, RopeStoreArgs a,
+    int64_t total) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (gid >= total) return;
+  const int64_t per_row = a.half / VEC;
+  const int64_t d = (gid % per_row) * VEC;
+  int64_t rest = gid / per_row;
+  const int64_t t = rest % a.tokens;
+  rest /= a.tokens;
+  const int64_t heads = a.q_heads + 2 * a.kv_heads;
+  const int64_t h = rest % heads;
+  const int64_t b = rest / heads;
+  const int64_t D = 2 * a.half;
+
+  const T* src;
+  T* dst;
+  if (h < a.q_heads) {
+    src = q + b * a.q_sb + h * a.q_sh + t * a.q_st;
+    dst = q_out + b * a.qo_sb + h * a.qo_sh + t * a.qo_st;
+  } else {
+    const int64_t position = positions[b] + t;
+    if (position < 0 || position >= a.capacity) {
+      if (overflow != nullptr) *overflow = 1;
+      return;
+    }
+    const bool is_key = h < a.q_heads + a.kv_heads;
+    const int64_t kh = is_key ? h - a.q_heads : h - a.q_heads - a.kv_heads;
+    const int64_t row = ((b * a.capacity + position) * a.kv_heads + kh) * D;
+    if (!is_key) {
+      const T* vs = v + b * a.v_sb + kh * a.v_sh + t * a.v_st;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        value_buffer[row + d + e] = vs[d + e];
+        value_buffer[row + d + a.half + e] = vs[d + a.half + e];
+      }
+      return;
+    }
+    src = k + b * a.k_sb + kh * a.k_sh + t * a.k_st;
+    dst = key_buffer + row;
+  }
+  const T* cr = cosine + b * a.c_sb + t * a.c_st;
+  const T* sr = sine + b * a.s_sb + t * a.s_st;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    float o1, o2;
+    slc::rope_pair<T>(slc::to_f32(src[d + e]), slc::to_f32(src[d + a.half + e]),
+                      slc::to_f32(cr[d + e]), slc::to_f32(cr[d + a.half + e]),
+                      slc::to_f32(sr[d + e]), slc::to_f32(sr[d + a.half + e]), o1, o2);
+    dst[d + e] = slc::from_f32<T>(o1);
+    dst[d + a.half + e] = slc::from_f32<T>(o2);
+  }
+}
+
+}  // namespace
+
+extern "C" int slc_hip_norm_linear_group(
+    const void* x, int64_t x_rs, const void* norm_weight, float epsilon, int64_t rows,
+    int64_t hidden, int count, const void* w0, const void* b0, void* y0, int64_t n0,
+    int64_t y0_rs, const void* w1, const void* b1, void* y1, int64_t n1, int64_t y1_rs,
+    const void* w2, const void* b2, void* y2, int64_t n2, int64_t y2_rs, int dtype,
+    void* stream) {
+  const char* what = "slc_hip_norm_linear_group";
+  if (int rc = check_rows(what, x, x_rs, rows, hidden, dtype, norm_weight != nullptr)) return rc;
+  SLC_REQUIRE(count >= 1 && count <= kMaxMatrices, "%s: 1 to 3 matrices", what);
+  FusedArgs a{};
+  a.x = x;
+  a.x_rs = x_rs;
+  a.norm_w = norm_weight;
+  a.eps = epsilon;
+  a.rows = static_cast<int>(rows);
+  a.hidden = static_cast<int>(hidden);
+  const void* ws[3] = {w0, w1, w2};
+  const void* bs[3] = {b0, b1, b2};
+  void* ys[3] = {y0, y1, y2};
+  const int64_t ns[3] = {n0, n1, n2};
+  const int64_t yrs[3] = {y0_rs, y1_rs, y2_rs};
+  int blocks = 0;
+  for (int i = 0; i < kMaxMatrices; ++i) {
+    if (i < count) {
+      SLC_REQUIRE(ws[i] && ys[i] && ns[i] >= 1 && ns[i] <= (1 << 24) && yrs[i] >= ns[i],
+                  "%s: bad matrix %d", what, i);
+      a.w[i] = ws[i];
+      a.bias[i] = bs[i];
+      a.y[i] = ys[i];
+      a.n[i] = static_cast<int>(ns[i]);
+      a.y_rs[i] = yrs[i];
+      blocks += static_cast<int>((ns[i] + 15) / 16);
+    }
+    a.block_end[i] = blocks;
+  }
+  return dispatch_rows<kStore>(a, dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int slc_hip_norm_linear_swiglu(const void* x, int64_t x_rs, const void* norm_weight,
+                                          float epsilon, int64_t rows, int64_t hidden,
+                                          int64_t features, const void* w_gate,
+                                          const void* w_up, void* y, int64_t y_rs, int dtype,
+                                          void* stream) {
+  const char* what = "slc_hip_norm_linear_swiglu";
+  if (int rc = check_rows(what, x, x_rs, rows, hidden, dtype, norm_weight != nullptr)) return rc;
+  SLC_REQUIRE(w_gate && w_up && y && features >= 1 && features <= (1 << 24) && y_rs >= features,
+              "%s: bad projections", what);
+  FusedArgs a{};
+  a.x = x;
+  a.x_rs = x_rs;
+  a.norm_w = norm_weight;
+  a.eps = epsilon;
+  a.rows = static_cast<int>(rows);
+  a.hidden = static_cast<int>(hidden);
+  a.w[0] = w_gate;
+  a.w[1] = w_up;
+  a.y[0] = y;
+  a.n[0] = static_cast<int>(features);
+  a.y_rs[0] = y_rs;
+  const int blocks = static_cast<int>((features + 15) / 16);
+  a.block_end[0] = a.block_end[1] = a.block_end[2] = blocks;
+  return dispatch_rows<kSwiglu>(a, dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int slc_hip_linear_residual(const void* x, int64_t x_rs, int64_t rows,
+                                       int64_t in_features, int64_t out_features,
+                                       const void* weight, const void* bias,
+                                       const void* residual, int64_t residual_rs, void* y,
+                                       int64_t y_rs, int dtype, void* stream) {
+  const char* what = "slc_hip_linear_residual";
+  if (int rc = check_rows(what, x, x_rs, rows, in_features, dtype, false)) return rc;
+  SLC_REQUIRE(weight && residual && y && out_features >= 1 && out_features <= (1 << 24) &&
+                  y_rs >= out_features && residual_rs >= out_features,
+              "%s: bad operands", what);
+  FusedArgs a{};
+  a.x = x;
+  a.x_rs = x_rs;
+  a.rows = static_cast<int>(rows);
+  a.hidden = static_cast<int>(in_features);
+  a.w[0] = weight;
+  a.bias[0] = bias;
+  a.y[0] = y;
+  a.n[0] = static_cast<int>(out_features);
+  a.y_rs[0] = y_rs;
+  a.residual = residual;
+  a.r_rs = residual_rs;
+  const int blocks = static_cast<int>((out_features + 15) / 16);
+  a.block_end[0] = a.block_end[1] = a.block_end[2] = blocks;
+  return dispatch_rows<kResidual>(a, dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int slc_hip_rope_kv_store(
+    const void* query, const void* key, const void* value, const void* cosine,
+    const void* sine, void* query_out, void* key_buffer, void* value_buffer,
+    const int64_t* positions, int* overflow, int dtype, int64_t batch, int64_t q_heads,
+    int64_t kv_heads, int64_t tokens, int64_t head_dim, int64_t capacity, int64_t q_sb,
+    int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t v_sb,
+    int64_t v_sh, int64_t v_st, int64_t cos_sb, int64_t cos_st, int64_t sin_sb,
+    int64_t sin_st, int64_t qo_sb, int64_t qo_sh, int64_t qo_st, void* stream) {
+  const char* what = "slc_hip_rope_kv_store";
+  SLC_REQUIRE(slc_host::is_float_dtype(dtype), "%s: bad dtype %d", what, dtype);
+  SLC_REQUIRE(batch >= 0 && q_heads >= 0 && kv_heads >= 0 && tokens >= 0 && head_dim > 0 &&
+                  head_dim % 2 == 0 && capacity >= 0,
+              "%s: bad sizes", what);
+  if (batch == 0 || tokens == 0 || q_heads + kv_heads == 0) return SLC_OK;
+  SLC_REQUIRE(query && key && value && cosine && sine && query_out && key_buffer &&
+                  value_buffer && positions,
+              "%s: null pointer", what);
+  RopeStoreArgs a{q_heads, kv_heads, tokens, head_dim / 2, capacity, q_sb, q_sh, q_st,
+                  k_sb,    k_sh,     k_st,   v_sb,         v_sh,     v_st, cos_sb, cos_st,
+                  sin_sb,  sin_st,   qo_sb,  qo_sh,        qo_st};
+  const int64_t per_row = (head_dim / 2) % 4 == 0 ? head_dim / 8 : head_dim / 2;
+  const int64_t total = batch * (q_heads + 2 * kv_heads) * tokens * per_row;
+  const dim3 grid(static_cast<unsigned>(slc_host::ceil_div(total, 256)));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool vec4 = (head_dim / 2) % 4 == 0;
+#define SLC_RS(T, V)                                                                      \
+  hipLaunchKernelGGL((rope_kv_store_kernel<T, V>), grid, dim3(256), 0, s,                \
+                     static_cast<const T*>(query), static_cast<const T*>(key),           \
+                     static_cast<const T*>(value), static_cast<const T*>(cosine),        \
+                     static_cast<const T*>(sine), static_cast<T*>(query_out),            \
+                     static_cast<T*>(key_buffer), static_cast<T*>(value_buffer), positions, \
+                     overflow, a, total)
+  if (dtype == SLC_BF16) {
+    if (vec4) SLC_RS(slc::bf16_t, 4); else SLC_RS(slc::bf16_t, 1);
+  } else if (dtype == SLC_F16) {
+    if (vec4) SLC_RS(slc::f16_t, 4); else SLC_RS(slc::f16_t, 1);
+  } else {
+    if (vec4) SLC_RS(float, 4); else SLC_RS(float, 1);
+  }
+#undef SLC_RS
+  return slc_host::check_launch(what);
+}

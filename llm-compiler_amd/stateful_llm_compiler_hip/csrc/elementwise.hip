@@ -10,6 +10,7 @@
 //   argmax      greedy next token over the vocabulary
 // Every op is one launch of 16-byte vector accesses where the layout allows.
 #include "common.hpp"
+#include "op_math.hpp"
 
 namespace {
 
@@ -93,8 +94,7 @@ __global__ __launch_bounds__(256) void binary_kernel(const T* __restrict__ a,
     if constexpr (OP == 0) {
       return x + y;
     } else {
-      const float s = x / (1.0f + expf(-x));
-      return slc::round_to<T>(s) * y;
+      return slc::swiglu_value<T>(x, y);
     }
   };
   if constexpr (VEC) {

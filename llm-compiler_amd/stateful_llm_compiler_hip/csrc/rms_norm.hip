@@ -12,6 +12,7 @@
 // Rows that do not fit the register plan, or mixed dtypes, use a one-block-
 // per-row kernel that re-reads the row (from L2) for the second pass.
 #include "common.hpp"
+#include "op_math.hpp"
 
 namespace {
 
@@ -29,42 +30,13 @@ __global__ __launch_bounds__(256) void rms_norm_wave_kernel(
   if (row >= rows) return;
   const int lane = threadIdx.x & 63;
   const int nvec = hidden / VEC;
-  const T* xr = x + row * x_rs;
-  float v[NV][VEC];
-  float sq = 0.0f;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int idx = lane + 64 * i;
-    if (idx < nvec) {
-      const uint4 raw = *reinterpret_cast<const uint4*>(xr + idx * VEC);
-      const T* e = reinterpret_cast<const T*>(&raw);
-#pragma unroll
-      for (int k = 0; k < VEC; ++k) {
-        v[i][k] = slc::to_f32(e[k]);
-        sq += v[i][k] * v[i][k];
-      }
-    }
-  }
-  sq = slc::wave_sum(sq);
-  const float inv = rsqrtf(sq / static_cast<float>(hidden) + eps);
+  uint4 out[NV];
+  slc::rms_norm_row<T, NV, ROUND>(x + row * x_rs, w, hidden, eps, lane, out);
   T* yr = y + row * y_rs;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int idx = lane + 64 * i;
-    if (idx < nvec) {
-      const uint4 wraw = *reinterpret_cast<const uint4*>(w + idx * VEC);
-      const T* we = reinterpret_cast<const T*>(&wraw);
-      uint4 out;
-      T* oe = reinterpret_cast<T*>(&out);
-#pragma unroll
-      for (int k = 0; k < VEC; ++k) {
-        const float n = v[i][k] * inv;
-        const float wk = slc::to_f32(we[k]);
-        oe[k] = ROUND ? slc::from_f32<T>(slc::round_to<T>(n) * wk)
-                      : slc::from_f32<T>(n * wk);
-      }
-      *reinterpret_cast<uint4*>(yr + idx * VEC) = out;
-    }
+    if (idx < nvec) *reinterpret_cast<uint4*>(yr + idx * VEC) = out[i];
   }
 }
 

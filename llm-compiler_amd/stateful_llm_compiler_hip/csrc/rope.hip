@@ -13,6 +13,7 @@
 // (batch, head, token) row: it reads each of x, cos and sin once and writes
 // both halves, so the kernel moves the algorithmic minimum of bytes.
 #include "common.hpp"
+#include "op_math.hpp"
 
 namespace {
 
@@ -102,14 +103,7 @@ __global__ __launch_bounds__(256) void rope_kernel(
   load_vec<T, VEC>(sr + d + a.half, s2);
   float o1[VEC], o2[VEC];
 #pragma unroll
-  for (int k = 0; k < VEC; ++k) {
-    const float p1 = x1[k] * c1[k];
-    const float p2 = x2[k] * s1[k];  // rounding is sign-symmetric: round(-a) = -round(a)
-    const float p3 = x2[k] * c2[k];
-    const float p4 = x1[k] * s2[k];
-    o1[k] = slc::round_to<T>(p1) - slc::round_to<T>(p2);
-    o2[k] = slc::round_to<T>(p3) + slc::round_to<T>(p4);
-  }
+  for (int k = 0; k < VEC; ++k) slc::rope_pair<T>(x1[k], x2[k], c1[k], c2[k], s1[k], s2[k], o1[k], o2[k]);
   store_vec<T, VEC>(dst + d, o1);
   store_vec<T, VEC>(dst + d + a.half, o2);
 }

@@ -32,9 +32,13 @@ from .backends import (
     hip_kv_advance,
     hip_kv_store,
     hip_linear,
+    hip_linear_residual,
+    hip_norm_linear_group,
+    hip_norm_linear_swiglu,
     hip_prefill_attention,
     hip_rms_norm,
     hip_rope,
+    hip_rope_kv_store,
     hip_rope_table,
     hip_swiglu,
 )
@@ -228,6 +232,24 @@ class PreallocatedKVCacheState:
         # visible prefixes are untouched, so the same object is returned.
         return self
 
+    def rope_store(
+        self,
+        slot: int,
+        query: torch.Tensor,
+        key: torch.Tensor,
+        value: torch.Tensor,
+        cosine: torch.Tensor,
+        sine: torch.Tensor,
+        positions: torch.Tensor,
+    ) -> tuple[torch.Tensor, "PreallocatedKVCacheState"]:
+        """RoPE of ``query``/``key`` with the rotated key and ``value`` stored
+        at ``positions`` in one kernel: the rotated query and this state."""
+
+        buffer_key, buffer_value = self._validate_store(slot, key, value, positions)
+        q_rot = hip_rope_kv_store(query, key, value, cosine, sine, buffer_key, buffer_value,
+                                  positions, overflow=self.overflow)
+        return q_rot, self
+
     def prefill_store(
         self,
         slot: int,
@@ -307,6 +329,10 @@ class HipExecutor:
             "kernel.hip.add": self._add,
             "kernel.hip.swiglu": self._swiglu,
             "kernel.hip.rope_table": self._rope_table,
+            "kernel.hip.norm_linear_group": self._norm_linear_group,
+            "kernel.hip.norm_linear_swiglu": self._norm_linear_swiglu,
+            "kernel.hip.linear_residual": self._linear_residual,
+            "kernel.hip.rope_kv_store": self._rope_kv_store,
             "runtime.kv.init": self._kv_init,
             "runtime.kv.length": self._kv_length,
             "runtime.kv.advance": self._kv_advance,
@@ -430,6 +456,46 @@ class HipExecutor:
             raise ExecutionError("kernel.hip.kv_prefill_store takes state, key and value")
         state, key, value = operands
         return state.prefill_store(int(attributes.get("slot", 0)), key, value)
+
+    @staticmethod
+    def _norm_linear_group(operands, attributes):
+        has_bias = list(attributes["has_bias"])
+        if len(operands) != 2 + len(has_bias) + sum(has_bias):
+            raise ExecutionError("kernel.hip.norm_linear_group operands do not match has_bias")
+        tensor, norm_weight = operands[:2]
+        weights, biases, i = [], [], 2
+        for bias_present in has_bias:
+            weights.append(operands[i])
+            biases.append(operands[i + 1] if bias_present else None)
+            i += 2 if bias_present else 1
+        outputs = hip_norm_linear_group(tensor, norm_weight, weights, biases,
+                                        epsilon=float(attributes["epsilon"]))
+        return outputs[0] if len(outputs) == 1 else tuple(outputs)
+
+    @staticmethod
+    def _norm_linear_swiglu(operands, attributes):
+        if len(operands) != 4:
+            raise ExecutionError("kernel.hip.norm_linear_swiglu takes input, norm, gate and up weights")
+        tensor, norm_weight, gate, up = operands
+        return hip_norm_linear_swiglu(tensor, norm_weight, gate, up, epsilon=float(attributes["epsilon"]))
+
+    @staticmethod
+    def _linear_residual(operands, attributes):
+        has_bias = bool(attributes.get("has_bias"))
+        if len(operands) != (4 if has_bias else 3):
+            raise ExecutionError("kernel.hip.linear_residual takes input, weight, [bias,] residual")
+        bias = operands[2] if has_bias else None
+        return hip_linear_residual(operands[0], operands[1], bias, operands[-1])
+
+    @staticmethod
+    def _rope_kv_store(operands, attributes):
+        if len(operands) != 7 or not isinstance(operands[0], PreallocatedKVCacheState):
+            raise ExecutionError("kernel.hip.rope_kv_store takes state, q, k, v, cos, sin, positions")
+        state, query, key, value, cosine, sine, positions = operands
+        if query.shape[-1] != int(attributes["head_dim"]):
+            raise ExecutionError("kernel.hip.rope_kv_store head dim mismatch")
+        return state.rope_store(int(attributes.get("slot", 0)), query, key, value, cosine, sine,
+                                positions)
 
     @staticmethod
     def _embedding(operands, attributes):

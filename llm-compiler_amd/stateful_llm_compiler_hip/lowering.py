@@ -75,8 +75,17 @@ _METADATA_LOWERINGS = {
 
 _LINEAR_TARGETS = {"fast": "kernel.hip.linear", "pytorch_compatible": "kernel.rocm_compat.linear"}
 
+# Decode-step fusions (passes/fusion.py) of the ops above.
+_FUSED_OPERATIONS = frozenset({
+    "kernel.hip.norm_linear_group",
+    "kernel.hip.norm_linear_swiglu",
+    "kernel.hip.linear_residual",
+    "kernel.hip.rope_kv_store",
+})
+
 EXECUTABLE_OPERATIONS = (
-    frozenset(_KERNEL_LOWERINGS.values())
+    _FUSED_OPERATIONS
+    | frozenset(_KERNEL_LOWERINGS.values())
     | frozenset(_RUNTIME_LOWERINGS.values())
     | frozenset(_METADATA_LOWERINGS.values())
     | frozenset(_LINEAR_TARGETS.values())

@@ -1,5 +1,6 @@
-"""ServeIR passes owned by this backend."""
+"""ServeIR / KernelIR passes owned by this backend."""
 
+from .fusion import FuseDecodeKernelsPass
 from .lowering_selection import SelectRMSNormLoweringPass
 
-__all__ = ["SelectRMSNormLoweringPass"]
+__all__ = ["FuseDecodeKernelsPass", "SelectRMSNormLoweringPass"]

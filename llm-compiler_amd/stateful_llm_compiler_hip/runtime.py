@@ -34,12 +34,13 @@ class Qwen2Runtime:
         numerical_mode: str = "fast",
         mask_dtype: str = "f32",
         validate: bool = True,
+        fuse: bool = True,
     ) -> None:
         self.config = config
         self.capacity = capacity
         self.dtype = dtype
         self.device = torch.device(device)
-        options = CompileOptions(numerical_mode=numerical_mode, require_full_lowering=True)
+        options = CompileOptions(numerical_mode=numerical_mode, require_full_lowering=True, fuse=fuse)
         self.prefill_result = compile_module(
             build_prefill_module(config, capacity=capacity, dtype=dtype, device=device,
                                  mask_dtype=mask_dtype), options)

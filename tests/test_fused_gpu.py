@@ -1,0 +1,139 @@
+"""Fused decode-step kernels on the GPU: each must equal, bit for bit, the
+sequence of single-op kernels it replaces (and so inherits their parity with
+the oracle), at every row count the fused path takes and on the fallback
+beyond it; and the fused Qwen2 graph must equal the unfused one."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from helpers import announce, assert_bitwise_equal, generator
+from stateful_llm_compiler_hip.backends import (
+    hip_add,
+    hip_kv_store,
+    hip_linear,
+    hip_linear_residual,
+    hip_norm_linear_group,
+    hip_norm_linear_swiglu,
+    hip_rms_norm,
+    hip_rope,
+    hip_rope_kv_store,
+    hip_swiglu,
+)
+
+pytestmark = pytest.mark.gpu
+
+ROWS = [1, 3, 8, 16, 17, 32, 40]  # 40 exceeds the fused limit: fallback path
+
+
+def _t(g, *shape, dtype=torch.bfloat16, scale=1.0, device):
+    return (torch.randn(*shape, generator=g) * scale).to(dtype).to(device)
+
+
+@pytest.mark.parametrize("rows", ROWS)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_norm_linear_group_matches_norm_then_linears(gpu, rows, dtype):
+    announce(f"norm_linear_group rows={rows} {dtype}")
+    g = generator(rows)
+    h = _t(g, rows, 1, 896, dtype=dtype, device=gpu)
+    nw = _t(g, 896, dtype=dtype, scale=0.5, device=gpu) + 1
+    ws = [_t(g, n, 896, dtype=dtype, scale=0.02, device=gpu) for n in (896, 128, 128)]
+    bs = [_t(g, n, dtype=dtype, scale=0.1, device=gpu) for n in (896, 128, 128)]
+    got = hip_norm_linear_group(h, nw, ws, bs, epsilon=1e-6)
+    x = hip_rms_norm(h, nw, epsilon=1e-6, round_before_weight=True)
+    want = [hip_linear(x, w, b) for w, b in zip(ws, bs)]
+    torch.cuda.synchronize()
+    for a, b in zip(got, want):
+        assert_bitwise_equal(a, b)
+    # one matrix, no bias, no norm
+    got1 = hip_norm_linear_group(h, None, ws[:1], [None], epsilon=1e-6)
+    assert_bitwise_equal(got1[0], hip_linear(h, ws[0]))
+
+
+@pytest.mark.parametrize("rows", ROWS)
+def test_norm_linear_swiglu_matches_the_mlp_front(gpu, rows):
+    announce(f"norm_linear_swiglu rows={rows}")
+    g = generator(100 + rows)
+    h = _t(g, rows, 1, 896, device=gpu)
+    nw = _t(g, 896, scale=0.5, device=gpu) + 1
+    wg = _t(g, 4864, 896, scale=0.02, device=gpu)
+    wu = _t(g, 4864, 896, scale=0.02, device=gpu)
+    got = hip_norm_linear_swiglu(h, nw, wg, wu, epsilon=1e-6)
+    x = hip_rms_norm(h, nw, epsilon=1e-6, round_before_weight=True)
+    want = hip_swiglu(hip_linear(x, wg), hip_linear(x, wu))
+    torch.cuda.synchronize()
+    assert_bitwise_equal(got, want)
+
+
+@pytest.mark.parametrize("rows", ROWS)
+@pytest.mark.parametrize("n,k", [(896, 896), (896, 4864), (100, 64)])
+def test_linear_residual_matches_linear_then_add(gpu, rows, n, k):
+    announce(f"linear_residual rows={rows} n={n} k={k}")
+    g = generator(200 + rows + n)
+    x = _t(g, rows, 1, k, device=gpu)
+    w = _t(g, n, k, scale=0.02, device=gpu)
+    r = _t(g, rows, 1, n, device=gpu)
+    bias = _t(g, n, scale=0.1, device=gpu) if n == 100 else None
+    got = hip_linear_residual(x, w, bias, r)
+    want = hip_add(r, hip_linear(x, w, bias))
+    torch.cuda.synchronize()
+    assert_bitwise_equal(got, want)
+
+
+@pytest.mark.parametrize("tokens", [1, 5])
+def test_rope_kv_store_matches_rope_then_store(gpu, tokens):
+    announce(f"rope_kv_store tokens={tokens}")
+    g = generator(300 + tokens)
+    B, QH, KVH, D, cap = 3, 14, 2, 64, 16
+    # q/k/v as the decode graph makes them: views of [B, T, H*D] projections.
+    q = _t(g, B, tokens, QH * D, device=gpu).view(B, tokens, QH, D).transpose(1, 2)
+    k = _t(g, B, tokens, KVH * D, device=gpu).view(B, tokens, KVH, D).transpose(1, 2)
+    v = _t(g, B, tokens, KVH * D, device=gpu).view(B, tokens, KVH, D).transpose(1, 2)
+    cos = _t(g, B, tokens, D, device=gpu)
+    sin = _t(g, B, tokens, D, device=gpu)
+    positions = torch.tensor([0, 7, cap - 2], device=gpu)  # the last row runs past the capacity
+    kb1 = _t(g, B, cap, KVH, D, device=gpu)
+    vb1 = _t(g, B, cap, KVH, D, device=gpu)
+    kb2, vb2 = kb1.clone(), vb1.clone()
+    flag1 = torch.zeros(1, dtype=torch.int32, device=gpu)
+    flag2 = torch.zeros(1, dtype=torch.int32, device=gpu)
+    q_got = hip_rope_kv_store(q, k, v, cos, sin, kb1, vb1, positions, overflow=flag1)
+    q_want, k_rot = hip_rope(q, k, cos, sin)
+    hip_kv_store(kb2, vb2, k_rot, v, positions, overflow=flag2)
+    torch.cuda.synchronize()
+    assert_bitwise_equal(q_got, q_want)
+    assert_bitwise_equal(kb1, kb2)
+    assert_bitwise_equal(vb1, vb2)
+    assert int(flag1.item()) == int(flag2.item()) == (1 if tokens > 2 else 0)
+
+
+def test_fused_qwen2_graph_equals_unfused(gpu):
+    from oracle.qwen2_model import causal_mask
+    from stateful_llm_compiler_hip.qwen2 import Qwen2Config, init_weights
+    from stateful_llm_compiler_hip.runtime import Qwen2Runtime
+
+    announce("fused vs unfused Qwen2 config-1 bf16")
+    config = Qwen2Config(num_layers=2, vocab_size=1024)
+    weights = {k: v.to(gpu) for k, v in init_weights(config, seed=0, dtype=torch.bfloat16).items()}
+    runs = []
+    for fuse in (True, False):
+        rt = Qwen2Runtime(config, weights, capacity=64, dtype=torch.bfloat16, device=str(gpu), fuse=fuse)
+        g = generator(1)
+        ids = torch.randint(0, config.vocab_size, (3, 5), generator=g).to(gpu)
+        pos = torch.arange(5).view(1, -1).expand(3, -1).contiguous().to(gpu)
+        logits, state = rt.prefill(ids, causal_mask(3, 5).to(gpu), pos)
+        outs = [logits]
+        token = logits[:, -1].argmax(-1, keepdim=True)
+        for step in range(3):
+            mask = torch.zeros(3, 1, 1, 6 + step, dtype=torch.bfloat16, device=gpu)
+            logits, state = rt.decode(token, mask, state)
+            outs.append(logits)
+            token = logits[:, -1].argmax(-1, keepdim=True)
+        outs += list(state.keys) + list(state.values)
+        runs.append(outs)
+        ops = len(rt.decode_result.module.functions[0].block.operations)
+        announce(f"fuse={fuse}: {ops} decode ops")
+    torch.cuda.synchronize()
+    for a, b in zip(*runs):
+        assert_bitwise_equal(a, b)

@@ -120,10 +120,19 @@ def test_full_lowering_of_24_layer_graphs(mode):
     counts = decode.coverage.lowered_by_name
     assert counts["runtime.kv.advance"] == 24 and counts["runtime.kv.length"] == 25
     if mode == "fast":
-        assert counts["kernel.hip.linear"] == 24 * 7 + 1
+        # Every layer's chains are fused; the vocabulary-sized LM head keeps
+        # its own norm and linear.
+        assert counts["kernel.hip.linear"] == 1 and counts["kernel.hip.rms_norm"] == 1
+        assert counts["kernel.hip.norm_linear_group"] == 24
+        assert counts["kernel.hip.norm_linear_swiglu"] == 24
+        assert counts["kernel.hip.linear_residual"] == 48
+        assert counts["kernel.hip.rope_kv_store"] == 24
         assert counts["kernel.hip.decode_attention"] == 24
-        assert counts["kernel.hip.rms_norm"] == 49
         assert not any(name.startswith("kernel.rocm_compat") for name in counts)
+        plain = compile_module(build_decode_module(config, capacity=2048), CompileOptions(fuse=False))
+        plain_counts = plain.coverage.lowered_by_name
+        assert plain_counts["kernel.hip.linear"] == 24 * 7 + 1
+        assert plain_counts["kernel.hip.rms_norm"] == 49
     else:
         assert counts["kernel.rocm_compat.linear"] == 24 * 7 + 1
         assert counts["kernel.hip.rope"] == 24  # bit-exact in both modes
