@@ -16,11 +16,13 @@
 //  * rope_kv_store       rope -> kv_store of the rotated keys and the values;
 //                        the rotated queries are written out.
 //
-// The weight-streaming loop is the decode linear kernel's (linear.hip,
-// linear_skinny_kernel): the same K split over the same 8 waves, the same
-// MFMA order and the same partial-sum order, hence the same bits.
+// slc_hip_linear runs its decode-sized (<= 32 rows) cases on this same kernel
+// (rows_linear), so a fused op and the ops it replaces share the K split over
+// the waves, the MFMA order and the partial-sum order, hence the same bits.
 // Semantics: src/stateful_llm_compiler/execution.py:674-692 (rms_norm),
 // triton_executor.py:159-176 (linear), :741-767 (rope), :743-781 (kv store).
+#include <mutex>
+
 #include "common.hpp"
 #include "op_math.hpp"
 
@@ -62,7 +64,9 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int 
 
 enum Epilogue { kStore = 0, kResidual = 1, kSwiglu = 2 };
 
-constexpr int kWaves = 8;        // K split of the decode linear kernel
+// Waves per workgroup (the K split).  (16 waves for long K measured twice as
+// slow on the down projection: a quarter of the registers per wave.)
+__host__ __device__ constexpr int waves_for(int) { return 8; }
 constexpr int kMaxRows = 32;     // rows (batch x tokens) the fused kernels take
 constexpr int kMaxMatrices = 3;
 
@@ -80,7 +84,24 @@ struct FusedArgs {
   int block_end[kMaxMatrices];     // cumulative 16-feature blocks
   const void* residual;            // [rows, n_0] with row stride r_rs
   int64_t r_rs;
+  int splits;                      // workgroups sharing one feature block's K
+  int region;                      // split-K scratch region of the calling stream
 };
+
+// ---- split-K across workgroups (narrow projections) ------------------------
+// A feature block whose K is split over `splits` workgroups: each publishes
+// its partial sums with agent-scope stores, bumps the block's counter, and
+// the workgroup that completes the count adds the partials in split order
+// (so the result does not depend on which finished last), applies the
+// epilogue and re-arms the counter.  The scratch lives in static device
+// memory, one region per stream (assigned on the host), so calls that run
+// concurrently on different streams do not share counters.
+constexpr int kSplitRegions = 16;
+constexpr int kSplitBlocks = 256;      // feature blocks per split call
+constexpr int kMaxSplits = 4;
+constexpr int kSplitFloats = kSplitBlocks * kMaxSplits * 2 * 256;  // MB <= 2: 2 MiB
+__device__ int g_split_counters[kSplitRegions][kSplitBlocks];
+__device__ float g_split_partials[kSplitRegions][kSplitFloats];
 
 // LDS row stride of the normalised input, in elements: 8 extra elements move
 // consecutive rows 4 banks apart, so the 16-row operand reads do not collide.
@@ -88,8 +109,9 @@ __host__ __device__ constexpr int norm_row(int hidden) { return hidden + 8; }
 
 // NV: 16-byte vectors per lane of the norm prologue (0 = no norm, the input
 // rows are read from global memory like the decode linear kernel does).
-template <typename T, int MB, int U, int NV, int EPI>
-__global__ __launch_bounds__(kWaves * 64) void fused_rows_kernel(FusedArgs p) {
+template <typename T, int MB, int KW, int U, int NV, int EPI>
+__global__ __launch_bounds__(KW * 64) void fused_rows_kernel(FusedArgs p) {
+  constexpr int kWaves = KW;
   using MF = Mfma<T>;
   constexpr int NW = EPI == kSwiglu ? 2 : 1;  // weight streams per workgroup
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -134,9 +156,14 @@ __global__ __launch_bounds__(kWaves * 64) void fused_rows_kernel(FusedArgs p) {
     __syncthreads();
   }
 
-  const int steps = (K + 31) / 32;               // 32-wide MFMA k-steps
-  const int per_wave = (steps + kWaves - 1) / kWaves;
-  const int s_begin = wave * per_wave;
+  // K range of this workgroup (its split), then of this wave.
+  const int all_steps = (K + 31) / 32;             // 32-wide MFMA k-steps
+  const int split = blockIdx.y;
+  const int per_split = (all_steps + p.splits - 1) / p.splits;
+  const int split_begin = split * per_split;
+  const int steps = min(all_steps, split_begin + per_split);
+  const int per_wave = (steps - split_begin + kWaves - 1) / kWaves;
+  const int s_begin = split_begin + wave * per_wave;
   const int s_end = min(s_begin + per_wave, steps);
 
   const int w_rows = min(16, N - n0);
@@ -224,14 +251,42 @@ __global__ __launch_bounds__(kWaves * 64) void fused_rows_kernel(FusedArgs p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) part(h, wave, i, lane, r) = acc[h][i][r];
   __syncthreads();
+  if (p.splits > 1) {
+    // Publish this split's sums (wave partials added in wave order).
+    float* mine = g_split_partials[p.region] + (blk * p.splits + split) * MB * 256;
+    for (int idx = tid; idx < MB * 64 * 4; idx += kWaves * 64) {
+      const int i = idx / 256, l = (idx / 4) % 64, r = idx % 4;
+      float sum = 0.0f;
+#pragma unroll
+      for (int v = 0; v < kWaves; ++v) sum += part(0, v, i, l, r);
+      __hip_atomic_store(mine + idx, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    __shared__ int last;
+    if (tid == 0) {
+      int* counter = &g_split_counters[p.region][blk];
+      const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = before == p.splits - 1;
+      if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last) return;
+  }
   for (int idx = tid; idx < MB * 64 * 4; idx += kWaves * 64) {
     const int i = idx / 256, l = (idx / 4) % 64, r = idx % 4;
     const int n = n0 + (l & 15);
     const int m = i * 16 + 4 * (l >> 4) + r;
     if (n >= N || m >= M) continue;
     float sum = 0.0f;
+    if (p.splits > 1) {
+      const float* all = g_split_partials[p.region] + blk * p.splits * MB * 256;
+      for (int q = 0; q < p.splits; ++q)
+        sum += __hip_atomic_load(all + q * MB * 256 + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
 #pragma unroll
-    for (int v = 0; v < kWaves; ++v) sum += part(0, v, i, l, r);
+      for (int v = 0; v < kWaves; ++v) sum += part(0, v, i, l, r);
+    }
     if constexpr (EPI == kSwiglu) {
       float up = 0.0f;
 #pragma unroll
@@ -254,9 +309,10 @@ template <typename T, int NV, int EPI>
 int launch_rows(FusedArgs& a, hipStream_t stream) {
   const int blocks = a.block_end[kMaxMatrices - 1];
   const int nw = EPI == kSwiglu ? 2 : 1;
+  const int kw = waves_for(a.hidden);
   auto go = [&](auto kernel, int mb) {
     const int xs_bytes = NV > 0 ? mb * 16 * norm_row(a.hidden) * 2 : 0;
-    const int bytes = xs_bytes + nw * kWaves * mb * 64 * 4 * 4;
+    const int bytes = xs_bytes + nw * kw * mb * 64 * 4 * 4;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
     if (e != hipSuccess) {
@@ -264,18 +320,138 @@ int launch_rows(FusedArgs& a, hipStream_t stream) {
                           hipGetErrorString(e));
       return static_cast<int>(e);
     }
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kWaves * 64),
-                       static_cast<unsigned>(bytes), stream, a);
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(a.splits)),
+                       dim3(kw * 64), static_cast<unsigned>(bytes), stream, a);
     return slc_host::check_launch("fused decode kernel");
   };
   // Prefetch depth: as deep as the registers allow (two weight streams for
   // SwiGLU halve it).
-  if (a.rows <= 16) return go(fused_rows_kernel<T, 1, EPI == kSwiglu ? 4 : 8, NV, EPI>, 1);
-  return go(fused_rows_kernel<T, 2, EPI == kSwiglu ? 2 : 4, NV, EPI>, 2);
+  constexpr int U1 = EPI == kSwiglu ? 4 : 8, U2 = EPI == kSwiglu ? 2 : 4;
+  if (a.rows <= 16) return go(fused_rows_kernel<T, 1, 8, U1, NV, EPI>, 1);
+  return go(fused_rows_kernel<T, 2, 8, U2, NV, EPI>, 2);
+}
+
+// Wide projections (the vocabulary head): enough 16-feature blocks to fill
+// the GPU without splitting K, so each wave owns one block over the whole K
+// (no cross-wave reduction, nothing through LDS) and keeps U k-steps of
+// weights in flight.
+constexpr int kWideBlocks = 1024;
+template <typename T, int MB, int U>
+__global__ __launch_bounds__(256) void wide_rows_kernel(FusedArgs p) {
+  using MF = Mfma<T>;
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int K = p.hidden, M = p.rows, N = p.n[0];
+  const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16;
+  if (n0 >= N) return;
+  const T* w = static_cast<const T*>(p.w[0]);
+  const int w_rows = min(16, N - n0);
+  const __amdgpu_buffer_rsrc_t rw =
+      make_rsrc(w + static_cast<int64_t>(n0) * K, static_cast<int64_t>(w_rows) * K * 2);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(
+      p.x, (static_cast<int64_t>(M) - 1) * p.x_rs * 2 + static_cast<int64_t>(K) * 2);
+  const int w_off = c * K * 2 + g * 16;
+  int x_off[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) x_off[i] = static_cast<int>((i * 16 + c) * p.x_rs * 2) + g * 16;
+  const int steps = (K + 31) / 32;
+  f32x4_t acc[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  uint4 wa[U], wb[U], xa[U][MB], xb[U][MB];
+  auto fetch = [&](int s0, uint4 (&wr)[U], uint4 (&xr)[U][MB]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = s0 + u;
+      const bool ok = s < steps && s * 32 + g * 8 < K;
+      wr[u] = ok ? buffer_load16(rw, w_off + s * 64) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+        xr[u][i] = ok ? buffer_load16(rx, x_off[i] + s * 64) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto multiply = [&](const uint4 (&wr)[U], const uint4 (&xr)[U][MB]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+        acc[i] = MF::run(__builtin_bit_cast(typename MF::vec, xr[u][i]),
+                         __builtin_bit_cast(typename MF::vec, wr[u]), acc[i]);
+  };
+  int s0 = 0;
+  fetch(s0, wa, xa);
+  while (s0 < steps) {
+    fetch(s0 + U, wb, xb);
+    multiply(wa, xa);
+    s0 += U;
+    if (s0 >= steps) break;
+    fetch(s0 + U, wa, xa);
+    multiply(wb, xb);
+    s0 += U;
+  }
+  // C layout: lane (col c = feature, rows 4g..4g+3 of block i).
+  const int n = n0 + c;
+  if (n >= N) return;
+  const float bias = p.bias[0] != nullptr ? slc::to_f32(static_cast<const T*>(p.bias[0])[n]) : 0.0f;
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = i * 16 + 4 * g + r;
+      if (m < M) {
+        float v = acc[i][r];
+        if (p.bias[0] != nullptr) v += bias;
+        static_cast<T*>(p.y[0])[m * p.y_rs[0] + n] = slc::from_f32<T>(v);
+      }
+    }
+}
+
+template <typename T>
+int launch_wide(FusedArgs& a, hipStream_t stream) {
+  const int blocks = (a.n[0] + 63) / 64;
+  if (a.rows <= 16) {
+    hipLaunchKernelGGL((wide_rows_kernel<T, 1, 8>), dim3(blocks), dim3(256), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((wide_rows_kernel<T, 2, 4>), dim3(blocks), dim3(256), 0, stream, a);
+  }
+  return slc_host::check_launch("decode linear (wide)");
+}
+
+// Split-K region of a stream: the first kSplitRegions distinct streams each
+// get one; later streams run without split-K (region -1).
+int split_region(hipStream_t stream) {
+  static std::mutex lock;
+  static hipStream_t owners[kSplitRegions];
+  static int used = 0;
+  std::lock_guard<std::mutex> guard(lock);
+  for (int i = 0; i < used; ++i)
+    if (owners[i] == stream) return i;
+  if (used == kSplitRegions) return -1;
+  owners[used] = stream;
+  return used++;
+}
+
+// Splits of K over workgroups for narrow projections (at most kSplitBlocks
+// feature blocks) with a long K (at least kSplitMinSteps k-steps; for short
+// K the cross-workgroup tail costs more than the split saves): up to
+// kMaxSplits, keeping at least 8 k-steps (one per wave) per split.  The count
+// depends on K alone, so a fused op and the single linears it replaces split
+// identically and agree bit for bit.
+constexpr int kSplitMinSteps = 64;
+int choose_splits(int blocks, int hidden, int epi, hipStream_t stream, int& region) {
+  region = 0;
+  const int steps = (hidden + 31) / 32;
+  if (epi == kSwiglu || blocks > kSplitBlocks || steps < kSplitMinSteps) return 1;
+  const int splits = kMaxSplits < steps / 8 ? kMaxSplits : steps / 8;
+  if (splits <= 1) return 1;
+  region = split_region(stream);
+  return region < 0 ? (region = 0, 1) : splits;
 }
 
 template <int EPI>
 int dispatch_rows(FusedArgs& a, int dtype, hipStream_t stream) {
+  a.splits = choose_splits(a.block_end[kMaxMatrices - 1], a.hidden, EPI, stream, a.region);
   const bool norm = a.norm_w != nullptr;
   const int nv = (a.hidden / 8 + 63) / 64;  // 16-byte vectors per lane
 #define SLC_ROWS(T)                                             \
@@ -377,6 +553,41 @@ __global__ __launch_bounds__(256) void rope_kv_store_kernel(
 }
 
 }  // namespace
+
+namespace slc_host {
+
+// Decode-sized plain linear (rows <= 32) for slc_hip_linear: the same kernel
+// as the fused ops, so fused and unfused graphs agree bit for bit.
+int rows_linear(const void* x, int64_t x_rs, int64_t rows, int64_t K, int64_t N,
+                const void* w, const void* bias, void* y, int64_t y_rs, int dtype,
+                hipStream_t stream) {
+  FusedArgs a{};
+  a.x = x;
+  a.x_rs = x_rs;
+  a.rows = static_cast<int>(rows);
+  a.hidden = static_cast<int>(K);
+  a.w[0] = w;
+  a.bias[0] = bias;
+  a.y[0] = y;
+  a.n[0] = static_cast<int>(N);
+  a.y_rs[0] = y_rs;
+  const int blocks = static_cast<int>((N + 15) / 16);
+  a.block_end[0] = a.block_end[1] = a.block_end[2] = blocks;
+  if (blocks >= kWideBlocks) {
+    return dtype == SLC_BF16 ? launch_wide<slc::bf16_t>(a, stream)
+                             : launch_wide<slc::f16_t>(a, stream);
+  }
+  return dispatch_rows<kStore>(a, dtype, stream);
+}
+
+bool rows_linear_eligible(const void* x, int64_t x_rs, int64_t rows, int64_t K, int64_t N,
+                          int dtype) {
+  return (dtype == SLC_BF16 || dtype == SLC_F16) && rows >= 1 && rows <= kMaxRows &&
+         K % 8 == 0 && K >= 8 && x_rs % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+         N <= (1 << 24);
+}
+
+}  // namespace slc_host
 
 extern "C" int slc_hip_norm_linear_group(
     const void* x, int64_t x_rs, const void* norm_weight, float epsilon, int64_t rows,

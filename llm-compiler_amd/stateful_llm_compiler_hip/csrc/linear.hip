@@ -19,6 +19,8 @@
 //    M uses 128 x 128 tiles (MFMA-bound).
 // fp32 (and shapes the vector path cannot take) use a classic LDS-tiled
 // FMA kernel.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace {
@@ -342,6 +344,10 @@ int launch_mfma(const void* x, const void* w, const void* bias, void* y, int M,
 template <typename T>
 int dispatch_mfma(const void* x, const void* w, const void* bias, void* y, int M,
                   int N, int K, int64_t x_rs, int64_t y_rs, hipStream_t s) {
+  // Up to 32 rows: the decode-step linear kernel the fused ops share.
+  const int dtype = sizeof(T) == 2 && std::is_same<T, slc::bf16_t>::value ? SLC_BF16 : SLC_F16;
+  if (M <= 32 && slc_host::rows_linear_eligible(x, x_rs, M, K, N, dtype))
+    return slc_host::rows_linear(x, x_rs, M, K, N, w, bias, y, y_rs, dtype, s);
   if (M <= 16) return launch_skinny<T, 1>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
   if (M <= 32) return launch_skinny<T, 2>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
   if (M <= 64) return launch_skinny<T, 4>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
