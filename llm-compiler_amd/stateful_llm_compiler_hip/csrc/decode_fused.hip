@@ -133,28 +133,6 @@ __global__ __launch_bounds__(KW * 64) void fused_rows_kernel(FusedArgs p) {
   unsigned char* xs = smem;
   float* partial = reinterpret_cast<float*>(smem + xs_bytes);  // [NW][kWaves][MB][64][4]
 
-  if constexpr (NV > 0) {
-    // Normalised input rows, exactly as the rms_norm kernel computes them.
-    constexpr int VEC = 16 / sizeof(T);
-    const T* x = static_cast<const T*>(p.x);
-    const T* nw = static_cast<const T*>(p.norm_w);
-    for (int m = wave; m < MB * 16; m += kWaves) {
-      uint4 out[NV];
-      if (m < M) {
-        slc::rms_norm_row<T, NV, true>(x + m * p.x_rs, nw, K, p.eps, lane, out);
-      } else {
-#pragma unroll
-        for (int i = 0; i < NV; ++i) out[i] = make_uint4(0, 0, 0, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int idx = lane + 64 * i;
-        if (idx < K / VEC)
-          *reinterpret_cast<uint4*>(xs + (m * norm_row(K) + idx * VEC) * 2) = out[i];
-      }
-    }
-    __syncthreads();
-  }
 
   // K range of this workgroup (its split), then of this wave.
   const int all_steps = (K + 31) / 32;             // 32-wide MFMA k-steps
@@ -230,6 +208,29 @@ __global__ __launch_bounds__(KW * 64) void fused_rows_kernel(FusedArgs p) {
 
   int s0 = s_begin;
   fetch(s0, wa, xa);
+  if constexpr (NV > 0) {
+    // Normalised input rows, exactly as the rms_norm kernel computes them
+    // (after the first weight loads are in flight: they do not depend on it).
+    constexpr int VEC = 16 / sizeof(T);
+    const T* x = static_cast<const T*>(p.x);
+    const T* nw = static_cast<const T*>(p.norm_w);
+    for (int m = wave; m < MB * 16; m += kWaves) {
+      uint4 out[NV];
+      if (m < M) {
+        slc::rms_norm_row<T, NV, true>(x + m * p.x_rs, nw, K, p.eps, lane, out);
+      } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) out[i] = make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int idx = lane + 64 * i;
+        if (idx < K / VEC)
+          *reinterpret_cast<uint4*>(xs + (m * norm_row(K) + idx * VEC) * 2) = out[i];
+      }
+    }
+    __syncthreads();
+  }
   while (s0 < s_end) {
     fetch(s0 + U, wb, xb);
     multiply(s0, wa, xa);
