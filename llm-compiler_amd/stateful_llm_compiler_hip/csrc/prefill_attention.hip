@@ -19,6 +19,8 @@
 //  * Causal: tiles entirely in a wave's future are skipped (and workgroups
 //    are launched heaviest-first); the diagonal tile is masked per element.
 // fp32 and other shapes take a simple wave-per-query kernel.
+#include <cmath>
+
 #include "common.hpp"
 
 namespace {
@@ -65,6 +67,10 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int 
 }
 
 constexpr int kD = 64;       // head dim of the MFMA kernel
+#ifndef SLC_PREFILL_GROUPED
+#define SLC_PREFILL_GROUPED 1
+#endif
+constexpr bool kUseGrouped = SLC_PREFILL_GROUPED != 0;
 constexpr int kKeys = 64;    // keys per tile
 constexpr int kQueries = 64; // queries per workgroup (4 waves x 16)
 constexpr int kRowBytes = kD * 2;
@@ -336,6 +342,346 @@ __global__ __launch_bounds__(256) void prefill_attention_generic_kernel(
   }
 }
 
+
+// ---- grouped-head kernel (v2) ------------------------------------------------
+// A workgroup owns 64 queries of ALL the query heads of one KV head (GQA
+// group G): G compute waves (one query head each, 64 queries = 4 MFMA column
+// blocks) plus one producer wave that streams the K, V (and mask) tiles of 64
+// keys into an LDS ring with direct-to-LDS loads.  K, V and the mask are thus
+// read once per workgroup for all G heads (the single-head kernel reads them
+// G times), and no VALU work or VGPR goes into staging.
+//  * S^T[key, query] = K . Q^T: K rows straight from the XOR-swizzled tile
+//    (ds_read_b128), Q^T in registers (4 query blocks reuse every K read).
+//  * O^T[dim, query] += V^T . P^T: V^T operands come from the natural V tile
+//    through the LDS transpose read (ds_read_b64_tr_b16), whose lane j of a
+//    16-lane group addresses 4 dims of key row T(j/4) and receives dim j of
+//    the 4 keys: two reads give the 8 keys in the P operand's slot order.
+//  * One barrier per tile: the producer waits for tile i, the barrier hands
+//    it to the consumers, then the producer refills the ring slot consumers
+//    released at that barrier.
+constexpr int kV2Queries = 64;
+constexpr int kV2Stages = 3;
+constexpr int kV2TileBytes = kKeys * kRowBytes;                 // 8 KB of K or of V
+// Mask tile: 64 query rows x 64 keys of the mask element type (0: no mask).
+template <int MK>
+constexpr int mask_elem_bytes() { return MK == 0 ? 0 : (MK == SLC_F32 + 1 ? 4 : 2); }
+template <int MK>
+constexpr int stage_bytes() { return 2 * kV2TileBytes + kV2Queries * kKeys * mask_elem_bytes<MK>(); }
+
+typedef short v4s_t __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, unsigned char* lds,
+                                          int voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      rsrc, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
+}
+__device__ __forceinline__ uint2 lds_read_tr(const unsigned char* p) {
+  const v4s_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s_t*)(p));
+  return __builtin_bit_cast(uint2, v);
+}
+
+// POW2: the softmax scale is a power of two (1/8 for head_dim 64), so
+// round(round(q.k) * scale) = round(q.k) * scale exactly and the second
+// rounding (and a multiply) can go.
+template <typename T, int G, int MK, bool CAUSAL, bool POW2>
+__global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
+    const T* __restrict__ query, const T* __restrict__ key, const T* __restrict__ value,
+    const void* __restrict__ mask, T* __restrict__ output, int tokens, int kv_heads,
+    int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t m_sb, int64_t m_sq, int64_t o_sb,
+    int64_t o_sh, int64_t o_st, float scale) {
+  using M = Mfma<T>;
+  constexpr int ME = mask_elem_bytes<MK>();
+  constexpr int kMaskRow = kKeys * ME;                 // bytes of one mask tile row
+  constexpr int kMaskTile = kV2Queries * kMaskRow;
+  __shared__ __attribute__((aligned(16))) unsigned char ring[kV2Stages][stage_bytes<MK>()];
+
+  const int nqb = gridDim.x;
+  const int qblk = CAUSAL ? nqb - 1 - static_cast<int>(blockIdx.x) : blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int g = lane >> 4;
+  const int c = lane & 15;
+  const int q0 = qblk * kV2Queries;
+  const float scale_log2e = scale * kLog2e;
+  const int key_end = CAUSAL ? min(q0 + kV2Queries, tokens) : tokens;
+  const int ntiles = (key_end + kKeys - 1) / kKeys;
+
+  if (wave == G) {
+    // ---- producer ---------------------------------------------------------
+    constexpr int kOps = (2 * kV2TileBytes + kMaskTile) / 1024;  // DMA ops per tile
+    const char* kbase = reinterpret_cast<const char*>(key + b * k_sb + kvh * k_sh);
+    const char* vbase = reinterpret_cast<const char*>(value + b * v_sb + kvh * v_sh);
+    const char* mbase = MK == 0 ? nullptr
+                                : static_cast<const char*>(mask) + (b * m_sb + static_cast<int64_t>(q0) * m_sq) * ME;
+    const int q_rows = min(kV2Queries, tokens - q0);
+    // Lane L of DMA instruction n fills LDS row 8n + L/8, chunk position L%8,
+    // with the global 16-byte chunk (L%8) ^ (row & 7) of that row.
+    auto issue = [&](int tile, int stage) {
+      unsigned char* dst = ring[stage];
+      const int k0 = tile * kKeys;
+      const int rows = tile < ntiles ? min(kKeys, tokens - k0) : 0;
+      const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + static_cast<int64_t>(k0) * k_st * 2,
+                                                  rows > 0 ? (static_cast<int64_t>(rows) - 1) * k_st * 2 + kRowBytes : 0);
+      const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + static_cast<int64_t>(k0) * v_st * 2,
+                                                  rows > 0 ? (static_cast<int64_t>(rows) - 1) * v_st * 2 + kRowBytes : 0);
+#pragma unroll
+      for (int n = 0; n < kV2TileBytes / 1024; ++n) {
+        const int row = 8 * n + lane / 8;
+        const int chunk = (lane % 8) ^ (row & 7);
+        lds_dma16(rk, dst + n * 1024, static_cast<int>(row * k_st * 2 + chunk * 16));
+        lds_dma16(rv, dst + kV2TileBytes + n * 1024, static_cast<int>(row * v_st * 2 + chunk * 16));
+      }
+      if constexpr (MK != 0) {
+        // Mask rows are queries, chunks 8 keys; whole rows stay inside the
+        // [T, T] plane (keys past T are masked as invalid anyway).
+        const int64_t bytes = tile < ntiles && q_rows > 0
+                                  ? ((static_cast<int64_t>(q_rows) - 1) * m_sq + tokens - k0) * ME
+                                  : 0;
+        const __amdgpu_buffer_rsrc_t rm = make_rsrc(mbase + static_cast<int64_t>(k0) * ME, bytes);
+#pragma unroll
+        for (int n = 0; n < kMaskTile / 1024; ++n) {
+          const int pos = n * 1024 + 16 * lane;
+          const int row = pos / kMaskRow;
+          const int chunk = ((pos % kMaskRow) >> 4) ^ (row & 7);
+          lds_dma16(rm, dst + 2 * kV2TileBytes + n * 1024, static_cast<int>(row * m_sq * ME + chunk * 16));
+        }
+      }
+    };
+#pragma unroll
+    for (int t = 0; t < kV2Stages - 1; ++t) issue(t, t);
+    for (int t = 0; t < ntiles; ++t) {
+      // Tile t landed: kStages - 2 later tiles (kOps each) may still fly.
+      asm volatile("s_waitcnt vmcnt(%0)" ::"i"((kV2Stages - 2) * kOps) : "memory");
+      __syncthreads();
+      issue(t + kV2Stages - 1, (t + kV2Stages - 1) % kV2Stages);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
+
+  // ---- consumers: wave w computes query head kvh * G + w ----------------------
+  const int h = kvh * G + wave;
+  typename M::vec qv[4][2];
+#pragma unroll
+  for (int qb = 0; qb < 4; ++qb) {
+    const int qrow = min(q0 + 16 * qb + c, tokens - 1);
+    const T* qp = query + b * q_sb + h * q_sh + static_cast<int64_t>(qrow) * q_st;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+      qv[qb][kk] = __builtin_bit_cast(typename M::vec,
+                                      *reinterpret_cast<const uint4*>(qp + kk * 32 + 8 * g));
+  }
+  float m_run[4], l_run[4];
+  f32x4_t acc[4][4];  // [dim block][query block]
+#pragma unroll
+  for (int qb = 0; qb < 4; ++qb) {
+    m_run[qb] = -INFINITY;
+    l_run[qb] = 0.0f;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) acc[db][qb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // Transpose-read lane addresses (bytes within a tile) for V^T blocks:
+  // lane j = c of group g reads key row 4g + j/4 (+16 for the second read)
+  // of a 32-key half, dims 16db + 4(j%4) .. +3.
+  int tr_off[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) {
+    const int row = 4 * g + (c >> 2);
+    const int dim = 16 * db + 4 * (c & 3);
+    tr_off[db] = row * kRowBytes + (((dim >> 3) ^ (row & 7)) << 4) + (dim & 7) * 2;
+  }
+  const int kv_off0 = c * kRowBytes;  // K operand row 16kb + c
+
+  for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();  // tile t is in ring[t % kStages]
+    const unsigned char* kt = ring[t % kV2Stages];
+    const unsigned char* vt = kt + kV2TileBytes;
+    const unsigned char* mt = kt + 2 * kV2TileBytes;  // mask tile, rows = queries
+    const int k0 = t * kKeys;
+
+    // S^T blocks: 4 key blocks x 4 query blocks.
+    f32x4_t st[4][4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      typename M::vec ka[2];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        ka[kk] = *reinterpret_cast<const typename M::vec*>(
+            kt + (16 * kb) * kRowBytes + kv_off0 + (((4 * kk + g) ^ (c & 7)) << 4));
+#pragma unroll
+      for (int qb = 0; qb < 4; ++qb) {
+        f32x4_t a = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        a = M::run(ka[0], qv[qb][0], a);
+        st[kb][qb] = M::run(ka[1], qv[qb][1], a);
+      }
+    }
+
+    // Scores (log2 units) with the reference's rounding, mask and validity.
+    const bool full = !CAUSAL ? k0 + kKeys <= tokens : k0 + kKeys <= q0 && k0 + kKeys <= tokens;
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb) {
+      const int my_query = q0 + 16 * qb + c;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        float mv[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (MK != 0) {
+          // Mask of keys 16kb + 4g .. +3 for this lane's query row.
+          const int row = 16 * qb + c;
+          const int byte = (16 * kb + 4 * g) * ME;
+          const unsigned char* mp = mt + row * kMaskRow + ((((byte >> 4) ^ (row & 7))) << 4) + (byte & 15);
+          if constexpr (ME == 4) {
+            const uint4 raw = *reinterpret_cast<const uint4*>(mp);
+            mv[0] = __uint_as_float(raw.x);
+            mv[1] = __uint_as_float(raw.y);
+            mv[2] = __uint_as_float(raw.z);
+            mv[3] = __uint_as_float(raw.w);
+          } else {
+            const uint2 raw = *reinterpret_cast<const uint2*>(mp);
+            const uint32_t w2[2] = {raw.x, raw.y};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const uint16_t bits = static_cast<uint16_t>(w2[r >> 1] >> (16 * (r & 1)));
+              if constexpr (MK == SLC_BF16 + 1) {
+                mv[r] = slc::to_f32(slc::bf16_t{bits});
+              } else {
+                mv[r] = slc::to_f32(slc::f16_t{bits});
+              }
+            }
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v;
+          if constexpr (POW2) {
+            v = slc::round_to<T>(st[kb][qb][r]) * scale_log2e;
+          } else {
+            v = slc::round_to<T>(slc::round_to<T>(st[kb][qb][r]) * scale) * kLog2e;
+          }
+          if constexpr (MK != 0) v = fmaf(mv[r], kLog2e, v);
+          if (!full) {
+            const int kidx = k0 + 16 * kb + 4 * g + r;
+            bool valid = kidx < tokens;
+            if constexpr (CAUSAL) valid = valid && kidx <= my_query;
+            v = valid ? v : -INFINITY;
+          }
+          st[kb][qb][r] = v;
+          mx = fmaxf(mx, v);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      if (__any(mx > m_run[qb] + kRescaleThreshold)) {
+        const float m_new = fmaxf(m_run[qb], mx);
+        const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - (m_new == -INFINITY ? 0.0f : m_new));
+        l_run[qb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) acc[db][qb] = acc[db][qb] * alpha;
+        m_run[qb] = m_new;
+      }
+    }
+
+    // P^T operands and O^T += V^T . P^T.
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      typename M::vec pv[4];
+#pragma unroll
+      for (int qb = 0; qb < 4; ++qb) {
+        const float m_use = m_run[qb] == -INFINITY ? 0.0f : m_run[qb];
+        u16x8 bits;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float p = __builtin_amdgcn_exp2f(st[2 * half + (i >> 2)][qb][i & 3] - m_use);
+          l_run[qb] += p;
+          bits.v[i] = bits_of<T>(p);
+        }
+        pv[qb] = __builtin_bit_cast(typename M::vec, bits);
+      }
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const uint2 lo = lds_read_tr(vt + half * 32 * kRowBytes + tr_off[db]);
+        const uint2 hi = lds_read_tr(vt + (half * 32 + 16) * kRowBytes + tr_off[db]);
+        const typename M::vec va = __builtin_bit_cast(typename M::vec, make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+        for (int qb = 0; qb < 4; ++qb) acc[db][qb] = M::run(va, pv[qb], acc[db][qb]);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int qb = 0; qb < 4; ++qb) {
+    float l = l_run[qb];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const int my_query = q0 + 16 * qb + c;
+    if (my_query < tokens) {
+      const float inv = 1.0f / l;
+      T* op = output + b * o_sb + h * o_sh + static_cast<int64_t>(my_query) * o_st;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        u16x8 e;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) e.v[r] = bits_of<T>(acc[db][qb][r] * inv);
+        uint2 packed;
+        packed.x = static_cast<uint32_t>(e.v[0]) | (static_cast<uint32_t>(e.v[1]) << 16);
+        packed.y = static_cast<uint32_t>(e.v[2]) | (static_cast<uint32_t>(e.v[3]) << 16);
+        *reinterpret_cast<uint2*>(op + 16 * db + 4 * g) = packed;
+      }
+    }
+  }
+}
+
+template <typename T, int G, int MK, bool CAUSAL>
+int launch_v2(const void* q, const void* k, const void* v, const void* mask, void* out,
+              int64_t batch, int tokens, int kv_heads, const int64_t* st, float scale,
+              hipStream_t stream) {
+  const dim3 grid((tokens + kV2Queries - 1) / kV2Queries, kv_heads, static_cast<unsigned>(batch));
+  int exponent = 0;
+  const bool pow2 = scale > 0.0f && std::frexp(scale, &exponent) == 0.5f && exponent > -100;
+  auto kernel = pow2 ? prefill_attention_v2_kernel<T, G, MK, CAUSAL, true>
+                     : prefill_attention_v2_kernel<T, G, MK, CAUSAL, false>;
+  hipLaunchKernelGGL(kernel, grid, dim3((G + 1) * 64), 0,
+                     stream, static_cast<const T*>(q), static_cast<const T*>(k),
+                     static_cast<const T*>(v), mask, static_cast<T*>(out), tokens, kv_heads,
+                     st[0], st[1], st[2], st[3], st[4], st[5], st[6], st[7], st[8], st[9], st[10],
+                     st[12], st[13], st[14], scale);
+  return slc_host::check_launch("slc_hip_prefill_attention(grouped)");
+}
+
+template <typename T, int G>
+int dispatch_v2(const void* q, const void* k, const void* v, const void* mask, int mask_dtype,
+                void* out, int64_t batch, int tokens, int kv_heads, int causal,
+                const int64_t* st, float scale, hipStream_t s) {
+#define SLC_V2(MKV)                                                                       \
+  return causal ? launch_v2<T, G, MKV, true>(q, k, v, mask, out, batch, tokens, kv_heads, st, scale, s) \
+                : launch_v2<T, G, MKV, false>(q, k, v, mask, out, batch, tokens, kv_heads, st, scale, s)
+  if (mask == nullptr) SLC_V2(0);
+  if (mask_dtype == SLC_BF16) SLC_V2(SLC_BF16 + 1);
+  if (mask_dtype == SLC_F16) SLC_V2(SLC_F16 + 1);
+  SLC_V2(SLC_F32 + 1);
+#undef SLC_V2
+}
+
+template <typename T>
+int try_v2(const void* q, const void* k, const void* v, const void* mask, int mask_dtype,
+           void* out, int64_t batch, int tokens, int kv_heads, int groups, int causal,
+           const int64_t* st, float scale, hipStream_t s) {
+  switch (groups) {
+    case 1: return dispatch_v2<T, 1>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, s);
+    case 2: return dispatch_v2<T, 2>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, s);
+    case 4: return dispatch_v2<T, 4>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, s);
+    case 7: return dispatch_v2<T, 7>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, s);
+    default: return dispatch_v2<T, 8>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, s);
+  }
+}
+
 template <typename T, int MK, bool CAUSAL>
 int launch_mfma(const void* q, const void* k, const void* v, const void* mask, void* out,
                 int64_t batch, int tokens, int q_heads, int groups, const int64_t* st,
@@ -418,6 +764,24 @@ extern "C" int slc_hip_prefill_attention(
   const bool mfma_ok = (dtype == SLC_BF16 || dtype == SLC_F16) && head_dim == kD &&
                        (bits & 15) == 0 && (strides & 7) == 0 && k_st >= kD && v_st >= kD &&
                        tokens * (k_st > v_st ? k_st : v_st) * 2 < (1LL << 31);
+  // The grouped kernel: GQA groups of 1, 2, 4, 7 or 8 heads, and a mask (if
+  // any) with unit key stride and 16-byte aligned rows.
+  const bool group_ok = groups == 1 || groups == 2 || groups == 4 || groups == 7 || groups == 8;
+  const int64_t me = mask == nullptr ? 0 : slc_host::dtype_size(mask_dtype);
+  const bool mask_ok =
+      mask == nullptr ||
+      (m_sk == 1 && (m_sq * me) % 16 == 0 && (m_sb * me) % 16 == 0 &&
+       (reinterpret_cast<uintptr_t>(mask) & 15) == 0 &&
+       ((tokens - 1) * m_sq + tokens) * me < (1LL << 31));
+  const bool out_ok = (reinterpret_cast<uintptr_t>(output) & 7) == 0 &&
+                      ((o_sb | o_sh | o_st) & 3) == 0;
+  if (mfma_ok && group_ok && mask_ok && out_ok && kv_heads <= 65535 && kUseGrouped) {
+    if (dtype == SLC_BF16)
+      return try_v2<slc::bf16_t>(query, key, value, mask, mask_dtype, output, batch, T_,
+                                 static_cast<int>(kv_heads), groups, causal, st, scale, s);
+    return try_v2<slc::f16_t>(query, key, value, mask, mask_dtype, output, batch, T_,
+                              static_cast<int>(kv_heads), groups, causal, st, scale, s);
+  }
   if (mfma_ok) {
     if (dtype == SLC_BF16) {
       return causal ? dispatch_mask<slc::bf16_t, true>(query, key, value, mask, mask_dtype, output, batch, T_, static_cast<int>(q_heads), groups, st, scale, s)

@@ -112,7 +112,8 @@ def test_linear_fp32(gpu, rows):
 # -------------------------------------------------------- prefill attention
 
 
-def _prefill_case(gpu, batch, tokens, dtype, seed, *, mask_kind, causal, q_heads=14, kv_heads=2, head_dim=64):
+def _prefill_case(gpu, batch, tokens, dtype, seed, *, mask_kind, causal, q_heads=14, kv_heads=2, head_dim=64,
+                  mask_dtype=torch.float32, scale=None):
     from stateful_llm_compiler_hip.backends import hip_prefill_attention
 
     g = generator(seed)
@@ -129,8 +130,11 @@ def _prefill_case(gpu, batch, tokens, dtype, seed, *, mask_kind, causal, q_heads
         mask = torch.zeros(batch, 1, tokens, tokens)
     else:
         mask = torch.randn(batch, 1, tokens, tokens, generator=g)
+    if mask is not None:
+        mask = mask.to(mask_dtype)
+    scale = head_dim**-0.5 if scale is None else scale
     expected = ref.prefill_attention(
-        q, k, v, mask, groups=q_heads // kv_heads, scale=head_dim**-0.5, causal=causal
+        q, k, v, mask, groups=q_heads // kv_heads, scale=scale, causal=causal
     )
 
     def dev(t):
@@ -138,7 +142,7 @@ def _prefill_case(gpu, batch, tokens, dtype, seed, *, mask_kind, causal, q_heads
 
     actual = hip_prefill_attention(
         dev(q), dev(k), dev(v), None if mask is None else mask.to(gpu),
-        scale=head_dim**-0.5, causal=causal,
+        scale=scale, causal=causal,
     )
     torch.cuda.synchronize()
     return actual.cpu(), expected
@@ -170,6 +174,35 @@ def test_prefill_bidirectional_zero_mask_bf16(gpu):
     # (test_prefill_attention.py:97-114).
     announce("prefill bf16 zero mask bidirectional")
     actual, expected = _prefill_case(gpu, 2, 80, torch.bfloat16, 7, mask_kind="zeros", causal=False)
+    assert_bf16_close(actual, expected)
+
+
+@pytest.mark.parametrize("q_heads,kv_heads", [(14, 2), (8, 1), (4, 4), (8, 4), (16, 4)])
+@pytest.mark.parametrize("tokens", [7, 64, 100, 257])
+@pytest.mark.parametrize("variant", ["causal-flag", "bf16-causal-mask", "f32-random-mask-causal", "f16-zeros"])
+def test_prefill_grouped_kernel(gpu, q_heads, kv_heads, tokens, variant):
+    # GQA groups of 7, 8, 1, 2 and 4 heads take the grouped-head kernel, with
+    # no mask, a 2-byte mask, or an fp32 mask (all with unit key stride).
+    announce(f"prefill grouped QH{q_heads} KVH{kv_heads} T={tokens} {variant}")
+    kind, causal, mdt = {
+        "causal-flag": ("none", True, torch.float32),
+        "bf16-causal-mask": ("causal", False, torch.bfloat16),
+        "f32-random-mask-causal": ("random", True, torch.float32),
+        "f16-zeros": ("zeros", False, torch.float16),
+    }[variant]
+    dtype = torch.float16 if variant == "f16-zeros" else torch.bfloat16
+    actual, expected = _prefill_case(gpu, 2, tokens, dtype, tokens + q_heads, mask_kind=kind, causal=causal,
+                                     q_heads=q_heads, kv_heads=kv_heads, mask_dtype=mdt)
+    assert_bf16_close(actual, expected)
+
+
+@pytest.mark.parametrize("scale", [0.1, 0.3, 0.25])
+def test_prefill_grouped_kernel_scale(gpu, scale):
+    # A scale that is not a power of two rounds the scaled score a second
+    # time; 0.25 takes the single-rounding path.
+    announce(f"prefill grouped scale={scale}")
+    actual, expected = _prefill_case(gpu, 2, 130, torch.bfloat16, 11, mask_kind="random", causal=True,
+                                     scale=scale)
     assert_bf16_close(actual, expected)
 
 
