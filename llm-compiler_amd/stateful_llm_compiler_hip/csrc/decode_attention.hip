@@ -551,7 +551,10 @@ int64_t choose_chunk(int64_t batch, int64_t kv_heads, int64_t mask_len,
   } else {
     const int64_t target_groups = 256;
     chunk = 2 * sweep;
-    while (batch * kv_heads * slc_host::ceil_div(mask_len, chunk) > target_groups) {
+    // Stop at one chunk per sequence: with more (batch, kv-head) pairs than
+    // the target the grid is already that wide.
+    while (chunk < mask_len &&
+           batch * kv_heads * slc_host::ceil_div(mask_len, chunk) > target_groups) {
       chunk *= 2;
     }
   }

@@ -193,6 +193,41 @@ def test_decode_attention_forced_split(gpu, split):
     assert_bf16_close(actual, expected)
 
 
+@pytest.mark.parametrize("split", [0, 32, 64, 100, 5000])
+@pytest.mark.parametrize("batch", [3, 65, 130])
+def test_decode_attention_balanced_split(gpu, batch, split):
+    # The length-balanced split lays every (batch, kv-head) tile range end to
+    # end: short sequences put several pairs into one workgroup, long ones
+    # spread over several workgroups, and a workgroup's range may start and
+    # end mid-sequence.  More than 64 sequences take several scan rounds.
+    announce(f"decode bf16 balanced split B={batch} split_tokens={split}")
+    g = generator(batch * 13 + split)
+    lengths = torch.randint(1, 200, (batch,), generator=g)
+    lengths[::7] = torch.randint(1, 33, lengths[::7].shape, generator=g)
+    lengths[1] = 256
+    actual, expected = _decode_case(
+        gpu, batch, 14, 2, 64, 256, lengths.tolist(), torch.bfloat16, batch + split,
+        split_tokens=split, mask_kind="random",
+    )
+    assert_bf16_close(actual, expected)
+
+
+@pytest.mark.parametrize("split", [0, 64])
+def test_decode_attention_empty_sequences(gpu, split):
+    # A sequence with no attended token is a softmax over an empty row: NaN,
+    # as in the reference; its neighbours are unaffected.
+    announce(f"decode bf16 empty sequences split_tokens={split}")
+    lengths = [0, 100, 0, 0, 37, 256, 0, 1]
+    actual, expected = _decode_case(
+        gpu, len(lengths), 14, 2, 64, 256, lengths, torch.bfloat16, 77, split_tokens=split,
+        mask_kind="random",
+    )
+    empty = torch.tensor(lengths) == 0
+    assert torch.isnan(expected[empty]).all()
+    assert torch.isnan(actual[empty]).all()
+    assert_bf16_close(actual[~empty], expected[~empty])
+
+
 @pytest.mark.parametrize("mask_dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("mask_len", [1000, 1001])
 def test_decode_attention_mask_dtype_and_length(gpu, mask_dtype, mask_len):
