@@ -103,9 +103,12 @@ def profiled_traffic() -> int | None:
     return None
 
 
-def dominant_kernel_us(call, reps: int) -> float:
-    """Mean duration of the dominant kernel of ``call()`` over ``reps`` eager
-    calls, from HIP events the library records around that kernel."""
+def dominant_kernel_us(call, reps: int, repeats: int = 20) -> float:
+    """Mean duration of one launch of the dominant kernel of ``call()``, from
+    HIP events the library records around it on its launch stream.  While the
+    events are armed the library launches that kernel ``repeats`` times back
+    to back (it rewrites the same outputs), so the launch latency of a single
+    call is amortised and the figure matches the profiler's kernel time."""
 
     from stateful_llm_compiler_hip import _native
 
@@ -116,13 +119,15 @@ def dominant_kernel_us(call, reps: int) -> float:
         e.record()
     torch.cuda.synchronize()
     try:
+        lib.slc_hip_set_timing_repeats(repeats)
         for b, e in pairs:
             lib.slc_hip_set_timing_events(b.cuda_event, e.cuda_event)
             call()
     finally:
         lib.slc_hip_set_timing_events(None, None)
+        lib.slc_hip_set_timing_repeats(1)
     torch.cuda.synchronize()
-    return 1e3 * sum(b.elapsed_time(e) for b, e in pairs) / reps
+    return 1e3 * sum(b.elapsed_time(e) for b, e in pairs) / reps / repeats
 
 
 def bench_decode_attention(steps: int, warmup: int, split_tokens: int) -> dict:
@@ -135,8 +140,11 @@ def bench_decode_attention(steps: int, warmup: int, split_tokens: int) -> dict:
     def step():
         return hip_decode_attention(q, k, v, lengths, mask, scale=D**-0.5, split_tokens=split_tokens)
 
-    # Warm the workspace and the library, then capture one step in a HIP graph
-    # so host launch overhead does not throttle a ~15 us kernel.
+    # Warm the workspace and the library, then capture steps in HIP graphs so
+    # host launch overhead does not throttle a ~20 us step: a graph of
+    # GRAPH_STEPS back-to-back steps (how a serving loop runs decode) and a
+    # one-step graph for the remainder, so the timed region runs exactly
+    # `steps` steps.
     for _ in range(3):
         step()
     torch.cuda.synchronize()
@@ -149,29 +157,34 @@ def bench_decode_attention(steps: int, warmup: int, split_tokens: int) -> dict:
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
+        for _ in range(GRAPH_STEPS):
+            out = step()
+    single = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(single):
         out = step()
-    for _ in range(warmup):
+    for _ in range(max(1, warmup // GRAPH_STEPS)):
         graph.replay()
     torch.cuda.synchronize()
 
-    # Per-step durations of the whole graph (split + merge kernels) with
-    # events on the replay stream.
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(min(steps, 200))]
+    # Per-step duration of the graphed steps (split + merge kernels and the
+    # gaps between launches) with events on the replay stream.
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(20)]
     for s, e in events:
         s.record()
         graph.replay()
         e.record()
     torch.cuda.synchronize()
-    step_us = 1e3 * sum(s.elapsed_time(e) for s, e in events) / len(events)
+    step_us = 1e3 * sum(s.elapsed_time(e) for s, e in events) / len(events) / GRAPH_STEPS
 
-    # Duration of the dominant (split-sequence) kernel alone: the library
-    # records the armed events right before and after it on the launch stream.
-    kernel_us = dominant_kernel_us(step, len(events))
+    # Duration of one launch of the dominant (split-sequence) kernel.
+    kernel_us = dominant_kernel_us(step, 100)
 
     torch.cuda.synchronize()
     start = time.perf_counter()
-    for _ in range(steps):
+    for _ in range(steps // GRAPH_STEPS):
         graph.replay()
+    for _ in range(steps % GRAPH_STEPS):
+        single.replay()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - start
     del out
@@ -187,6 +200,7 @@ def bench_decode_attention(steps: int, warmup: int, split_tokens: int) -> dict:
 
 
 MFMA_PEAK_TFLOPS = 2500.0  # dense bf16
+GRAPH_STEPS = 10  # decode-attention steps per graph replay
 
 
 def _time_graph(fn, reps: int = 20, outer: int = 5) -> float:

@@ -70,6 +70,14 @@ SLC_API const char* slc_hip_last_error(void);
 SLC_API void slc_hip_set_timing_events(void* begin, void* end);
 
 /*
+ * Measurement hook (no counterpart in the reference): while timing events are
+ * armed, launch the dominant kernel `repeats` times back to back between them
+ * (it rewrites the same outputs each time), so the per-launch average excludes
+ * the launch latency of a single call.  Default 1.
+ */
+SLC_API void slc_hip_set_timing_repeats(int repeats);
+
+/*
  * kv_store: scatter the current step's K/V rows into the preallocated
  * B x capacity x H x D buffers.
  *   key_buffer/value_buffer : [batch, capacity, heads, head_dim], contiguous

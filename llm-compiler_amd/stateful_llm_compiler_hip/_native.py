@@ -46,6 +46,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "slc_hip_version": (_I, []),
     "slc_hip_last_error": (ctypes.c_char_p, []),
     "slc_hip_set_timing_events": (None, [_P, _P]),
+    "slc_hip_set_timing_repeats": (None, [ctypes.c_int]),
     "slc_hip_kv_store": (
         _I,
         [_P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _P],

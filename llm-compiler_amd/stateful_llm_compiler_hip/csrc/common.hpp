@@ -105,6 +105,10 @@ int check_launch(const char* what);
 // with them on the launch stream.  Both are no-ops otherwise.
 void mark_kernel_begin(hipStream_t stream);
 void mark_kernel_end(hipStream_t stream);
+// Launches of the dominant kernel between the two events: the armed repeat
+// count (slc_hip_set_timing_repeats) while events are armed, else 1.  The
+// kernel must be idempotent for its inputs (it only rewrites its outputs).
+int timed_repeats();
 
 inline int dtype_size(int dtype) {
   switch (dtype) {

@@ -595,14 +595,16 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
                      static_cast<int>(st[3]), st[4], st[5],                   \
                      static_cast<int>(st[6]), st[7], st[8], scale,            \
                      static_cast<int>(chunk), static_cast<int>(nchunks))
-  if (mask == nullptr) {
-    SLC_MFMA(0);
-  } else if (mask_dtype == SLC_BF16) {
-    SLC_MFMA(SLC_BF16 + 1);
-  } else if (mask_dtype == SLC_F16) {
-    SLC_MFMA(SLC_F16 + 1);
-  } else {
-    SLC_MFMA(SLC_F32 + 1);
+  for (int rep = slc_host::timed_repeats(); rep > 0; --rep) {
+    if (mask == nullptr) {
+      SLC_MFMA(0);
+    } else if (mask_dtype == SLC_BF16) {
+      SLC_MFMA(SLC_BF16 + 1);
+    } else if (mask_dtype == SLC_F16) {
+      SLC_MFMA(SLC_F16 + 1);
+    } else {
+      SLC_MFMA(SLC_F32 + 1);
+    }
   }
 #undef SLC_MFMA
   slc_host::mark_kernel_end(stream);

@@ -8,6 +8,7 @@ namespace {
 thread_local char g_last_error[512] = "";
 thread_local hipEvent_t g_begin = nullptr;
 thread_local hipEvent_t g_end = nullptr;
+thread_local int g_repeats = 1;
 }
 
 namespace slc_host {
@@ -37,6 +38,8 @@ void mark_kernel_end(hipStream_t stream) {
   if (g_end != nullptr) hipEventRecord(g_end, stream);
 }
 
+int timed_repeats() { return g_begin != nullptr ? g_repeats : 1; }
+
 }  // namespace slc_host
 
 extern "C" int slc_hip_version(void) { return 100; }
@@ -47,3 +50,5 @@ extern "C" void slc_hip_set_timing_events(void* begin, void* end) {
   g_begin = static_cast<hipEvent_t>(begin);
   g_end = static_cast<hipEvent_t>(end);
 }
+
+extern "C" void slc_hip_set_timing_repeats(int repeats) { g_repeats = repeats > 1 ? repeats : 1; }
