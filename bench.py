@@ -368,6 +368,10 @@ def main() -> None:
     parser.add_argument("--no-model", action="store_true", help="skip the decode tok/s leg")
     parser.add_argument("--no-kernels", action="store_true", help="skip the other-op roofline table")
     parser.add_argument(
+        "--model-only", action="store_true",
+        help="only run the decode tok/s leg and print its numbers (for profiling the decode step)",
+    )
+    parser.add_argument(
         "--calibrate-copy", type=int, default=0, metavar="MIB",
         help="only run 5 plain device-to-device copies of MIB MiB (counter calibration)",
     )
@@ -389,6 +393,10 @@ def main() -> None:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibration_copy_bytes": src.numel()}))
+        return
+
+    if args.model_only:
+        print(json.dumps(bench_decode_tokens()))
         return
 
     result = bench_decode_attention(args.steps, args.warmup, args.split_tokens)
@@ -419,7 +427,7 @@ def main() -> None:
             "unit": "GB/s",
             "frac": round(result["achieved_gbs"] / HBM_PEAK_GBS, 4),
             "traffic": profiled_traffic(),
-            "kernel": "decode_attention_mfma_kernel (split-sequence); merge kernel separate",
+            "kernel": "decode_attention_mfma_kernel (split-sequence, partials merged by the last workgroup of each (batch, kv-head))",
             "kernel_us": round(result["kernel_us"], 3),
             "step_us_graph": round(result["step_us"], 3),
             "algorithmic_bytes": result["bytes"],

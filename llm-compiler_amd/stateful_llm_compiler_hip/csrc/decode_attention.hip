@@ -26,6 +26,8 @@
 //    the extra launch.)
 //  * Loops stop at the batch's own length, not at the capacity.
 // Other dtypes/shapes take a straightforward wave-per-token kernel.
+#include <mutex>
+
 #include "common.hpp"
 
 namespace {
@@ -116,6 +118,145 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int 
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 0));
 }
 
+// ---- merge inside the split kernel ------------------------------------------
+// With a counter region (one per stream, static device memory) every split
+// workgroup publishes its partial with agent-scope stores, waits for them to
+// complete and bumps its (batch, kv-head)'s counter; the workgroup that
+// completes the count merges the partials (agent-scope loads: they bypass the
+// non-coherent per-XCD caches) and re-arms the counter.  No release fence is
+// needed: the count is bumped only after this workgroup's stores completed.
+// The merge weighs the chunks exactly as the separate merge kernel does, so
+// both paths give bit-identical outputs.
+constexpr int kCounterRegions = 16;
+constexpr int kCounterPairs = 8192;  // (batch, kv-head) pairs per region
+__device__ int g_merge_counters[kCounterRegions][kCounterPairs];
+
+__device__ __forceinline__ void publish(float* p, float v, const int* counters) {
+  if (counters != nullptr) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    *p = v;
+  }
+}
+__device__ __forceinline__ float fetch_partial(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+constexpr int kFusedMergeUnroll = 8;
+template <typename T, int D>
+__device__ __forceinline__ void merge_if_last(const float* part_o, const float* part_ml,
+                                              T* output, int* counters, unsigned char* smem,
+                                              int64_t b, int kvh, int q_heads, int kv_heads,
+                                              int groups, int64_t o_sb, int64_t o_sh,
+                                              int nchunks) {
+  const int tid = threadIdx.x;
+  __shared__ int is_last;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores landed
+  __syncthreads();
+  if (tid == 0) {
+    int* counter = counters + b * kv_heads + kvh;
+    const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = before == nchunks - 1;
+    if (is_last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!is_last) return;
+  // One round of loads: each thread owns up to two outputs (head, d) and
+  // loads every chunk's (max, sum) of their heads and acc of their dims at
+  // once, then weighs them in chunk order exactly as the merge kernel does.
+  const int64_t head0 = b * q_heads + kvh * groups;
+  const int n_out = groups * D;
+  for (int base = 0; base < n_out; base += 2 * kThreads) {
+    int head[2], dim[2];
+    bool valid[2];
+#pragma unroll
+    for (int o = 0; o < 2; ++o) {
+      const int idx = base + tid + o * kThreads;
+      valid[o] = idx < n_out;
+      head[o] = valid[o] ? idx / D : 0;
+      dim[o] = idx % D;
+    }
+    float mmax[2] = {-INFINITY, -INFINITY};
+    float lsum[2] = {0.0f, 0.0f};
+    float acc[2] = {0.0f, 0.0f};
+    if (nchunks <= kFusedMergeUnroll) {
+      // Every chunk's (max, sum, acc) in one batch of loads.
+      float m[2][kFusedMergeUnroll], l[2][kFusedMergeUnroll], v[2][kFusedMergeUnroll];
+#pragma unroll
+      for (int o = 0; o < 2; ++o)
+#pragma unroll
+        for (int k = 0; k < kFusedMergeUnroll; ++k) {
+          const bool ok = valid[o] && k < nchunks;
+          const int64_t p = (head0 + head[o]) * nchunks + k;
+          m[o][k] = ok ? fetch_partial(part_ml + 2 * p) : -INFINITY;
+          l[o][k] = ok ? fetch_partial(part_ml + 2 * p + 1) : 0.0f;
+          v[o][k] = ok ? fetch_partial(part_o + p * D + dim[o]) : 0.0f;
+        }
+#pragma unroll
+      for (int o = 0; o < 2; ++o) {
+#pragma unroll
+        for (int k = 0; k < kFusedMergeUnroll; ++k) mmax[o] = fmaxf(mmax[o], m[o][k]);
+        const float mu = mmax[o] == -INFINITY ? 0.0f : mmax[o];
+#pragma unroll
+        for (int k = 0; k < kFusedMergeUnroll; ++k) {
+          if (k < nchunks) {
+            const float w = fast_exp2(m[o][k] - mu);  // exp2(-inf) = 0 for empty chunks
+            lsum[o] += w * l[o][k];
+            acc[o] += w * (w != 0.0f ? v[o][k] : 0.0f);
+          }
+        }
+      }
+    }
+    // More chunks: pass 1 (max) and pass 2 (weights), the loads of each batch
+    // of chunks issued before any is used.
+    for (int i0 = 0; nchunks > kFusedMergeUnroll && i0 < nchunks; i0 += kFusedMergeUnroll) {
+      float m[2][kFusedMergeUnroll];
+#pragma unroll
+      for (int o = 0; o < 2; ++o)
+#pragma unroll
+        for (int k = 0; k < kFusedMergeUnroll; ++k) {
+          const int64_t p = (head0 + head[o]) * nchunks + i0 + k;
+          m[o][k] = valid[o] && i0 + k < nchunks ? fetch_partial(part_ml + 2 * p) : -INFINITY;
+        }
+#pragma unroll
+      for (int o = 0; o < 2; ++o)
+#pragma unroll
+        for (int k = 0; k < kFusedMergeUnroll; ++k) mmax[o] = fmaxf(mmax[o], m[o][k]);
+    }
+    for (int i0 = 0; nchunks > kFusedMergeUnroll && i0 < nchunks; i0 += kFusedMergeUnroll) {
+      float m[2][kFusedMergeUnroll], l[2][kFusedMergeUnroll], v[2][kFusedMergeUnroll];
+#pragma unroll
+      for (int o = 0; o < 2; ++o)
+#pragma unroll
+        for (int k = 0; k < kFusedMergeUnroll; ++k) {
+          const bool ok = valid[o] && i0 + k < nchunks;
+          const int64_t p = (head0 + head[o]) * nchunks + i0 + k;
+          m[o][k] = ok ? fetch_partial(part_ml + 2 * p) : -INFINITY;
+          l[o][k] = ok ? fetch_partial(part_ml + 2 * p + 1) : 0.0f;
+          v[o][k] = ok ? fetch_partial(part_o + p * D + dim[o]) : 0.0f;
+        }
+#pragma unroll
+      for (int o = 0; o < 2; ++o) {
+        const float mu = mmax[o] == -INFINITY ? 0.0f : mmax[o];
+#pragma unroll
+        for (int k = 0; k < kFusedMergeUnroll; ++k) {
+          if (i0 + k < nchunks) {
+            const float w = fast_exp2(m[o][k] - mu);  // exp2(-inf) = 0 for empty chunks
+            lsum[o] += w * l[o][k];
+            acc[o] += w * (w != 0.0f ? v[o][k] : 0.0f);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 0; o < 2; ++o) {
+      if (!valid[o]) continue;
+      const int qh = kvh * groups + head[o];
+      output[b * o_sb + qh * o_sh + dim[o]] = slc::from_f32<T>(acc[o] * (1.0f / lsum[o]));
+    }
+  }
+}
+
 // Rescale the running (max, sum, acc) only when a tile's max exceeds the
 // running max by more than this (log2 units): probabilities stay <= 2^8, and
 // most tiles skip the accumulator rescale entirely.
@@ -133,7 +274,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     int64_t capacity, int64_t mask_len, int64_t q_sb, int64_t q_sh,
     int64_t kv_sb, int kv_ss, int64_t kv_sh, int64_t m_sb, int m_ss,
     int64_t o_sb, int64_t o_sh, float scale, int chunk_tokens,
-    int nchunks) {
+    int nchunks, int* __restrict__ counters) {
   using M = Mfma<T>;
   using Layout = SharedLayout<T, D>;
   constexpr int KK = D / 32;            // MFMA k-steps over head_dim
@@ -164,9 +305,12 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     // merges to 0/0 = NaN, like the reference's softmax over an all -inf row.
     if (tid < groups) {
       const int64_t p = (b * q_heads + kvh * groups + tid) * nchunks + chunk;
-      part_ml[2 * p] = -INFINITY;
-      part_ml[2 * p + 1] = 0.0f;
+      publish(part_ml + 2 * p, -INFINITY, counters);
+      publish(part_ml + 2 * p + 1, 0.0f, counters);
     }
+    if (counters != nullptr)
+      merge_if_last<T, D>(part_o, part_ml, output, counters, smem, b, kvh, q_heads, kv_heads,
+                          groups, o_sb, o_sh, nchunks);
     return;
   }
   const int chunk_end = min(chunk_start + chunk_tokens, end);
@@ -379,12 +523,17 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
       output[b * o_sb + qh * o_sh + d] = slc::from_f32<T>(osum / lsum);
     } else {
       const int64_t p = (b * q_heads + qh) * nchunks + chunk;
-      part_o[p * D + d] = osum;
+      publish(part_o + p * D + d, osum, counters);
       if (d == 0) {
-        part_ml[2 * p] = mmax;
-        part_ml[2 * p + 1] = lsum;
+        publish(part_ml + 2 * p, mmax, counters);
+        publish(part_ml + 2 * p + 1, lsum, counters);
       }
     }
+  }
+  if (nchunks > 1 && counters != nullptr) {
+    __syncthreads();  // the merge reuses the LDS
+    merge_if_last<T, D>(part_o, part_ml, output, counters, smem, b, kvh, q_heads, kv_heads,
+                        groups, o_sb, o_sh, nchunks);
   }
 }
 
@@ -567,6 +716,42 @@ int64_t choose_chunk(int64_t batch, int64_t kv_heads, int64_t mask_len,
 //   float part_o[batch * q_heads * nchunks * D]
 //   float part_ml[batch * q_heads * nchunks * 2]
 
+#ifndef SLC_DECODE_FUSED_MERGE
+#define SLC_DECODE_FUSED_MERGE 1
+#endif
+
+// Counter region of a stream for the in-kernel merge: the first
+// kCounterRegions distinct streams each get one (calls on one stream run in
+// order, so they never share counters concurrently); later streams use the
+// separate merge kernel.
+int counter_region(hipStream_t stream) {
+  static std::mutex lock;
+  static hipStream_t owners[kCounterRegions];
+  static int used = 0;
+  std::lock_guard<std::mutex> guard(lock);
+  for (int i = 0; i < used; ++i)
+    if (owners[i] == stream) return i;
+  if (used == kCounterRegions) return -1;
+  owners[used] = stream;
+  return used++;
+}
+
+// Device address of a region's counters on the current device (each device
+// holds its own copy of the static array), or nullptr if it cannot be found.
+int* merge_counters(int region) {
+  static std::mutex lock;
+  static int* base[64] = {};
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return nullptr;
+  std::lock_guard<std::mutex> guard(lock);
+  if (base[device] == nullptr) {
+    void* address = nullptr;
+    if (hipGetSymbolAddress(&address, HIP_SYMBOL(g_merge_counters)) != hipSuccess) return nullptr;
+    base[device] = static_cast<int*>(address);
+  }
+  return base[device] + static_cast<int64_t>(region) * kCounterPairs;
+}
+
 template <typename T, int D>
 int launch_mfma(const void* query, const void* kb, const void* vb,
                 const void* lengths, int lengths_dtype, const void* mask,
@@ -583,6 +768,14 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
   const int groups = static_cast<int>(q_heads / kv_heads);
   const dim3 grid(static_cast<unsigned>(nchunks), static_cast<unsigned>(kv_heads),
                   static_cast<unsigned>(batch));
+  // Merge inside the split kernel when this stream has a counter region and
+  // the chunk weights fit the kernel's LDS; else the separate merge kernel.
+  int* counters = nullptr;
+  if (nchunks > 1 && SLC_DECODE_FUSED_MERGE && batch * kv_heads <= kCounterPairs &&
+      (2 * groups * nchunks + groups) * 4 <= SharedLayout<T, D>::kBytes) {
+    const int region = counter_region(stream);
+    if (region >= 0) counters = merge_counters(region);
+  }
   slc_host::mark_kernel_begin(stream);
 #define SLC_MFMA(MK)                                                          \
   hipLaunchKernelGGL((decode_attention_mfma_kernel<T, D, MK>), grid, dim3(kThreads), \
@@ -594,7 +787,7 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
                      groups, capacity, mask_len, st[0], st[1], st[2],         \
                      static_cast<int>(st[3]), st[4], st[5],                   \
                      static_cast<int>(st[6]), st[7], st[8], scale,            \
-                     static_cast<int>(chunk), static_cast<int>(nchunks))
+                     static_cast<int>(chunk), static_cast<int>(nchunks), counters)
   for (int rep = slc_host::timed_repeats(); rep > 0; --rep) {
     if (mask == nullptr) {
       SLC_MFMA(0);
@@ -609,7 +802,7 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
 #undef SLC_MFMA
   slc_host::mark_kernel_end(stream);
   int rc = slc_host::check_launch("slc_hip_decode_attention");
-  if (rc != SLC_OK || nchunks == 1) return rc;
+  if (rc != SLC_OK || nchunks == 1 || counters != nullptr) return rc;
   hipLaunchKernelGGL((decode_attention_merge_kernel<T, D>),
                      dim3(static_cast<unsigned>(batch * kv_heads)), dim3(256), 0,
                      stream, part_o, part_ml, static_cast<T*>(output),

@@ -391,3 +391,31 @@ def test_rope_other_dtypes_bitexact(gpu, dtype):
     torch.cuda.synchronize()
     assert_bitwise_equal(aq, eq)
     assert_bitwise_equal(ak, ek)
+
+
+def test_decode_attention_merge_in_kernel_matches_merge_kernel(gpu):
+    # The split kernel merges in its last workgroup per (batch, kv-head) when
+    # the stream owns a counter region (16 streams do); further streams use
+    # the separate merge kernel.  Both weigh the chunks identically, so all
+    # streams must agree bit for bit, call after call.
+    from stateful_llm_compiler_hip.backends import hip_decode_attention
+
+    announce("decode bf16 in-kernel merge vs merge kernel over 20 streams")
+    g = generator(91)
+    batch, cap = 8, 2048
+    q = torch.randn(batch, 14, 1, 64, generator=g).bfloat16().to(gpu)
+    k = torch.randn(batch, cap, 2, 64, generator=g).bfloat16().to(gpu)
+    v = torch.randn(batch, cap, 2, 64, generator=g).bfloat16().to(gpu)
+    lengths = torch.randint(1, cap + 1, (batch,), generator=g).to(gpu)
+    lengths[0] = 0  # an empty sequence: NaN on both paths
+    mask = torch.randn(batch, 1, 1, cap, generator=g).bfloat16().to(gpu)
+    outs = []
+    for _ in range(20):
+        stream = torch.cuda.Stream()
+        with torch.cuda.stream(stream):
+            for _ in range(2):
+                out = hip_decode_attention(q, k, v, lengths, mask, scale=0.125)
+        stream.synchronize()
+        outs.append(out.cpu())
+    for out in outs[1:]:
+        assert torch.equal(out.view(torch.int16), outs[0].view(torch.int16))
