@@ -9,6 +9,8 @@
 //                                                     (execution.py:421-443)
 //   argmax      greedy next token over the vocabulary
 // Every op is one launch of 16-byte vector accesses where the layout allows.
+#include <algorithm>
+
 #include "common.hpp"
 #include "op_math.hpp"
 
@@ -151,32 +153,34 @@ __device__ __forceinline__ bool argmax_better(float v, int64_t i, float best, in
   return i < best_i;
 }
 
-template <typename T>
-__global__ __launch_bounds__(1024) void argmax_kernel(const T* __restrict__ logits,
-                                                      int64_t* __restrict__ out, int64_t cols,
-                                                      int64_t row_stride, int vector_ok) {
-  __shared__ float sv[16];
-  __shared__ int64_t si[16];
+// Best (value, index) of row[begin, end) over the workgroup: each thread
+// scans 16-byte vectors (or elements), then waves and workgroup reduce.
+// Returns the result in every thread of wave 0 (thread 0 is authoritative).
+template <typename T, int THREADS>
+__device__ __forceinline__ void row_segment_best(const T* row, int64_t begin, int64_t end,
+                                                 bool vector_ok, float& best, int64_t& best_i) {
+  __shared__ float sv[THREADS / 64];
+  __shared__ int64_t si[THREADS / 64];
   constexpr int VEC = 16 / sizeof(T);
-  const int64_t r = blockIdx.x;
-  const T* row = logits + r * row_stride;
-  float best = -INFINITY;
-  int64_t best_i = INT64_MAX;
-  int64_t done = 0;
+  best = -INFINITY;
+  best_i = INT64_MAX;
+  int64_t done = begin;
   if (vector_ok) {
-    const int64_t nvec = cols / VEC;
+    // begin is a multiple of VEC (the host aligns segments).
+    const int64_t v0 = begin / VEC;
+    const int64_t v1 = end / VEC;
     const uint4* vrow = reinterpret_cast<const uint4*>(row);
-    for (int64_t base = threadIdx.x; base < nvec; base += 4 * 1024) {
+    for (int64_t base = v0 + threadIdx.x; base < v1; base += 4 * THREADS) {
       uint4 raw[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int64_t j = base + u * 1024;
-        raw[u] = j < nvec ? vrow[j] : make_uint4(0, 0, 0, 0);
+        const int64_t j = base + u * THREADS;
+        raw[u] = j < v1 ? vrow[j] : make_uint4(0, 0, 0, 0);
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int64_t j = base + u * 1024;
-        if (j >= nvec) break;
+        const int64_t j = base + u * THREADS;
+        if (j >= v1) break;
         const T* e = reinterpret_cast<const T*>(&raw[u]);
 #pragma unroll
         for (int k = 0; k < VEC; ++k) {
@@ -188,9 +192,9 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const T* __restrict__ logi
         }
       }
     }
-    done = nvec * VEC;
+    done = v1 * VEC;
   }
-  for (int64_t i = done + threadIdx.x; i < cols; i += 1024) {
+  for (int64_t i = done + threadIdx.x; i < end; i += THREADS) {
     const float v = slc::to_f32(row[i]);
     if (argmax_better(v, i, best, best_i)) {
       best = v;
@@ -211,14 +215,93 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const T* __restrict__ logi
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < 16; ++w) {
+    for (int w = 1; w < THREADS / 64; ++w) {
       if (argmax_better(sv[w], si[w], best, best_i)) {
         best = sv[w];
         best_i = si[w];
       }
     }
-    out[r] = best_i < cols ? best_i : 0;
   }
+}
+
+template <typename T>
+__global__ __launch_bounds__(1024) void argmax_kernel(const T* __restrict__ logits,
+                                                      int64_t* __restrict__ out, int64_t cols,
+                                                      int64_t row_stride, int vector_ok) {
+  const int64_t r = blockIdx.x;
+  float best;
+  int64_t best_i;
+  row_segment_best<T, 1024>(logits + r * row_stride, 0, cols, vector_ok != 0, best, best_i);
+  if (threadIdx.x == 0) out[r] = best_i < cols ? best_i : 0;
+}
+
+// Wide rows: `segs` workgroups per row each reduce one segment and publish
+// (value, index) with agent-scope stores; the workgroup that completes the
+// row's count (per-stream counter region) combines the segments in order and
+// re-arms the counter.  Ties keep the lowest index because segments are
+// combined in index order with the same comparison.
+constexpr int kArgmaxRegions = 16;
+constexpr int kArgmaxRows = 256;
+constexpr int kArgmaxSegs = 64;
+constexpr int kArgmaxThreads = 256;
+__device__ int g_argmax_counters[kArgmaxRegions][kArgmaxRows];
+__device__ float g_argmax_value[kArgmaxRegions][kArgmaxRows * kArgmaxSegs];
+__device__ int64_t g_argmax_index[kArgmaxRegions][kArgmaxRows * kArgmaxSegs];
+
+template <typename T>
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_split_kernel(
+    const T* __restrict__ logits, int64_t* __restrict__ out, int64_t cols, int64_t row_stride,
+    int vector_ok, int64_t seg_len, int region) {
+  const int seg = blockIdx.x;
+  const int segs = gridDim.x;
+  const int r = blockIdx.y;
+  const int64_t begin = seg * seg_len;
+  const int64_t end = begin + seg_len < cols ? begin + seg_len : cols;
+  float best;
+  int64_t best_i;
+  row_segment_best<T, kArgmaxThreads>(logits + r * row_stride, begin, end, vector_ok != 0,
+                                      best, best_i);
+  __shared__ int is_last;
+  if (threadIdx.x == 0) {
+    const int slot = r * kArgmaxSegs + seg;
+    __hip_atomic_store(&g_argmax_value[region][slot], best, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&g_argmax_index[region][slot], best_i, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // published before counting
+    const int before = __hip_atomic_fetch_add(&g_argmax_counters[region][r], 1, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+    is_last = before == segs - 1;
+    if (is_last)
+      __hip_atomic_store(&g_argmax_counters[region][r], 0, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!is_last || threadIdx.x >= 64) return;
+  // Wave 0 combines: lane s holds segment s (and s + 64 ...), then a
+  // lowest-index-first reduction.
+  float v = -INFINITY;
+  int64_t i = INT64_MAX;
+  for (int s = threadIdx.x; s < segs; s += 64) {
+    const int slot = r * kArgmaxSegs + s;
+    const float sv = __hip_atomic_load(&g_argmax_value[region][slot], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+    const int64_t si = __hip_atomic_load(&g_argmax_index[region][slot], __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    if (argmax_better(sv, si, v, i)) {
+      v = sv;
+      i = si;
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(v, off, 64);
+    const int64_t oi = __shfl_xor(i, off, 64);
+    if (argmax_better(ov, oi, v, i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+  if (threadIdx.x == 0) out[r] = i < cols ? i : 0;
 }
 
 template <typename T>
@@ -355,9 +438,32 @@ extern "C" int slc_hip_argmax(const void* logits, int64_t* output, int dtype, in
   if (rows == 0) return SLC_OK;
   SLC_REQUIRE(logits && output, "slc_hip_argmax: null pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>(rows));
   const int64_t es = slc_host::dtype_size(dtype);
   const int vector_ok = (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (row_stride * es) % 16 == 0;
+  // Wide rows split over several workgroups per row (about one per CU in
+  // total, segments of at least 4096 elements) when the stream owns a
+  // counter region; else one 1024-thread workgroup per row.
+  const int64_t vec = 16 / es;
+  int64_t segs = std::min<int64_t>(kArgmaxSegs, std::max<int64_t>(1, 256 / rows));
+  segs = std::min<int64_t>(segs, std::max<int64_t>(1, cols / 4096));
+  const int region = segs > 1 && rows <= kArgmaxRows ? slc_host::stream_region(slc_host::kRegionArgmax, s) : -1;
+  if (region >= 0) {
+    const int64_t seg_len = slc_host::ceil_div(slc_host::ceil_div(cols, segs), vec) * vec;
+    segs = slc_host::ceil_div(cols, seg_len);
+    const dim3 grid(static_cast<unsigned>(segs), static_cast<unsigned>(rows));
+#define SLC_ARGMAX_SPLIT(TT)                                                                  \
+  hipLaunchKernelGGL((argmax_split_kernel<TT>), grid, dim3(kArgmaxThreads), 0, s,            \
+                     static_cast<const TT*>(logits), output, cols, row_stride, vector_ok, seg_len, \
+                     region)
+    switch (dtype) {
+      case SLC_BF16: SLC_ARGMAX_SPLIT(slc::bf16_t); break;
+      case SLC_F16: SLC_ARGMAX_SPLIT(slc::f16_t); break;
+      default: SLC_ARGMAX_SPLIT(float);
+    }
+#undef SLC_ARGMAX_SPLIT
+    return slc_host::check_launch("slc_hip_argmax");
+  }
+  const dim3 grid(static_cast<unsigned>(rows));
   switch (dtype) {
     case SLC_BF16:
       hipLaunchKernelGGL((argmax_kernel<slc::bf16_t>), grid, dim3(1024), 0, s,

@@ -115,3 +115,24 @@ def test_argmax_matches_torch(gpu, dtype):
     out = hip_argmax(logits.to(gpu))
     torch.cuda.synchronize()
     assert torch.equal(out.cpu(), logits.argmax(-1))
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 151936), (8, 151936), (3, 50001), (300, 8192), (2, 100)])
+def test_argmax_segments_ties_and_nan(gpu, rows, cols):
+    # Wide rows are reduced by several workgroups per row (segments combined
+    # in index order by the last one): ties across segment boundaries keep the
+    # first index, a NaN wins like torch.argmax, odd widths end mid-vector.
+    from stateful_llm_compiler_hip.backends import hip_argmax
+
+    announce(f"argmax segments rows={rows} cols={cols}")
+    g = generator(rows + cols)
+    logits = torch.randn(rows, cols, generator=g).bfloat16()
+    logits[0, cols - 1] = 50.0
+    logits[0, cols // 2] = 50.0       # tie in a later and an earlier segment
+    if rows > 1:
+        logits[1, cols // 3] = float("nan")
+        logits[1, cols - 2] = float("nan")
+    for _ in range(3):  # the per-row counters re-arm between calls
+        out = hip_argmax(logits.to(gpu))
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), logits.argmax(-1))
