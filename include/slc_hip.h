@@ -255,6 +255,12 @@ SLC_API int slc_hip_argmax(const void* logits, int64_t* output, int dtype, int64
  *                       at or past the capacity are skipped and set *overflow
  *                       (triton_rope.py:299-390 then triton_kv.py:71-129).
  *                       Buffers are contiguous [B, capacity, kv_heads, D].
+ *                       With lengths_out set it also advances the lengths:
+ *                       lengths_out[b] = positions[b] + advance (in place
+ *                       allowed), flagging *overflow past the capacity, as
+ *                       slc_hip_kv_advance does after the store (the
+ *                       runtime.kv.advance that follows the store in the
+ *                       decode graph, execution.py:741-767).
  */
 SLC_API int slc_hip_norm_linear_group(
     const void* x, int64_t x_rs, const void* norm_weight, float epsilon, int64_t rows,
@@ -274,11 +280,11 @@ SLC_API int slc_hip_linear_residual(const void* x, int64_t x_rs, int64_t rows,
 SLC_API int slc_hip_rope_kv_store(
     const void* query, const void* key, const void* value, const void* cosine,
     const void* sine, void* query_out, void* key_buffer, void* value_buffer,
-    const int64_t* positions, int* overflow, int dtype, int64_t batch, int64_t q_heads,
-    int64_t kv_heads, int64_t tokens, int64_t head_dim, int64_t capacity, int64_t q_sb,
-    int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t v_sb,
-    int64_t v_sh, int64_t v_st, int64_t cos_sb, int64_t cos_st, int64_t sin_sb,
-    int64_t sin_st, int64_t qo_sb, int64_t qo_sh, int64_t qo_st, void* stream);
+    const int64_t* positions, int* overflow, int64_t* lengths_out, int64_t advance, int dtype,
+    int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t tokens, int64_t head_dim,
+    int64_t capacity, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh,
+    int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t cos_sb, int64_t cos_st,
+    int64_t sin_sb, int64_t sin_st, int64_t qo_sb, int64_t qo_sh, int64_t qo_st, void* stream);
 
 #ifdef __cplusplus
 }

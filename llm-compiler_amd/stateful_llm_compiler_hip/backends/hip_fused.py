@@ -167,10 +167,14 @@ def hip_rope_kv_store(
     positions: torch.Tensor,
     *,
     overflow: torch.Tensor | None = None,
+    advance: int = 0,
+    lengths_out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """``q_rot, k_rot = rope(query, key, cosine, sine)``; store ``k_rot`` and
     ``value`` rows at ``positions[b] + t`` of the [B, Cap, H, D] buffers;
-    return ``q_rot``."""
+    return ``q_rot``.  With ``advance > 0`` also write
+    ``lengths_out = positions + advance`` (``lengths_out`` may be
+    ``positions``), as the kv advance after the store would."""
 
     tensors = (query, key, value, cosine, sine, key_buffer, value_buffer, positions)
     if not all(t.is_cuda for t in tensors):
@@ -196,11 +200,21 @@ def hip_rope_kv_store(
     if len(dtypes) != 1:
         raise ValueError("HIP rope_kv_store: dtypes must match")
     q_out = torch.empty((batch, q_heads, tokens, head_dim), device=query.device, dtype=query.dtype)
-    positions = positions.contiguous()
+    if advance < 0 or (advance > 0) != (lengths_out is not None):
+        raise ValueError("HIP rope_kv_store: advance > 0 needs lengths_out (and only then)")
+    if lengths_out is not None and (lengths_out.shape != (batch,) or lengths_out.dtype != torch.int64
+                                    or not lengths_out.is_cuda or not lengths_out.is_contiguous()):
+        raise ValueError("HIP rope_kv_store: lengths_out must be a contiguous [batch] int64 GPU tensor")
+    if not positions.is_contiguous():
+        if lengths_out is not None and lengths_out.data_ptr() == positions.data_ptr():
+            raise ValueError("HIP rope_kv_store: in-place advance needs contiguous positions")
+        positions = positions.contiguous()
     status = _native.library().slc_hip_rope_kv_store(
         query.data_ptr(), key.data_ptr(), value.data_ptr(), cosine.data_ptr(), sine.data_ptr(),
         q_out.data_ptr(), key_buffer.data_ptr(), value_buffer.data_ptr(), positions.data_ptr(),
-        None if overflow is None else overflow.data_ptr(), _native.dtype_tag(query.dtype),
+        None if overflow is None else overflow.data_ptr(),
+        None if lengths_out is None else lengths_out.data_ptr(), int(advance),
+        _native.dtype_tag(query.dtype),
         batch, q_heads, kv_heads, tokens, head_dim, key_buffer.shape[1],
         query.stride(0), query.stride(1), query.stride(2),
         key.stride(0), key.stride(1), key.stride(2),

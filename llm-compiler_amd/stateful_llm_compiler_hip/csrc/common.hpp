@@ -116,7 +116,7 @@ int timed_repeats();
 // (calls on one stream run in order, so a region is never used by two calls
 // at once); further streams get -1 and take a path without such scratch.
 constexpr int kStreamRegions = 16;
-enum RegionKind { kRegionArgmax = 0, kRegionKinds = 1 };
+enum RegionKind { kRegionArgmax = 0, kRegionRopeStore = 1, kRegionKinds = 2 };
 int stream_region(RegionKind kind, hipStream_t stream);
 
 inline int dtype_size(int dtype) {

@@ -495,61 +495,91 @@ struct RopeStoreArgs {
 // heads (rotated into q_out), [QH, QH + KVH) key heads (rotated into the key
 // buffer row positions[b] + t), [QH + KVH, QH + 2 KVH) value heads (copied
 // into the value buffer).  Rows past the capacity are skipped and flagged.
+// Lengths advance folded into the store: with `lengths_out` set, every
+// workgroup counts itself done once all its threads have read their positions
+// (the per-stream counter), and the last one writes
+// lengths_out[b] = positions[b] + advance (in place is fine: every read
+// happened before the count completed), flags an advance past the capacity and
+// re-arms the counter.
+constexpr int kRopeStoreRegions = 16;
+__device__ int g_rope_store_counters[kRopeStoreRegions];
+
 template <typename T, int VEC>
 __global__ __launch_bounds__(256) void rope_kv_store_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ cosine, const T* __restrict__ sine, T* __restrict__ q_out,
     T* __restrict__ key_buffer, T* __restrict__ value_buffer,
-    const int64_t* __restrict__ positions, int* __restrict__ overflow, RopeStoreArgs a,
-    int64_t total) {
+    const int64_t* positions, int* __restrict__ overflow, RopeStoreArgs a,
+    int64_t total, int64_t* lengths_out, int64_t batch, int64_t advance, int region) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (gid >= total) return;
-  const int64_t per_row = a.half / VEC;
-  const int64_t d = (gid % per_row) * VEC;
-  int64_t rest = gid / per_row;
-  const int64_t t = rest % a.tokens;
-  rest /= a.tokens;
-  const int64_t heads = a.q_heads + 2 * a.kv_heads;
-  const int64_t h = rest % heads;
-  const int64_t b = rest / heads;
-  const int64_t D = 2 * a.half;
+  if (gid < total) {
+    const int64_t per_row = a.half / VEC;
+    const int64_t d = (gid % per_row) * VEC;
+    int64_t rest = gid / per_row;
+    const int64_t t = rest % a.tokens;
+    rest /= a.tokens;
+    const int64_t heads = a.q_heads + 2 * a.kv_heads;
+    const int64_t h = rest % heads;
+    const int64_t b = rest / heads;
+    const int64_t D = 2 * a.half;
 
-  const T* src;
-  T* dst;
-  if (h < a.q_heads) {
-    src = q + b * a.q_sb + h * a.q_sh + t * a.q_st;
-    dst = q_out + b * a.qo_sb + h * a.qo_sh + t * a.qo_st;
-  } else {
-    const int64_t position = positions[b] + t;
-    if (position < 0 || position >= a.capacity) {
-      if (overflow != nullptr) *overflow = 1;
-      return;
+    const T* src = nullptr;
+    T* dst = nullptr;
+    if (h < a.q_heads) {
+      src = q + b * a.q_sb + h * a.q_sh + t * a.q_st;
+      dst = q_out + b * a.qo_sb + h * a.qo_sh + t * a.qo_st;
+    } else {
+      const int64_t position = positions[b] + t;
+      if (position < 0 || position >= a.capacity) {
+        if (overflow != nullptr) *overflow = 1;
+      } else {
+        const bool is_key = h < a.q_heads + a.kv_heads;
+        const int64_t kh = is_key ? h - a.q_heads : h - a.q_heads - a.kv_heads;
+        const int64_t row = ((b * a.capacity + position) * a.kv_heads + kh) * D;
+        if (!is_key) {
+          const T* vs = v + b * a.v_sb + kh * a.v_sh + t * a.v_st;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            value_buffer[row + d + e] = vs[d + e];
+            value_buffer[row + d + a.half + e] = vs[d + a.half + e];
+          }
+        } else {
+          src = k + b * a.k_sb + kh * a.k_sh + t * a.k_st;
+          dst = key_buffer + row;
+        }
+      }
     }
-    const bool is_key = h < a.q_heads + a.kv_heads;
-    const int64_t kh = is_key ? h - a.q_heads : h - a.q_heads - a.kv_heads;
-    const int64_t row = ((b * a.capacity + position) * a.kv_heads + kh) * D;
-    if (!is_key) {
-      const T* vs = v + b * a.v_sb + kh * a.v_sh + t * a.v_st;
+    if (src != nullptr) {
+      const T* cr = cosine + b * a.c_sb + t * a.c_st;
+      const T* sr = sine + b * a.s_sb + t * a.s_st;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        value_buffer[row + d + e] = vs[d + e];
-        value_buffer[row + d + a.half + e] = vs[d + a.half + e];
+        float o1, o2;
+        slc::rope_pair<T>(slc::to_f32(src[d + e]), slc::to_f32(src[d + a.half + e]),
+                          slc::to_f32(cr[d + e]), slc::to_f32(cr[d + a.half + e]),
+                          slc::to_f32(sr[d + e]), slc::to_f32(sr[d + a.half + e]), o1, o2);
+        dst[d + e] = slc::from_f32<T>(o1);
+        dst[d + a.half + e] = slc::from_f32<T>(o2);
       }
-      return;
     }
-    src = k + b * a.k_sb + kh * a.k_sh + t * a.k_st;
-    dst = key_buffer + row;
   }
-  const T* cr = cosine + b * a.c_sb + t * a.c_st;
-  const T* sr = sine + b * a.s_sb + t * a.s_st;
-#pragma unroll
-  for (int e = 0; e < VEC; ++e) {
-    float o1, o2;
-    slc::rope_pair<T>(slc::to_f32(src[d + e]), slc::to_f32(src[d + a.half + e]),
-                      slc::to_f32(cr[d + e]), slc::to_f32(cr[d + a.half + e]),
-                      slc::to_f32(sr[d + e]), slc::to_f32(sr[d + a.half + e]), o1, o2);
-    dst[d + e] = slc::from_f32<T>(o1);
-    dst[d + a.half + e] = slc::from_f32<T>(o2);
+  if (lengths_out == nullptr) return;
+  __shared__ int is_last;
+  __syncthreads();  // every thread of this workgroup has read its positions
+  if (threadIdx.x == 0) {
+    const int before = __hip_atomic_fetch_add(&g_rope_store_counters[region], 1,
+                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = before == static_cast<int>(gridDim.x) - 1;
+    if (is_last)
+      __hip_atomic_store(&g_rope_store_counters[region], 0, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!is_last) return;
+  for (int64_t b = threadIdx.x; b < batch; b += blockDim.x) {
+    const int64_t next = positions[b] + advance;
+    lengths_out[b] = next;
+    if (overflow != nullptr && (next > a.capacity || next < 0)) *overflow = 1;
   }
 }
 
@@ -684,17 +714,23 @@ extern "C" int slc_hip_linear_residual(const void* x, int64_t x_rs, int64_t rows
 extern "C" int slc_hip_rope_kv_store(
     const void* query, const void* key, const void* value, const void* cosine,
     const void* sine, void* query_out, void* key_buffer, void* value_buffer,
-    const int64_t* positions, int* overflow, int dtype, int64_t batch, int64_t q_heads,
-    int64_t kv_heads, int64_t tokens, int64_t head_dim, int64_t capacity, int64_t q_sb,
-    int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t v_sb,
-    int64_t v_sh, int64_t v_st, int64_t cos_sb, int64_t cos_st, int64_t sin_sb,
-    int64_t sin_st, int64_t qo_sb, int64_t qo_sh, int64_t qo_st, void* stream) {
+    const int64_t* positions, int* overflow, int64_t* lengths_out, int64_t advance, int dtype,
+    int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t tokens, int64_t head_dim,
+    int64_t capacity, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh,
+    int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t cos_sb, int64_t cos_st,
+    int64_t sin_sb, int64_t sin_st, int64_t qo_sb, int64_t qo_sh, int64_t qo_st, void* stream) {
   const char* what = "slc_hip_rope_kv_store";
   SLC_REQUIRE(slc_host::is_float_dtype(dtype), "%s: bad dtype %d", what, dtype);
   SLC_REQUIRE(batch >= 0 && q_heads >= 0 && kv_heads >= 0 && tokens >= 0 && head_dim > 0 &&
                   head_dim % 2 == 0 && capacity >= 0,
               "%s: bad sizes", what);
-  if (batch == 0 || tokens == 0 || q_heads + kv_heads == 0) return SLC_OK;
+  SLC_REQUIRE(lengths_out == nullptr || advance > 0, "%s: advance must be positive", what);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (batch == 0) return SLC_OK;
+  if (tokens == 0 || q_heads + kv_heads == 0) {
+    if (lengths_out == nullptr) return SLC_OK;
+    return slc_hip_kv_advance(positions, lengths_out, batch, advance, capacity, overflow, stream);
+  }
   SLC_REQUIRE(query && key && value && cosine && sine && query_out && key_buffer &&
                   value_buffer && positions,
               "%s: null pointer", what);
@@ -704,15 +740,19 @@ extern "C" int slc_hip_rope_kv_store(
   const int64_t per_row = (head_dim / 2) % 4 == 0 ? head_dim / 8 : head_dim / 2;
   const int64_t total = batch * (q_heads + 2 * kv_heads) * tokens * per_row;
   const dim3 grid(static_cast<unsigned>(slc_host::ceil_div(total, 256)));
-  hipStream_t s = static_cast<hipStream_t>(stream);
   const bool vec4 = (head_dim / 2) % 4 == 0;
+  // The advance rides on the store kernel when this stream owns a counter
+  // region; otherwise it is its own launch after the store.
+  int region = -1;
+  if (lengths_out != nullptr) region = slc_host::stream_region(slc_host::kRegionRopeStore, s);
+  int64_t* fused_out = region >= 0 ? lengths_out : nullptr;
 #define SLC_RS(T, V)                                                                      \
   hipLaunchKernelGGL((rope_kv_store_kernel<T, V>), grid, dim3(256), 0, s,                \
                      static_cast<const T*>(query), static_cast<const T*>(key),           \
                      static_cast<const T*>(value), static_cast<const T*>(cosine),        \
                      static_cast<const T*>(sine), static_cast<T*>(query_out),            \
                      static_cast<T*>(key_buffer), static_cast<T*>(value_buffer), positions, \
-                     overflow, a, total)
+                     overflow, a, total, fused_out, batch, advance, region < 0 ? 0 : region)
   if (dtype == SLC_BF16) {
     if (vec4) SLC_RS(slc::bf16_t, 4); else SLC_RS(slc::bf16_t, 1);
   } else if (dtype == SLC_F16) {
@@ -721,5 +761,7 @@ extern "C" int slc_hip_rope_kv_store(
     if (vec4) SLC_RS(float, 4); else SLC_RS(float, 1);
   }
 #undef SLC_RS
-  return slc_host::check_launch(what);
+  const int rc = slc_host::check_launch(what);
+  if (rc != SLC_OK || lengths_out == nullptr || fused_out != nullptr) return rc;
+  return slc_hip_kv_advance(positions, lengths_out, batch, advance, capacity, overflow, stream);
 }

@@ -250,6 +250,33 @@ class PreallocatedKVCacheState:
                                   positions, overflow=self.overflow)
         return q_rot, self
 
+    def rope_store_advance(
+        self,
+        slot: int,
+        query: torch.Tensor,
+        key: torch.Tensor,
+        value: torch.Tensor,
+        cosine: torch.Tensor,
+        sine: torch.Tensor,
+        *,
+        delta: int,
+    ) -> tuple[torch.Tensor, "PreallocatedKVCacheState"]:
+        """``rope_store`` at this slot's lengths followed by ``advance(slot,
+        delta)``, in one kernel: the rotated query and the advanced state."""
+
+        if delta <= 0:
+            raise ExecutionError("KV advance delta must be positive")
+        positions = self.positions(slot)
+        buffer_key, buffer_value = self._validate_store(slot, key, value, positions)
+        out = positions if self.in_place_lengths else torch.empty_like(positions)
+        q_rot = hip_rope_kv_store(query, key, value, cosine, sine, buffer_key, buffer_value,
+                                  positions, overflow=self.overflow, advance=delta, lengths_out=out)
+        lengths = list(self.lengths)
+        lengths[slot] = out
+        zero = None if self.zero_slots is None else self.zero_slots - {slot}
+        return q_rot, replace(self, lengths=tuple(lengths), generation=self.generation + 1,
+                              zero_slots=zero)
+
     def prefill_store(
         self,
         slot: int,
@@ -494,8 +521,12 @@ class HipExecutor:
         state, query, key, value, cosine, sine, positions = operands
         if query.shape[-1] != int(attributes["head_dim"]):
             raise ExecutionError("kernel.hip.rope_kv_store head dim mismatch")
-        return state.rope_store(int(attributes.get("slot", 0)), query, key, value, cosine, sine,
-                                positions)
+        slot = int(attributes.get("slot", 0))
+        delta = int(attributes.get("advance", 0))
+        if delta:
+            # positions is this slot's length tensor (the fusion pass checks it).
+            return state.rope_store_advance(slot, query, key, value, cosine, sine, delta=delta)
+        return state.rope_store(slot, query, key, value, cosine, sine, positions)
 
     @staticmethod
     def _embedding(operands, attributes):

@@ -10,6 +10,7 @@ memory):
   rms_norm -> gate, up linears -> swiglu            kernel.hip.norm_linear_swiglu
   linear -> add (with a residual)                   kernel.hip.linear_residual
   rope -> kv_store of the rotated key               kernel.hip.rope_kv_store
+  rope_kv_store -> kv.advance of the same slot      kernel.hip.rope_kv_store (advance)
 
 A chain is fused only when its intermediate values have no other user and
 are not returned, so no value the program can observe disappears.  The
@@ -63,7 +64,7 @@ def _fuse_function(function: Function) -> Counter[str]:
     counts: Counter[str] = Counter()
     # Each rule runs to a fixed point before the next so that the SwiGLU rule
     # sees the gate/up linears before the group rule could claim them.
-    for rule in (_fuse_swiglu, _fuse_group, _fuse_residual, _fuse_rope_store):
+    for rule in (_fuse_swiglu, _fuse_group, _fuse_residual, _fuse_rope_store, _fuse_store_advance):
         while True:
             name = rule(function)
             if name is None:
@@ -259,4 +260,49 @@ def _fuse_rope_store(function: Function) -> str | None:
         )
         _replace(function, [r_index, s_index], s_index, new)
         return new.name
+    return None
+
+
+def _fuse_store_advance(function: Function) -> str | None:
+    """rope_kv_store whose state feeds only the kv.advance of the same slot
+    (nothing reads the state in between), with positions = that slot's
+    kv.length of the same incoming state: the store kernel advances too."""
+
+    ops = function.block.operations
+    uses, producer = _uses(function), _producers(function)
+    for s_index, store in enumerate(ops):
+        if store.name != "kernel.hip.rope_kv_store" or store.attributes.get("advance"):
+            continue
+        state_in, positions = store.operands[0], store.operands[6]
+        p_index = producer.get(id(positions))
+        if p_index is None:
+            continue
+        length = ops[p_index]
+        if (length.name != "runtime.kv.length" or length.operands[0] is not state_in
+                or length.attributes.get("slot", 0) != store.attributes.get("slot", 0)):
+            continue
+        state_out = store.results[1]
+        users = uses[id(state_out)]
+        if len(users) != 1 or users[0][0] >= len(ops):
+            continue
+        a_index = users[0][0]
+        advance = ops[a_index]
+        if (advance.name != "runtime.kv.advance"
+                or advance.attributes.get("slot", 0) != store.attributes.get("slot", 0)):
+            continue
+        delta = int(advance.attributes.get("delta", 1))
+        if delta <= 0:
+            continue
+        # The positions tensor is advanced in place when the state's lengths
+        # are: nothing may read it after the store.
+        if any(user > s_index for user, _ in uses[id(positions)]):
+            continue
+        attributes = dict(store.attributes)
+        attributes["advance"] = delta
+        attributes["fused_from"] = list(store.attributes.get("fused_from", [store.name])) + [advance.name]
+        attributes["lowered_from"] = str(store.attributes.get("lowered_from", "")) + "+serve.kv.advance"
+        new = Operation(store.name, list(store.operands), [store.results[0], advance.results[0]],
+                        attributes, store.effects)
+        _replace(function, [s_index, a_index], a_index, new)
+        return "kernel.hip.rope_kv_store+advance"
     return None

@@ -137,3 +137,42 @@ def test_fused_qwen2_graph_equals_unfused(gpu):
     torch.cuda.synchronize()
     for a, b in zip(*runs):
         assert_bitwise_equal(a, b)
+
+
+@pytest.mark.parametrize("in_place", [True, False])
+def test_rope_kv_store_advance_matches_store_then_advance(gpu, in_place):
+    # The store kernel's last workgroup advances the lengths (in place or into
+    # a new tensor) exactly as the kv advance launched after it would, and
+    # flags an advance past the capacity; repeated calls re-arm its counter.
+    from stateful_llm_compiler_hip.backends import hip_kv_advance
+
+    announce(f"rope_kv_store + advance in_place={in_place}")
+    g = generator(401)
+    B, QH, KVH, D, cap = 5, 14, 2, 64, 32
+    for step in range(3):
+        q = _t(g, B, 1, QH * D, device=gpu).view(B, 1, QH, D).transpose(1, 2)
+        k = _t(g, B, 1, KVH * D, device=gpu).view(B, 1, KVH, D).transpose(1, 2)
+        v = _t(g, B, 1, KVH * D, device=gpu).view(B, 1, KVH, D).transpose(1, 2)
+        cos = _t(g, B, 1, D, device=gpu)
+        sin = _t(g, B, 1, D, device=gpu)
+        start = torch.tensor([0, 3, 17, cap - 2, cap - 1], device=gpu) + step
+        kb1 = _t(g, B, cap, KVH, D, device=gpu)
+        vb1 = _t(g, B, cap, KVH, D, device=gpu)
+        kb2, vb2 = kb1.clone(), vb1.clone()
+        flag1 = torch.zeros(1, dtype=torch.int32, device=gpu)
+        flag2 = torch.zeros(1, dtype=torch.int32, device=gpu)
+        pos1 = start.clone()
+        out1 = pos1 if in_place else torch.full_like(pos1, -7)
+        q1 = hip_rope_kv_store(q, k, v, cos, sin, kb1, vb1, pos1, overflow=flag1, advance=1,
+                               lengths_out=out1)
+        pos2 = start.clone()
+        q2 = hip_rope_kv_store(q, k, v, cos, sin, kb2, vb2, pos2, overflow=flag2)
+        out2 = hip_kv_advance(pos2, 1, cap, overflow=flag2)
+        torch.cuda.synchronize()
+        assert_bitwise_equal(q1, q2)
+        assert_bitwise_equal(kb1, kb2)
+        assert_bitwise_equal(vb1, vb2)
+        assert out1.tolist() == out2.tolist() == (start + 1).tolist()
+        assert int(flag1.item()) == int(flag2.item()) == (1 if step >= 1 else 0)
+        if not in_place:
+            assert pos1.tolist() == start.tolist()

@@ -36,8 +36,12 @@ def test_decode_graph_fuses_every_layer_chain():
         assert gone not in c, gone
     before = len(plain.module.functions[0].block.operations)
     after = len(fused.module.functions[0].block.operations)
-    # per layer: norm+3 linears, norm+2 linears+swiglu, 2 x linear+add, rope+store
-    assert before - after == layers * (3 + 3 + 2 + 1) + 1
+    # per layer: norm+3 linears, norm+2 linears+swiglu, 2 x linear+add,
+    # rope+store, store+advance
+    assert before - after == layers * (3 + 3 + 2 + 1 + 1) + 1
+    assert sum(1 for op in fused.module.functions[0].block.operations
+               if op.name == "kernel.hip.rope_kv_store" and op.attributes.get("advance") == 1) == layers
+    assert "runtime.kv.advance" not in c
     stats = next(p for p in fused.passes if p.name == "fuse-decode-kernels").statistics
     assert stats["fused"]["kernel.hip.rope_kv_store"] == layers
 
