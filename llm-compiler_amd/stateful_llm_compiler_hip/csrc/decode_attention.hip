@@ -687,6 +687,10 @@ bool mfma_eligible(int dtype, int64_t head_dim, int64_t groups) {
          (head_dim == 64 || head_dim == 128) && groups <= kMaxGroups;
 }
 
+#ifndef SLC_DECODE_MIN_CHUNK
+#define SLC_DECODE_MIN_CHUNK 256
+#endif
+
 // Sequence chunk of the split-sequence grid: the smallest power-of-two
 // multiple of the workgroup's 128-token sweep that keeps the grid at about one
 // workgroup per CU (256 CUs on MI355X); longer chunks amortise the per-wave
@@ -699,7 +703,7 @@ int64_t choose_chunk(int64_t batch, int64_t kv_heads, int64_t mask_len,
     chunk = slc_host::ceil_div(split_tokens, sweep) * sweep;
   } else {
     const int64_t target_groups = 256;
-    chunk = 2 * sweep;
+    chunk = SLC_DECODE_MIN_CHUNK;
     // Stop at one chunk per sequence: with more (batch, kv-head) pairs than
     // the target the grid is already that wide.
     while (chunk < mask_len &&

@@ -20,6 +20,7 @@
 //    are launched heaviest-first); the diagonal tile is masked per element.
 // fp32 and other shapes take a simple wave-per-query kernel.
 #include <cmath>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -382,9 +383,14 @@ __device__ __forceinline__ uint2 lds_read_tr(const unsigned char* p) {
   return __builtin_bit_cast(uint2, v);
 }
 
-// POW2: the softmax scale is a power of two (1/8 for head_dim 64), so
-// round(round(q.k) * scale) = round(q.k) * scale exactly and the second
-// rounding (and a multiply) can go.
+// POW2: bf16 and the softmax scale is a power of two (1/8 for head_dim 64):
+// multiplying a normal bf16 value by 2^k is exact and stays a bf16 value
+// (bf16 has fp32's exponent range), so round(round(q.k) * scale) =
+// round(q.k) * scale and the second rounding (and a multiply) can go.  The
+// two differ only when the scaled score falls below bf16's normal range
+// (|score| < 2^-126), where the difference vanishes in the softmax's
+// s - max.  fp16 keeps both roundings: its narrow exponent range makes
+// subnormal scaled scores common.
 template <typename T, int G, int MK, bool CAUSAL, bool POW2>
 __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
     const T* __restrict__ query, const T* __restrict__ key, const T* __restrict__ value,
@@ -644,7 +650,8 @@ int launch_v2(const void* q, const void* k, const void* v, const void* mask, voi
               hipStream_t stream) {
   const dim3 grid((tokens + kV2Queries - 1) / kV2Queries, kv_heads, static_cast<unsigned>(batch));
   int exponent = 0;
-  const bool pow2 = scale > 0.0f && std::frexp(scale, &exponent) == 0.5f && exponent > -100;
+  const bool pow2 = std::is_same_v<T, slc::bf16_t> && scale > 0.0f &&
+                    std::frexp(scale, &exponent) == 0.5f && exponent > -100;
   auto kernel = pow2 ? prefill_attention_v2_kernel<T, G, MK, CAUSAL, true>
                      : prefill_attention_v2_kernel<T, G, MK, CAUSAL, false>;
   hipLaunchKernelGGL(kernel, grid, dim3((G + 1) * 64), 0,
