@@ -264,7 +264,7 @@ constexpr float kRescaleThreshold = 8.0f;
 
 // MK: mask element type (0 = no mask, else an slc_dtype tag + 1), a template
 // parameter so the load path has no data-dependent branches.
-template <typename T, int D, int MK>
+template <typename T, int D, int MK, bool L64>
 __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     const T* __restrict__ query, const T* __restrict__ key_buffer,
     const T* __restrict__ value_buffer, const void* __restrict__ lengths,
@@ -293,27 +293,26 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   const int g = lane >> 4;  // lane group: MFMA k-slice / output row block
   const int c = lane & 15;  // MFMA row (A) / column (B, C)
 
-  int64_t end64 = slc::load_length(lengths, b, lengths_dtype);
-  end64 = end64 < 0 ? 0 : end64;
-  end64 = end64 < mask_len ? end64 : mask_len;
-  end64 = end64 < capacity ? end64 : capacity;
-  const int end = static_cast<int>(end64);  // host guarantees capacity < 2^30
-  const int chunk_start = chunk * chunk_tokens;
-  if (nchunks > 1 && chunk_start >= end) {
-    // Nothing of this batch in the chunk: an empty partial (max -inf, sum 0),
-    // which the merge weighs by zero.  A sequence with no token at all thus
-    // merges to 0/0 = NaN, like the reference's softmax over an all -inf row.
-    if (tid < groups) {
-      const int64_t p = (b * q_heads + kvh * groups + tid) * nchunks + chunk;
-      publish(part_ml + 2 * p, -INFINITY, counters);
-      publish(part_ml + 2 * p + 1, 0.0f, counters);
+  // Issued first (memory reads complete in issue order, so consuming it
+  // later waits only for it), used after the query loads are issued.
+  // A vector (buffer) load: a scalar load would share its counter with the
+  // kernel-argument loads and be waited for before the tiles are issued.
+  // L64: int64 lengths (a template parameter, so no branch separates the load
+  // from its use).
+  uint32_t length_lo, length_hi = 0;
+  {
+    constexpr int es = L64 ? 8 : 4;
+    const __amdgpu_buffer_rsrc_t rl =
+        make_rsrc(static_cast<const char*>(lengths) + b * es, es);
+    if constexpr (L64) {
+      const auto pair = __builtin_amdgcn_raw_buffer_load_b64(rl, 0, 0, 0);
+      length_lo = static_cast<uint32_t>(pair[0]);
+      length_hi = static_cast<uint32_t>(pair[1]);
+    } else {
+      length_lo = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rl, 0, 0, 0));
     }
-    if (counters != nullptr)
-      merge_if_last<T, D>(part_o, part_ml, output, counters, smem, b, kvh, q_heads, kv_heads,
-                          groups, o_sb, o_sh, nchunks);
-    return;
   }
-  const int chunk_end = min(chunk_start + chunk_tokens, end);
+  const int chunk_start = chunk * chunk_tokens;
 
   // Q^T as the B operand: lane (head c, k-slice g) holds dims kk*32+8g..+7.
   typename M::vec qv[KK];
@@ -368,8 +367,8 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   // scores) through buffer resources bounded at the chunk end.  K and V use
   // the same lane layout: lane (row c, k-slice g) of 16-row block j holds
   // dims kk*32+8g..+7 of token t0+16j+c.
-  auto load_tile = [&](int t0, Tile& tile) {
-    const int rows = chunk_end - t0;
+  auto load_tile = [&](int t0, Tile& tile, int bound) {
+    const int rows = bound - t0;
     const int nbytes = rows > 0 ? rows * row_bytes : 0;
     const int64_t shift = static_cast<int64_t>(t0) * row_bytes;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + shift, nbytes);
@@ -404,6 +403,39 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
         }
     }
   };
+
+  constexpr int kStride = kWaves * kTile;
+  const int t_first = chunk_start + wave * kTile;
+
+  // The length is consumed only here, after the query loads were issued
+  // (the asm ties its registers to this point; the compiler would otherwise
+  // read it into scalars right after the load and wait for it).
+  asm volatile("" : "+v"(length_lo), "+v"(length_hi)::"memory");
+  int64_t end64 = L64 ? static_cast<int64_t>((static_cast<uint64_t>(length_hi) << 32) | length_lo)
+                      : static_cast<int64_t>(static_cast<int32_t>(length_lo));
+  end64 = end64 < 0 ? 0 : end64;
+  end64 = end64 < mask_len ? end64 : mask_len;
+  end64 = end64 < capacity ? end64 : capacity;
+  const int end = static_cast<int>(end64);  // host guarantees capacity < 2^30
+  if (nchunks > 1 && chunk_start >= end) {
+    // Nothing of this batch in the chunk: an empty partial (max -inf, sum 0),
+    // which the merge weighs by zero.  A sequence with no token at all thus
+    // merges to 0/0 = NaN, like the reference's softmax over an all -inf row.
+    if (tid < groups) {
+      const int64_t p = (b * q_heads + kvh * groups + tid) * nchunks + chunk;
+      publish(part_ml + 2 * p, -INFINITY, counters);
+      publish(part_ml + 2 * p + 1, 0.0f, counters);
+    }
+    if (counters != nullptr)
+      merge_if_last<T, D>(part_o, part_ml, output, counters, smem, b, kvh, q_heads, kv_heads,
+                          groups, o_sb, o_sh, nchunks);
+    return;
+  }
+  const int chunk_end = min(chunk_start + chunk_tokens, end);
+
+  Tile ta, tb;
+  load_tile(t_first, ta, chunk_end);
+  load_tile(t_first + kStride, tb, chunk_end);
 
   auto compute_tile = [&](int t0, const Tile& tile) {
     // S^T tile: two 16-token MFMA blocks; lane holds tokens 16j+4g+r, head c.
@@ -470,19 +502,12 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   // Two tiles in flight per wave: while tile A is consumed, tile B (issued
   // earlier) and the refill of A stream in.  Prefetches past the chunk end are
   // zero-length buffer ranges and touch no memory.
-  constexpr int kStride = kWaves * kTile;
-  {
-    int t0 = chunk_start + wave * kTile;
-    Tile ta, tb;
-    load_tile(t0, ta);
-    load_tile(t0 + kStride, tb);
-    for (; t0 < chunk_end; t0 += 2 * kStride) {
-      compute_tile(t0, ta);
-      load_tile(t0 + 2 * kStride, ta);
-      if (t0 + kStride >= chunk_end) break;
-      compute_tile(t0 + kStride, tb);
-      load_tile(t0 + 3 * kStride, tb);
-    }
+  for (int t0 = t_first; t0 < chunk_end; t0 += 2 * kStride) {
+    compute_tile(t0, ta);
+    load_tile(t0 + 2 * kStride, ta, chunk_end);
+    if (t0 + kStride >= chunk_end) break;
+    compute_tile(t0 + kStride, tb);
+    load_tile(t0 + 3 * kStride, tb, chunk_end);
   }
 
   // Finish the per-lane partial sums of l over the 4 lane groups.
@@ -782,7 +807,13 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
   }
   slc_host::mark_kernel_begin(stream);
 #define SLC_MFMA(MK)                                                          \
-  hipLaunchKernelGGL((decode_attention_mfma_kernel<T, D, MK>), grid, dim3(kThreads), \
+  if (lengths_dtype == SLC_I64) {                                             \
+    SLC_MFMA_L(MK, true);                                                     \
+  } else {                                                                    \
+    SLC_MFMA_L(MK, false);                                                    \
+  }
+#define SLC_MFMA_L(MK, L64)                                                   \
+  hipLaunchKernelGGL((decode_attention_mfma_kernel<T, D, MK, L64>), grid, dim3(kThreads), \
                      0, stream, static_cast<const T*>(query),                 \
                      static_cast<const T*>(kb), static_cast<const T*>(vb),    \
                      lengths, lengths_dtype, mask, mask_dtype,                \
@@ -804,6 +835,7 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
     }
   }
 #undef SLC_MFMA
+#undef SLC_MFMA_L
   slc_host::mark_kernel_end(stream);
   int rc = slc_host::check_launch("slc_hip_decode_attention");
   if (rc != SLC_OK || nchunks == 1 || counters != nullptr) return rc;
