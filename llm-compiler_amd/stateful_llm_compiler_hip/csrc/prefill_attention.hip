@@ -4,7 +4,9 @@
 // executor) and backends/triton_prefill_attention.py:10-150 (fused kernel):
 //   out[b,h,q,:] = sum_k softmax_k(scale * q.k + mask[b,q,k]) v[b,k,h/g,:]
 // with keys k > q removed when the op is causal (causal=True); an additive
-// mask (B x 1 x T x T) is applied when given.  fp32 softmax and accumulation.
+// mask (B x 1 x T x T) is applied when given.  q.k and its scaling are
+// rounded to the I/O dtype as the reference executor's matmul and multiply
+// are; fp32 softmax and accumulation.
 //
 // MI355X design (bf16 / fp16, head_dim 64):
 //  * A workgroup is 4 waves x 16 queries of one (batch, query head); K/V tiles
@@ -217,7 +219,7 @@ __global__ __launch_bounds__(256) void prefill_attention_mfma_kernel(
         for (int r = 0; r < 4; ++r) {
           const int kidx = k0 + kb * 16 + 4 * g + r;
           // q.k and its scaling are materialised in the tensor dtype, as the
-          // reference's matmul and multiply do; softmax stays fp32.
+          // reference executor's matmul and multiply do; softmax stays fp32.
           float v = slc::round_to<T>(slc::round_to<T>(st[r]) * scale) * kLog2e;
           if constexpr (MK != 0) {
             if (kidx < tokens) {
@@ -383,14 +385,13 @@ __device__ __forceinline__ uint2 lds_read_tr(const unsigned char* p) {
   return __builtin_bit_cast(uint2, v);
 }
 
-// POW2: bf16 and the softmax scale is a power of two (1/8 for head_dim 64):
-// multiplying a normal bf16 value by 2^k is exact and stays a bf16 value
-// (bf16 has fp32's exponent range), so round(round(q.k) * scale) =
-// round(q.k) * scale and the second rounding (and a multiply) can go.  The
-// two differ only when the scaled score falls below bf16's normal range
-// (|score| < 2^-126), where the difference vanishes in the softmax's
-// s - max.  fp16 keeps both roundings: its narrow exponent range makes
-// subnormal scaled scores common.
+// POW2: bf16 with a power-of-two scale (1/8 for head_dim 64): a normal bf16
+// value times 2^k is exact and stays a bf16 value (bf16 has fp32's exponent
+// range), so bf16(bf16(q.k) * scale) = bf16(q.k) * scale and the second
+// rounding goes.  (They differ only for scaled scores below bf16's normal
+// range, |score| < 2^-126, where the difference vanishes in score - max.)
+// fp16 keeps both roundings: its narrow exponent range makes subnormal
+// scaled scores common.
 template <typename T, int G, int MK, bool CAUSAL, bool POW2>
 __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
     const T* __restrict__ query, const T* __restrict__ key, const T* __restrict__ value,
@@ -414,7 +415,8 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
   const int g = lane >> 4;
   const int c = lane & 15;
   const int q0 = qblk * kV2Queries;
-  const float scale_log2e = scale * kLog2e;
+  // Factor from the rounded score to log2 units.
+  const float c_log2 = POW2 ? scale * kLog2e : kLog2e;
   const int key_end = CAUSAL ? min(q0 + kV2Queries, tokens) : tokens;
   const int ntiles = (key_end + kKeys - 1) / kKeys;
 
@@ -529,7 +531,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
       }
     }
 
-    // Scores (log2 units) with the reference's rounding, mask and validity.
+    // Scores with the mask and validity (fp32, as the reference's fused kernel).
     const bool full = !CAUSAL ? k0 + kKeys <= tokens : k0 + kKeys <= q0 && k0 + kKeys <= tokens;
 #pragma unroll
     for (int qb = 0; qb < 4; ++qb) {
@@ -565,13 +567,15 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          float v;
-          if constexpr (POW2) {
-            v = slc::round_to<T>(st[kb][qb][r]) * scale_log2e;
-          } else {
-            v = slc::round_to<T>(slc::round_to<T>(st[kb][qb][r]) * scale) * kLog2e;
-          }
-          if constexpr (MK != 0) v = fmaf(mv[r], kLog2e, v);
+          // r = the executor's rounded score: bf16(bf16(q.k) * scale), or
+          // bf16(q.k) when the scale is a power of two (POW2; the product is
+          // then exact and scaled inside the exp2 argument).  Without a mask
+          // the row max is taken over r (times the positive factor c it is
+          // the max of the log2-domain scores); with one the scores become
+          // c * r + mask * log2(e).
+          float v = slc::round_to<T>(st[kb][qb][r]);
+          if constexpr (!POW2) v = slc::round_to<T>(v * scale);
+          if constexpr (MK != 0) v = fmaf(v, c_log2, mv[r] * kLog2e);
           if (!full) {
             const int kidx = k0 + 16 * kb + 4 * g + r;
             bool valid = kidx < tokens;
@@ -584,6 +588,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
       }
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      if constexpr (MK == 0) mx *= c_log2;
       if (__any(mx > m_run[qb] + kRescaleThreshold)) {
         const float m_new = fmaxf(m_run[qb], mx);
         const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - (m_new == -INFINITY ? 0.0f : m_new));
@@ -604,7 +609,8 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
         u16x8 bits;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float p = __builtin_amdgcn_exp2f(st[2 * half + (i >> 2)][qb][i & 3] - m_use);
+          const float x = st[2 * half + (i >> 2)][qb][i & 3];
+          const float p = __builtin_amdgcn_exp2f(MK == 0 ? fmaf(x, c_log2, -m_use) : x - m_use);
           l_run[qb] += p;
           bits.v[i] = bits_of<T>(p);
         }
@@ -650,8 +656,8 @@ int launch_v2(const void* q, const void* k, const void* v, const void* mask, voi
               hipStream_t stream) {
   const dim3 grid((tokens + kV2Queries - 1) / kV2Queries, kv_heads, static_cast<unsigned>(batch));
   int exponent = 0;
-  const bool pow2 = std::is_same_v<T, slc::bf16_t> && scale > 0.0f &&
-                    std::frexp(scale, &exponent) == 0.5f && exponent > -100;
+  const bool pow2 = std::is_same_v<T, slc::bf16_t> && std::frexp(scale, &exponent) == 0.5f &&
+                    exponent > -100;
   auto kernel = pow2 ? prefill_attention_v2_kernel<T, G, MK, CAUSAL, true>
                      : prefill_attention_v2_kernel<T, G, MK, CAUSAL, false>;
   hipLaunchKernelGGL(kernel, grid, dim3((G + 1) * 64), 0,
@@ -782,7 +788,10 @@ extern "C" int slc_hip_prefill_attention(
        ((tokens - 1) * m_sq + tokens) * me < (1LL << 31));
   const bool out_ok = (reinterpret_cast<uintptr_t>(output) & 7) == 0 &&
                       ((o_sb | o_sh | o_st) & 3) == 0;
-  if (mfma_ok && group_ok && mask_ok && out_ok && kv_heads <= 65535 && kUseGrouped) {
+  // The grouped kernel takes the row max before the scale factor: positive
+  // scale.
+  if (mfma_ok && group_ok && mask_ok && out_ok && kv_heads <= 65535 && kUseGrouped &&
+      scale > 0.0f) {
     if (dtype == SLC_BF16)
       return try_v2<slc::bf16_t>(query, key, value, mask, mask_dtype, output, batch, T_,
                                  static_cast<int>(kv_heads), groups, causal, st, scale, s);

@@ -199,7 +199,8 @@ def test_prefill_grouped_kernel(gpu, q_heads, kv_heads, tokens, variant):
 @pytest.mark.parametrize("scale", [0.1, 0.3, 0.25])
 def test_prefill_grouped_kernel_scale(gpu, scale):
     # A scale that is not a power of two rounds the scaled score a second
-    # time; 0.25 takes the single-rounding path.
+    # time (as the reference executor does); 0.25 takes the single-rounding
+    # path.
     announce(f"prefill grouped scale={scale}")
     actual, expected = _prefill_case(gpu, 2, 130, torch.bfloat16, 11, mask_kind="random", causal=True,
                                      scale=scale)
