@@ -485,19 +485,26 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
       qv[qb][kk] = __builtin_bit_cast(typename M::vec,
                                       *reinterpret_cast<const uint4*>(qp + kk * 32 + 8 * g));
   }
-  float m_run[4], l_run[4];
-  f32x4_t acc[4][4];  // [dim block][query block]
+  // acc[4] is the softmax denominator: the P.V MFMA against a block of ones
+  // sums each query's probabilities (all 16 rows of the block hold the
+  // same sum), so the matrix cores, not the VALU, do the row sums, and the
+  // running rescale applies to it with the outputs.
+  float m_run[4];
+  f32x4_t acc[5][4];  // [dim block, then the row-sum block][query block]
 #pragma unroll
   for (int qb = 0; qb < 4; ++qb) {
     m_run[qb] = -INFINITY;
-    l_run[qb] = 0.0f;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) acc[db][qb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int db = 0; db < 5; ++db) acc[db][qb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
   // Transpose-read lane addresses (bytes within a tile) for V^T blocks:
   // lane j = c of group g reads key row 4g + j/4 (+16 for the second read)
   // of a 32-key half, dims 16db + 4(j%4) .. +3.
+  u16x8 one_bits;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) one_bits.v[i] = bits_of<T>(1.0f);
+  const typename M::vec ones = __builtin_bit_cast(typename M::vec, one_bits);
   int tr_off[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) {
@@ -592,9 +599,8 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
       if (__any(mx > m_run[qb] + kRescaleThreshold)) {
         const float m_new = fmaxf(m_run[qb], mx);
         const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - (m_new == -INFINITY ? 0.0f : m_new));
-        l_run[qb] *= alpha;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) acc[db][qb] = acc[db][qb] * alpha;
+        for (int db = 0; db < 5; ++db) acc[db][qb] = acc[db][qb] * alpha;
         m_run[qb] = m_new;
       }
     }
@@ -611,7 +617,6 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
         for (int i = 0; i < 8; ++i) {
           const float x = st[2 * half + (i >> 2)][qb][i & 3];
           const float p = __builtin_amdgcn_exp2f(MK == 0 ? fmaf(x, c_log2, -m_use) : x - m_use);
-          l_run[qb] += p;
           bits.v[i] = bits_of<T>(p);
         }
         pv[qb] = __builtin_bit_cast(typename M::vec, bits);
@@ -624,14 +629,14 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
 #pragma unroll
         for (int qb = 0; qb < 4; ++qb) acc[db][qb] = M::run(va, pv[qb], acc[db][qb]);
       }
+#pragma unroll
+      for (int qb = 0; qb < 4; ++qb) acc[4][qb] = M::run(ones, pv[qb], acc[4][qb]);
     }
   }
 
 #pragma unroll
   for (int qb = 0; qb < 4; ++qb) {
-    float l = l_run[qb];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    const float l = acc[4][qb][0];
     const int my_query = q0 + 16 * qb + c;
     if (my_query < tokens) {
       const float inv = 1.0f / l;
