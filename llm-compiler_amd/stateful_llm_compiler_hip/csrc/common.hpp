@@ -92,6 +92,31 @@ __device__ __forceinline__ int64_t load_length(const void* lengths, int64_t b,
   return static_cast<int64_t>(static_cast<const int32_t*>(lengths)[b]);
 }
 
+// Max of x over lanes l and l ^ 16 (and l ^ 32): the gfx950 lane-swap
+// instructions exchange rows of 16 (halves of 32) between two registers in the
+// VALU, where __shfl_xor goes through LDS (ds_bpermute) and its latency.  With
+// x in both operands the two results hold x of each pair of lanes.
+__device__ __forceinline__ float max_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 }  // namespace slc
 
 // Host-side helpers shared by the C entry points.

@@ -458,8 +458,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     float mx = s[0];
 #pragma unroll
     for (int i = 1; i < 8; ++i) mx = fmaxf(mx, s[i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = slc::max_xor32(slc::max_xor16(mx));
     if (__any(mx > m_run + kRescaleThreshold)) {
       const float m_new = fmaxf(m_run, mx);
       const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.0f : m_new));

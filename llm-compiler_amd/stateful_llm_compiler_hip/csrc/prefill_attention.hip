@@ -593,8 +593,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
           mx = fmaxf(mx, v);
         }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = slc::max_xor32(slc::max_xor16(mx));
       if constexpr (MK == 0) mx *= c_log2;
       if (__any(mx > m_run[qb] + kRescaleThreshold)) {
         const float m_new = fmaxf(m_run[qb], mx);
