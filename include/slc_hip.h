@@ -52,7 +52,9 @@ enum slc_dtype {
   SLC_I64 = 4
 };
 
-enum slc_status { SLC_OK = 0, SLC_ERR_INVALID_ARGUMENT = -1 };
+/* SLC_ERR_UNSUPPORTED: a fused entry point's kernel does not take these
+ * arguments; nothing was launched and the caller runs the unfused ops. */
+enum slc_status { SLC_OK = 0, SLC_ERR_INVALID_ARGUMENT = -1, SLC_ERR_UNSUPPORTED = -2 };
 
 /* Library version (major*10000 + minor*100 + patch). */
 SLC_API int slc_hip_version(void);
@@ -285,6 +287,37 @@ SLC_API int slc_hip_rope_kv_store(
     int64_t capacity, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh,
     int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t cos_sb, int64_t cos_st,
     int64_t sin_sb, int64_t sin_st, int64_t qo_sb, int64_t qo_sh, int64_t qo_st, void* stream);
+
+/*
+ * rope_decode_attention: one decode token's RoPE, KV store, length advance and
+ * GQA attention in one kernel.  Replaces rope_kv_store (with advance = 1)
+ * followed by slc_hip_decode_attention of the rotated query over the advanced
+ * state -- the reference's triton_rope, triton_kv_store, kv.advance and
+ * triton_decode_attention sequence (triton_rope.py:299-390,
+ * triton_kv.py:71-129, execution.py:741-767, triton_attention.py:134-210) --
+ * with bit-identical results:
+ *   pos = lengths[b]; key_buffer[b, pos] = rope(key[b]); value_buffer[b, pos]
+ *   = value[b] (skipped, *overflow set, when pos is outside [0, capacity));
+ *   out[b, h] = decode attention of rope(query[b, h]) over the tokens
+ *   s < min(pos + 1, mask_len, capacity); lengths_out[b] = pos + 1 (in place
+ *   allowed; *overflow set past the capacity).
+ * query [B, q_heads, D], key/value [B, kv_heads, D] (one token), cosine/sine
+ * [B, D] (the token's rows); buffers [B, capacity, kv_heads, D] with strides
+ * as in slc_hip_decode_attention; lengths int64; the workspace is
+ * slc_hip_decode_attention_workspace_size(batch, q_heads, head_dim, mask_len,
+ * kv_heads, dtype, 0) bytes.  Returns SLC_ERR_UNSUPPORTED (nothing launched)
+ * for shapes, dtypes or alignments its kernel does not take.
+ */
+SLC_API int slc_hip_rope_decode_attention(
+    const void* query, const void* key, const void* value, const void* cosine,
+    const void* sine, void* key_buffer, void* value_buffer, const int64_t* lengths,
+    int64_t* lengths_out, int* overflow, const void* mask, int mask_dtype, void* output,
+    void* workspace, int64_t workspace_bytes, int dtype, int64_t batch, int64_t q_heads,
+    int64_t kv_heads, int64_t head_dim, int64_t capacity, int64_t mask_len, int64_t q_stride_b,
+    int64_t q_stride_h, int64_t k_stride_b, int64_t k_stride_h, int64_t v_stride_b,
+    int64_t v_stride_h, int64_t cos_stride_b, int64_t sin_stride_b, int64_t kv_stride_b,
+    int64_t kv_stride_s, int64_t kv_stride_h, int64_t mask_stride_b, int64_t mask_stride_s,
+    int64_t out_stride_b, int64_t out_stride_h, float scale, void* stream);
 
 #ifdef __cplusplus
 }

@@ -146,3 +146,98 @@ def hip_decode_attention(
     )
     _native.check(status, "slc_hip_decode_attention")
     return output
+
+
+def hip_rope_decode_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    cosine: torch.Tensor,
+    sine: torch.Tensor,
+    key_buffer: torch.Tensor,
+    value_buffer: torch.Tensor,
+    lengths: torch.Tensor,
+    lengths_out: torch.Tensor,
+    attention_mask: torch.Tensor | None,
+    *,
+    scale: float,
+    overflow: torch.Tensor | None = None,
+) -> torch.Tensor | None:
+    """One decode token's RoPE, KV store at ``lengths``, length advance by one
+    (into ``lengths_out``, which may be ``lengths``) and GQA attention, in one
+    kernel; bit-identical to ``hip_rope_kv_store(..., advance=1)`` followed by
+    ``hip_decode_attention`` of the rotated query over the advanced lengths.
+
+    query [B, QH, 1, D] and key/value [B, KVH, 1, D] unrotated projections,
+    cosine/sine [B, 1, D].  Returns None, having done nothing, when the fused
+    kernel does not take the case (the caller then runs the two ops).
+    """
+
+    tensors = [query, key, value, cosine, sine, key_buffer, value_buffer, lengths, lengths_out]
+    if attention_mask is not None:
+        tensors.append(attention_mask)
+    if not all(tensor.is_cuda for tensor in tensors):
+        return None
+    if (
+        query.ndim != 4 or key.ndim != 4 or value.ndim != 4 or query.shape[2] != 1
+        or key.shape != value.shape or key.shape[2] != 1 or key_buffer.ndim != 4
+        or key_buffer.shape != value_buffer.shape or key_buffer.stride() != value_buffer.stride()
+        or cosine.ndim != 3 or cosine.shape != sine.shape or cosine.shape[1] != 1
+    ):
+        return None
+    batch, query_heads, _, head_dim = query.shape
+    kv_heads = key.shape[1]
+    capacity = key_buffer.shape[1]
+    if (
+        key.shape[0] != batch or key_buffer.shape[0] != batch or key_buffer.shape[2] != kv_heads
+        or key_buffer.shape[3] != head_dim or key.shape[3] != head_dim
+        or cosine.shape != (batch, 1, head_dim) or query_heads % kv_heads
+        or lengths.shape != (batch,) or lengths_out.shape != (batch,)
+        or lengths.dtype != torch.int64 or lengths_out.dtype != torch.int64
+        or any(t.dtype != query.dtype for t in (key, value, cosine, sine, key_buffer, value_buffer))
+        or any(t.stride(-1) != 1 for t in (query, key, value, cosine, sine, key_buffer))
+    ):
+        return None
+    if attention_mask is not None and (
+        attention_mask.ndim != 4 or attention_mask.shape[:3] != (batch, 1, 1)
+        or attention_mask.dtype not in (torch.float16, torch.bfloat16, torch.float32)
+    ):
+        return None
+    lib = _native.library()
+    output = torch.empty_like(query)
+    if batch == 0:
+        return output
+    dtype = _native.dtype_tag(query.dtype)
+    mask_len = capacity if attention_mask is None else attention_mask.shape[-1]
+    if mask_len > capacity:
+        return None
+    nbytes = lib.slc_hip_decode_attention_workspace_size(
+        batch, query_heads, head_dim, mask_len, kv_heads, dtype, 0
+    )
+    workspace = _workspace(query.device, nbytes)
+    if attention_mask is None:
+        mask_ptr, mask_dtype, mask_sb, mask_ss = None, 0, 0, 0
+    else:
+        mask_ptr = attention_mask.data_ptr()
+        mask_dtype = _native.dtype_tag(attention_mask.dtype)
+        mask_sb, mask_ss = attention_mask.stride(0), attention_mask.stride(3)
+    status = lib.slc_hip_rope_decode_attention(
+        query.data_ptr(), key.data_ptr(), value.data_ptr(), cosine.data_ptr(), sine.data_ptr(),
+        key_buffer.data_ptr(), value_buffer.data_ptr(), lengths.data_ptr(),
+        lengths_out.data_ptr(), None if overflow is None else overflow.data_ptr(),
+        mask_ptr, mask_dtype, output.data_ptr(),
+        None if workspace is None else workspace.data_ptr(), nbytes, dtype,
+        batch, query_heads, kv_heads, head_dim, capacity, mask_len,
+        query.stride(0), query.stride(1), key.stride(0), key.stride(1),
+        value.stride(0), value.stride(1), cosine.stride(0), sine.stride(0),
+        key_buffer.stride(0), key_buffer.stride(1), key_buffer.stride(2),
+        mask_sb, mask_ss, output.stride(0), output.stride(1), float(scale),
+        _native.current_stream(query.device),
+    )
+    if status == _UNSUPPORTED:
+        return None
+    _native.check(status, "slc_hip_rope_decode_attention")
+    return output
+
+
+_UNSUPPORTED = -2  # SLC_ERR_UNSUPPORTED

@@ -29,6 +29,7 @@
 #include <mutex>
 
 #include "common.hpp"
+#include "op_math.hpp"
 
 namespace {
 
@@ -130,6 +131,8 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int 
 constexpr int kCounterRegions = 16;
 constexpr int kCounterPairs = 8192;  // (batch, kv-head) pairs per region
 __device__ int g_merge_counters[kCounterRegions][kCounterPairs];
+// Per-batch length-advance counters of the RoPE + store variant.
+__device__ int g_advance_counters[kCounterRegions][kCounterPairs];
 
 __device__ __forceinline__ void publish(float* p, float v, const int* counters) {
   if (counters != nullptr) {
@@ -143,21 +146,92 @@ __device__ __forceinline__ float fetch_partial(const float* p) {
 }
 
 constexpr int kFusedMergeUnroll = 8;
+// Length advance folded into the attention kernel: every workgroup of a
+// batch bumps the batch's counter once all its waves have read the length
+// (the merge's barrier), and the one completing the count writes the new
+// length (flagging an advance past the capacity) and re-arms the counter.
+struct LenAdvance {
+  int* counter;      // nullptr: no advance
+  int total;         // workgroups per batch (kv heads x chunks)
+  int64_t* out;      // the batch's length
+  int64_t next;      // its new value
+  int* overflow;
+  int64_t capacity;
+};
+
+__device__ __forceinline__ void finish_advance(const LenAdvance& adv, int before) {
+  if (adv.counter == nullptr || before != adv.total - 1) return;
+  __hip_atomic_store(adv.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  *adv.out = adv.next;
+  if (adv.overflow != nullptr && (adv.next > adv.capacity || adv.next < 0)) *adv.overflow = 1;
+}
+
+// RoPE + KV store of the new token folded into the attention kernel
+// (slc_hip_rope_decode_attention).  key/value: the token's projections
+// [b, kv_head, D] (key before RoPE); cosine/sine: [b, D] rows of its position.
+struct RopeStore {
+  const void* key;
+  const void* value;
+  const void* cosine;
+  const void* sine;
+  int64_t k_sb, k_sh, v_sb, v_sh, c_sb, s_sb;
+  int64_t* lengths_out;
+  int* overflow;
+  int* counters;  // per-batch advance counters of the stream's region
+};
+
+// Qwen2 half rotation of one lane's slices: slice kk pairs with kk + KK/2
+// (dims d and d + D/2), rounded exactly as the RoPE kernel rounds.
+template <typename T, int KK>
+__device__ __forceinline__ void rope_slices(uint4 (&x)[KK], const uint4 (&cs)[KK],
+                                            const uint4 (&sn)[KK]) {
+  constexpr int H = KK / 2;
+  auto f = [](uint16_t bits) {
+    T t;
+    t.bits = bits;
+    return slc::to_f32(t);
+  };
+#pragma unroll
+  for (int kk = 0; kk < H; ++kk) {
+    u16x8 a = __builtin_bit_cast(u16x8, x[kk]);
+    u16x8 z = __builtin_bit_cast(u16x8, x[kk + H]);
+    const u16x8 c1 = __builtin_bit_cast(u16x8, cs[kk]);
+    const u16x8 c2 = __builtin_bit_cast(u16x8, cs[kk + H]);
+    const u16x8 s1 = __builtin_bit_cast(u16x8, sn[kk]);
+    const u16x8 s2 = __builtin_bit_cast(u16x8, sn[kk + H]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float o1, o2;
+      slc::rope_pair<T>(f(a.v[i]), f(z.v[i]), f(c1.v[i]), f(c2.v[i]), f(s1.v[i]), f(s2.v[i]),
+                        o1, o2);
+      a.v[i] = bits_of<T>(o1);
+      z.v[i] = bits_of<T>(o2);
+    }
+    x[kk] = __builtin_bit_cast(uint4, a);
+    x[kk + H] = __builtin_bit_cast(uint4, z);
+  }
+}
+
 template <typename T, int D>
 __device__ __forceinline__ void merge_if_last(const float* part_o, const float* part_ml,
                                               T* output, int* counters, unsigned char* smem,
                                               int64_t b, int kvh, int q_heads, int kv_heads,
                                               int groups, int64_t o_sb, int64_t o_sh,
-                                              int nchunks) {
+                                              int nchunks, const LenAdvance& adv) {
   const int tid = threadIdx.x;
   __shared__ int is_last;
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores landed
   __syncthreads();
   if (tid == 0) {
     int* counter = counters + b * kv_heads + kvh;
+    // Both counters in flight together.
+    const int len_before = adv.counter != nullptr
+        ? __hip_atomic_fetch_add(adv.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+        : 0;
     const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     is_last = before == nchunks - 1;
     if (is_last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    finish_advance(adv, len_before);
   }
   __syncthreads();
   if (!is_last) return;
@@ -264,7 +338,7 @@ constexpr float kRescaleThreshold = 8.0f;
 
 // MK: mask element type (0 = no mask, else an slc_dtype tag + 1), a template
 // parameter so the load path has no data-dependent branches.
-template <typename T, int D, int MK, bool L64>
+template <typename T, int D, int MK, bool L64, bool ROPE>
 __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     const T* __restrict__ query, const T* __restrict__ key_buffer,
     const T* __restrict__ value_buffer, const void* __restrict__ lengths,
@@ -274,7 +348,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     int64_t capacity, int64_t mask_len, int64_t q_sb, int64_t q_sh,
     int64_t kv_sb, int kv_ss, int64_t kv_sh, int64_t m_sb, int m_ss,
     int64_t o_sb, int64_t o_sh, float scale, int chunk_tokens,
-    int nchunks, int* __restrict__ counters) {
+    int nchunks, int* __restrict__ counters, RopeStore rs) {
   using M = Mfma<T>;
   using Layout = SharedLayout<T, D>;
   constexpr int KK = D / 32;            // MFMA k-steps over head_dim
@@ -315,18 +389,41 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   const int chunk_start = chunk * chunk_tokens;
 
   // Q^T as the B operand: lane (head c, k-slice g) holds dims kk*32+8g..+7.
+  // ROPE: the query arrives unrotated and is rotated here; every lane also
+  // holds its slices of the new token's rotated key and its value (each
+  // rotation pair, dims d and d + D/2, is the lane's slices kk and kk + KK/2).
   typename M::vec qv[KK];
+  uint4 knew[ROPE ? KK : 1], vnew[ROPE ? KK : 1];
   {
     const int head = kvh * groups + c;
+    uint4 raw[KK];
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
-      uint4 raw = make_uint4(0, 0, 0, 0);
+      raw[kk] = make_uint4(0, 0, 0, 0);
       if (c < groups) {
-        raw = *reinterpret_cast<const uint4*>(query + b * q_sb + head * q_sh +
-                                              kk * 32 + 8 * g);
+        raw[kk] = *reinterpret_cast<const uint4*>(query + b * q_sb + head * q_sh +
+                                                  kk * 32 + 8 * g);
       }
-      qv[kk] = as_vec<T>(raw);
     }
+    if constexpr (ROPE) {
+      const T* kr = static_cast<const T*>(rs.key) + b * rs.k_sb + kvh * rs.k_sh;
+      const T* vr = static_cast<const T*>(rs.value) + b * rs.v_sb + kvh * rs.v_sh;
+      const T* cr = static_cast<const T*>(rs.cosine) + b * rs.c_sb;
+      const T* sr = static_cast<const T*>(rs.sine) + b * rs.s_sb;
+      uint4 cs[KK], sn[KK];
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const int d = kk * 32 + 8 * g;
+        knew[kk] = *reinterpret_cast<const uint4*>(kr + d);
+        vnew[kk] = *reinterpret_cast<const uint4*>(vr + d);
+        cs[kk] = *reinterpret_cast<const uint4*>(cr + d);
+        sn[kk] = *reinterpret_cast<const uint4*>(sr + d);
+      }
+      rope_slices<T, KK>(raw, cs, sn);
+      rope_slices<T, KK>(knew, cs, sn);
+    }
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) qv[kk] = as_vec<T>(raw[kk]);
   }
 
   const char* kbase = reinterpret_cast<const char*>(key_buffer + b * kv_sb + kvh * kv_sh);
@@ -413,10 +510,37 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   asm volatile("" : "+v"(length_lo), "+v"(length_hi)::"memory");
   int64_t end64 = L64 ? static_cast<int64_t>((static_cast<uint64_t>(length_hi) << 32) | length_lo)
                       : static_cast<int64_t>(static_cast<int32_t>(length_lo));
+  // ROPE: the length is the new token's position; attention covers it too.
+  const int64_t pos = end64;
+  if constexpr (ROPE) end64 = pos + 1;
   end64 = end64 < 0 ? 0 : end64;
   end64 = end64 < mask_len ? end64 : mask_len;
   end64 = end64 < capacity ? end64 : capacity;
   const int end = static_cast<int>(end64);  // host guarantees capacity < 2^30
+  LenAdvance adv{nullptr, 0, nullptr, 0, nullptr, capacity};
+  if constexpr (ROPE) {
+    adv = LenAdvance{rs.counters + b, kv_heads * nchunks, rs.lengths_out + b, pos + 1,
+                     rs.overflow, capacity};
+    // The new row is written by the workgroup of the chunk holding it (the
+    // last chunk when it lies past the mask); that workgroup's own tile
+    // loads of the row are replaced by the registers (patch below), so no
+    // workgroup depends on when the write lands.
+    const bool in_range = pos >= 0 && pos < capacity;
+    const int64_t owner = in_range ? min(pos / chunk_tokens, static_cast<int64_t>(nchunks) - 1) : 0;
+    if (in_range && chunk == owner && wave == 0 && c == 0) {
+      char* krow = reinterpret_cast<char*>(const_cast<T*>(key_buffer) + b * kv_sb + kvh * kv_sh) +
+                   pos * static_cast<int64_t>(kv_ss) * 2;
+      char* vrow = reinterpret_cast<char*>(const_cast<T*>(value_buffer) + b * kv_sb + kvh * kv_sh) +
+                   pos * static_cast<int64_t>(kv_ss) * 2;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        *reinterpret_cast<uint4*>(krow + kk * 64 + 16 * g) = knew[kk];
+        *reinterpret_cast<uint4*>(vrow + kk * 64 + 16 * g) = vnew[kk];
+      }
+    }
+    if (!in_range && chunk == 0 && kvh == 0 && tid == 0 && rs.overflow != nullptr)
+      *rs.overflow = 1;
+  }
   if (nchunks > 1 && chunk_start >= end) {
     // Nothing of this batch in the chunk: an empty partial (max -inf, sum 0),
     // which the merge weighs by zero.  A sequence with no token at all thus
@@ -428,7 +552,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     }
     if (counters != nullptr)
       merge_if_last<T, D>(part_o, part_ml, output, counters, smem, b, kvh, q_heads, kv_heads,
-                          groups, o_sb, o_sh, nchunks);
+                          groups, o_sb, o_sh, nchunks, adv);
     return;
   }
   const int chunk_end = min(chunk_start + chunk_tokens, end);
@@ -501,10 +625,30 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   // Two tiles in flight per wave: while tile A is consumed, tile B (issued
   // earlier) and the refill of A stream in.  Prefetches past the chunk end are
   // zero-length buffer ranges and touch no memory.
+  // ROPE: the new token's row of a tile comes from the registers.
+  auto patch = [&](int t0, Tile& tile) {
+    if constexpr (ROPE) {
+      if (pos >= t0 && pos < t0 + kTile) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const bool mine = t0 + 16 * j + c == pos;
+#pragma unroll
+          for (int kk = 0; kk < KK; ++kk) {
+            if (mine) {
+              tile.k[j][kk] = knew[kk];
+              tile.v[j][kk] = vnew[kk];
+            }
+          }
+        }
+      }
+    }
+  };
   for (int t0 = t_first; t0 < chunk_end; t0 += 2 * kStride) {
+    patch(t0, ta);
     compute_tile(t0, ta);
     load_tile(t0 + 2 * kStride, ta, chunk_end);
     if (t0 + kStride >= chunk_end) break;
+    patch(t0 + kStride, tb);
     compute_tile(t0 + kStride, tb);
     load_tile(t0 + 3 * kStride, tb, chunk_end);
   }
@@ -554,10 +698,17 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
       }
     }
   }
+  if constexpr (ROPE) {
+    // One chunk: no merge to carry the advance.  Every wave read the length
+    // before the combine's barriers, so the count may be bumped now.
+    if (nchunks == 1 && tid == 0)
+      finish_advance(adv, __hip_atomic_fetch_add(adv.counter, 1, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT));
+  }
   if (nchunks > 1 && counters != nullptr) {
     __syncthreads();  // the merge reuses the LDS
     merge_if_last<T, D>(part_o, part_ml, output, counters, smem, b, kvh, q_heads, kv_heads,
-                        groups, o_sb, o_sh, nchunks);
+                        groups, o_sb, o_sh, nchunks, adv);
   }
 }
 
@@ -766,19 +917,27 @@ int counter_region(hipStream_t stream) {
 
 // Device address of a region's counters on the current device (each device
 // holds its own copy of the static array), or nullptr if it cannot be found.
-int* merge_counters(int region) {
+// advance: the length-advance counters instead of the merge counters.
+int* merge_counters(int region, bool advance = false) {
   static std::mutex lock;
-  static int* base[64] = {};
+  static int* base[2][64] = {};
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return nullptr;
   std::lock_guard<std::mutex> guard(lock);
-  if (base[device] == nullptr) {
+  int*& slot = base[advance ? 1 : 0][device];
+  if (slot == nullptr) {
     void* address = nullptr;
-    if (hipGetSymbolAddress(&address, HIP_SYMBOL(g_merge_counters)) != hipSuccess) return nullptr;
-    base[device] = static_cast<int*>(address);
+    const hipError_t e = advance
+        ? hipGetSymbolAddress(&address, HIP_SYMBOL(g_advance_counters))
+        : hipGetSymbolAddress(&address, HIP_SYMBOL(g_merge_counters));
+    if (e != hipSuccess) return nullptr;
+    slot = static_cast<int*>(address);
   }
-  return base[device] + static_cast<int64_t>(region) * kCounterPairs;
+  return slot + static_cast<int64_t>(region) * kCounterPairs;
 }
+
+// Status of a fused call the kernels cannot take (nothing was launched).
+constexpr int kUnsupported = -2;
 
 template <typename T, int D>
 int launch_mfma(const void* query, const void* kb, const void* vb,
@@ -786,7 +945,8 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
                 int mask_dtype, void* output, void* workspace, int64_t batch,
                 int64_t q_heads, int64_t kv_heads, int64_t capacity,
                 int64_t mask_len, const int64_t* st, float scale,
-                int64_t chunk, int64_t nchunks, hipStream_t stream) {
+                int64_t chunk, int64_t nchunks, hipStream_t stream,
+                const RopeStore* rope = nullptr) {
   float* part_o = nullptr;
   float* part_ml = nullptr;
   if (nchunks > 1) {
@@ -804,16 +964,9 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
     const int region = counter_region(stream);
     if (region >= 0) counters = merge_counters(region);
   }
-  slc_host::mark_kernel_begin(stream);
-#define SLC_MFMA(MK)                                                          \
-  if (lengths_dtype == SLC_I64) {                                             \
-    SLC_MFMA_L(MK, true);                                                     \
-  } else {                                                                    \
-    SLC_MFMA_L(MK, false);                                                    \
-  }
-#define SLC_MFMA_L(MK, L64)                                                   \
-  hipLaunchKernelGGL((decode_attention_mfma_kernel<T, D, MK, L64>), grid, dim3(kThreads), \
-                     0, stream, static_cast<const T*>(query),                 \
+#define SLC_MFMA_K(MK, L64, ROPE)                                             \
+  hipLaunchKernelGGL((decode_attention_mfma_kernel<T, D, MK, L64, ROPE>), grid,           \
+                     dim3(kThreads), 0, stream, static_cast<const T*>(query),           \
                      static_cast<const T*>(kb), static_cast<const T*>(vb),    \
                      lengths, lengths_dtype, mask, mask_dtype,                \
                      static_cast<T*>(output), part_o, part_ml,                \
@@ -821,7 +974,37 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
                      groups, capacity, mask_len, st[0], st[1], st[2],         \
                      static_cast<int>(st[3]), st[4], st[5],                   \
                      static_cast<int>(st[6]), st[7], st[8], scale,            \
-                     static_cast<int>(chunk), static_cast<int>(nchunks), counters)
+                     static_cast<int>(chunk), static_cast<int>(nchunks), counters, rs)
+  RopeStore rs{};
+  if (rope != nullptr) {
+    // The advance rides on the in-kernel merge (or, with one chunk, on the
+    // workgroup's end); int64 lengths only.
+    const int region = counter_region(stream);
+    int* advance = region >= 0 && batch <= kCounterPairs ? merge_counters(region, true) : nullptr;
+    if (advance == nullptr || lengths_dtype != SLC_I64 || (nchunks > 1 && counters == nullptr))
+      return kUnsupported;
+    rs = *rope;
+    rs.counters = advance;
+#define SLC_ROPE(MK) SLC_MFMA_K(MK, true, true)
+    if (mask == nullptr) {
+      SLC_ROPE(0);
+    } else if (mask_dtype == SLC_BF16) {
+      SLC_ROPE(SLC_BF16 + 1);
+    } else if (mask_dtype == SLC_F16) {
+      SLC_ROPE(SLC_F16 + 1);
+    } else {
+      SLC_ROPE(SLC_F32 + 1);
+    }
+#undef SLC_ROPE
+    return slc_host::check_launch("slc_hip_rope_decode_attention");
+  }
+  slc_host::mark_kernel_begin(stream);
+#define SLC_MFMA(MK)                                                          \
+  if (lengths_dtype == SLC_I64) {                                             \
+    SLC_MFMA_K(MK, true, false);                                              \
+  } else {                                                                    \
+    SLC_MFMA_K(MK, false, false);                                             \
+  }
   for (int rep = slc_host::timed_repeats(); rep > 0; --rep) {
     if (mask == nullptr) {
       SLC_MFMA(0);
@@ -834,7 +1017,7 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
     }
   }
 #undef SLC_MFMA
-#undef SLC_MFMA_L
+#undef SLC_MFMA_K
   slc_host::mark_kernel_end(stream);
   int rc = slc_host::check_launch("slc_hip_decode_attention");
   if (rc != SLC_OK || nchunks == 1 || counters != nullptr) return rc;
@@ -998,4 +1181,66 @@ extern "C" int slc_hip_decode_attention(
                                         head_dim, capacity, ml, st, scale,
                                         s);
   }
+}
+
+extern "C" int slc_hip_rope_decode_attention(
+    const void* query, const void* key, const void* value, const void* cosine,
+    const void* sine, void* key_buffer, void* value_buffer, const int64_t* lengths,
+    int64_t* lengths_out, int* overflow, const void* mask, int mask_dtype, void* output,
+    void* workspace, int64_t workspace_bytes, int dtype, int64_t batch, int64_t q_heads,
+    int64_t kv_heads, int64_t head_dim, int64_t capacity, int64_t mask_len, int64_t q_stride_b,
+    int64_t q_stride_h, int64_t k_stride_b, int64_t k_stride_h, int64_t v_stride_b,
+    int64_t v_stride_h, int64_t cos_stride_b, int64_t sin_stride_b, int64_t kv_stride_b,
+    int64_t kv_stride_s, int64_t kv_stride_h, int64_t mask_stride_b, int64_t mask_stride_s,
+    int64_t out_stride_b, int64_t out_stride_h, float scale, void* stream) {
+  SLC_REQUIRE(mask == nullptr || slc_host::is_float_dtype(mask_dtype),
+              "slc_hip_rope_decode_attention: bad mask dtype %d", mask_dtype);
+  SLC_REQUIRE(batch >= 0 && q_heads > 0 && kv_heads > 0 && head_dim > 0 && capacity > 0 &&
+                  mask_len >= 0 && q_heads % kv_heads == 0,
+              "slc_hip_rope_decode_attention: bad sizes");
+  SLC_REQUIRE(batch <= 65535 && kv_heads <= 65535,
+              "slc_hip_rope_decode_attention: batch/kv_heads exceed grid limits");
+  if (batch == 0) return SLC_OK;
+  SLC_REQUIRE(query && key && value && cosine && sine && key_buffer && value_buffer && lengths &&
+                  lengths_out && output,
+              "slc_hip_rope_decode_attention: null pointer");
+  const int64_t groups = q_heads / kv_heads;
+  // The fused kernel's cases; everything else is the caller's two-kernel path.
+  if (!mfma_eligible(dtype, head_dim, groups) || mask_len <= 0) return kUnsupported;
+  const uint64_t bits =
+      reinterpret_cast<uintptr_t>(query) | reinterpret_cast<uintptr_t>(key) |
+      reinterpret_cast<uintptr_t>(value) | reinterpret_cast<uintptr_t>(cosine) |
+      reinterpret_cast<uintptr_t>(sine) | reinterpret_cast<uintptr_t>(key_buffer) |
+      reinterpret_cast<uintptr_t>(value_buffer);
+  const int64_t strides = q_stride_b | q_stride_h | k_stride_b | k_stride_h | v_stride_b |
+                          v_stride_h | cos_stride_b | sin_stride_b | kv_stride_b |
+                          kv_stride_s | kv_stride_h;
+  const int64_t mask_es = mask == nullptr ? 0 : slc_host::dtype_size(mask_dtype);
+  if ((bits & 15) != 0 || (strides & 7) != 0 || kv_stride_s <= 0 || mask_stride_s < 0 ||
+      capacity * kv_stride_s * 2 >= (int64_t{1} << 31) ||
+      mask_len * mask_stride_s * mask_es >= (int64_t{1} << 31) || capacity >= (int64_t{1} << 30))
+    return kUnsupported;
+  const int64_t chunk = choose_chunk(batch, kv_heads, mask_len, 0);
+  const int64_t nchunks = slc_host::ceil_div(mask_len, chunk);
+  const int64_t need = nchunks > 1 ? batch * q_heads * nchunks * (head_dim + 2) * 4 : 0;
+  SLC_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need),
+              "slc_hip_rope_decode_attention: workspace of %lld bytes needed, got %lld",
+              (long long)need, (long long)workspace_bytes);
+  const int64_t st[9] = {q_stride_b,    q_stride_h,    kv_stride_b,  kv_stride_s, kv_stride_h,
+                         mask_stride_b, mask_stride_s, out_stride_b, out_stride_h};
+  RopeStore rope{key,          value,        cosine,       sine,        k_stride_b,
+                 k_stride_h,   v_stride_b,   v_stride_h,   cos_stride_b, sin_stride_b,
+                 lengths_out,  overflow,     nullptr};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define SLC_ROPE_CALL(TT, DD)                                                                  \
+  launch_mfma<TT, DD>(query, key_buffer, value_buffer, lengths, SLC_I64, mask, mask_dtype,     \
+                      output, workspace, batch, q_heads, kv_heads, capacity, mask_len, st,     \
+                      scale, chunk, nchunks, s, &rope)
+  if (dtype == SLC_BF16) {
+    if (head_dim == 64) return SLC_ROPE_CALL(slc::bf16_t, 64);
+    return SLC_ROPE_CALL(slc::bf16_t, 128);
+  }
+  if (head_dim == 64) return SLC_ROPE_CALL(slc::f16_t, 64);
+  return SLC_ROPE_CALL(slc::f16_t, 128);
+#undef SLC_ROPE_CALL
 }

@@ -28,6 +28,7 @@ import torch.nn.functional as F
 from .backends import (
     hip_add,
     hip_decode_attention,
+    hip_rope_decode_attention,
     hip_embedding,
     hip_kv_advance,
     hip_kv_store,
@@ -277,6 +278,44 @@ class PreallocatedKVCacheState:
         return q_rot, replace(self, lengths=tuple(lengths), generation=self.generation + 1,
                               zero_slots=zero)
 
+    def rope_store_attention(
+        self,
+        slot: int,
+        query: torch.Tensor,
+        key: torch.Tensor,
+        value: torch.Tensor,
+        cosine: torch.Tensor,
+        sine: torch.Tensor,
+        attention_mask: torch.Tensor,
+        *,
+        groups: int,
+        scale: float,
+    ) -> tuple[torch.Tensor, "PreallocatedKVCacheState"]:
+        """``rope_store_advance(slot, ..., delta=1)`` then ``decode_attention``
+        of the rotated query over the advanced state, in one kernel where it
+        takes the case (else the two ops): the attention output and the
+        advanced state."""
+
+        positions = self.positions(slot)
+        buffer_key, buffer_value = self._validate_store(slot, key, value, positions)
+        self._attention_inputs(slot, query, attention_mask, groups)
+        out = positions if self.in_place_lengths else torch.empty_like(positions)
+        result = None
+        if key.shape[2] == 1:
+            result = hip_rope_decode_attention(
+                query, key, value, cosine, sine, buffer_key, buffer_value, positions, out,
+                attention_mask, scale=scale, overflow=self.overflow,
+            )
+        if result is None:
+            q_rot, state = self.rope_store_advance(slot, query, key, value, cosine, sine, delta=1)
+            return state.decode_attention(slot, q_rot, attention_mask, groups=groups,
+                                          scale=scale), state
+        lengths = list(self.lengths)
+        lengths[slot] = out
+        zero = None if self.zero_slots is None else self.zero_slots - {slot}
+        return result, replace(self, lengths=tuple(lengths), generation=self.generation + 1,
+                               zero_slots=zero)
+
     def prefill_store(
         self,
         slot: int,
@@ -360,6 +399,7 @@ class HipExecutor:
             "kernel.hip.norm_linear_swiglu": self._norm_linear_swiglu,
             "kernel.hip.linear_residual": self._linear_residual,
             "kernel.hip.rope_kv_store": self._rope_kv_store,
+            "kernel.hip.rope_store_attention": self._rope_store_attention,
             "runtime.kv.init": self._kv_init,
             "runtime.kv.length": self._kv_length,
             "runtime.kv.advance": self._kv_advance,
@@ -527,6 +567,22 @@ class HipExecutor:
             # positions is this slot's length tensor (the fusion pass checks it).
             return state.rope_store_advance(slot, query, key, value, cosine, sine, delta=delta)
         return state.rope_store(slot, query, key, value, cosine, sine, positions)
+
+    @staticmethod
+    def _rope_store_attention(operands, attributes):
+        if len(operands) != 8 or not isinstance(operands[0], PreallocatedKVCacheState):
+            raise ExecutionError(
+                "kernel.hip.rope_store_attention takes state, q, k, v, cos, sin, positions, mask"
+            )
+        state, query, key, value, cosine, sine, _positions, mask = operands
+        if query.shape[-1] != int(attributes["head_dim"]):
+            raise ExecutionError("kernel.hip.rope_store_attention head dim mismatch")
+        # positions is this slot's length tensor and the advance is one token
+        # (the fusion pass checks both).
+        return state.rope_store_attention(
+            int(attributes.get("slot", 0)), query, key, value, cosine, sine, mask,
+            groups=int(attributes["groups"]), scale=float(attributes["scale"]),
+        )
 
     @staticmethod
     def _embedding(operands, attributes):

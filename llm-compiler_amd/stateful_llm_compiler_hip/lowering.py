@@ -81,6 +81,7 @@ _FUSED_OPERATIONS = frozenset({
     "kernel.hip.norm_linear_swiglu",
     "kernel.hip.linear_residual",
     "kernel.hip.rope_kv_store",
+    "kernel.hip.rope_store_attention",
 })
 
 EXECUTABLE_OPERATIONS = (

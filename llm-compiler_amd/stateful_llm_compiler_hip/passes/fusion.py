@@ -11,6 +11,7 @@ memory):
   linear -> add (with a residual)                   kernel.hip.linear_residual
   rope -> kv_store of the rotated key               kernel.hip.rope_kv_store
   rope_kv_store -> kv.advance of the same slot      kernel.hip.rope_kv_store (advance)
+  rope_kv_store (advance 1) -> decode_attention     kernel.hip.rope_store_attention
 
 A chain is fused only when its intermediate values have no other user and
 are not returned, so no value the program can observe disappears.  The
@@ -64,7 +65,8 @@ def _fuse_function(function: Function) -> Counter[str]:
     counts: Counter[str] = Counter()
     # Each rule runs to a fixed point before the next so that the SwiGLU rule
     # sees the gate/up linears before the group rule could claim them.
-    for rule in (_fuse_swiglu, _fuse_group, _fuse_residual, _fuse_rope_store, _fuse_store_advance):
+    for rule in (_fuse_swiglu, _fuse_group, _fuse_residual, _fuse_rope_store, _fuse_store_advance,
+                 _fuse_store_attention):
         while True:
             name = rule(function)
             if name is None:
@@ -305,4 +307,49 @@ def _fuse_store_advance(function: Function) -> str | None:
                         attributes, store.effects)
         _replace(function, [s_index, a_index], a_index, new)
         return "kernel.hip.rope_kv_store+advance"
+    return None
+
+
+def _fuse_store_attention(function: Function) -> str | None:
+    """rope_kv_store advancing by one token whose rotated query and advanced
+    state feed a decode_attention of the same slot (the query nowhere else,
+    nothing touching either state in between): one kernel stores, advances
+    and attends."""
+
+    ops = function.block.operations
+    uses = _uses(function)
+    for s_index, store in enumerate(ops):
+        if store.name != "kernel.hip.rope_kv_store" or store.attributes.get("advance") != 1:
+            continue
+        q_rot, state_out = store.results
+        users = uses[id(q_rot)]
+        if len(users) != 1 or users[0][0] >= len(ops) or users[0][1] != 1:
+            continue
+        a_index = users[0][0]
+        attention = ops[a_index]
+        if (attention.name != "kernel.hip.decode_attention" or len(attention.operands) != 3
+                or attention.operands[0] is not state_out
+                or attention.attributes.get("slot", 0) != store.attributes.get("slot", 0)):
+            continue
+        state_in = store.operands[0]
+        between = range(s_index + 1, a_index)
+        if any(user in between for value in (state_in, state_out) for user, _ in uses[id(value)]):
+            continue
+        attributes = {
+            "slot": store.attributes.get("slot", 0),
+            "head_dim": store.attributes.get("head_dim"),
+            "variant": store.attributes.get("variant"),
+            "advance": 1,
+            "groups": attention.attributes["groups"],
+            "scale": attention.attributes["scale"],
+            "algorithm": attention.attributes.get("algorithm"),
+            "numerical_mode": attention.attributes.get("numerical_mode"),
+            "fused_from": list(store.attributes.get("fused_from", [store.name])) + [attention.name],
+            "lowered_from": str(store.attributes.get("lowered_from", "")) + "+serve.decode_attention",
+        }
+        new = Operation("kernel.hip.rope_store_attention",
+                        list(store.operands) + [attention.operands[2]],
+                        [attention.results[0], state_out], attributes, store.effects)
+        _replace(function, [s_index, a_index], a_index, new)
+        return new.name
     return None

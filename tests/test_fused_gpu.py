@@ -176,3 +176,86 @@ def test_rope_kv_store_advance_matches_store_then_advance(gpu, in_place):
         assert int(flag1.item()) == int(flag2.item()) == (1 if step >= 1 else 0)
         if not in_place:
             assert pos1.tolist() == start.tolist()
+
+
+@pytest.mark.parametrize(
+    "B,QH,KVH,D,cap,mask_len,dtype,mask_kind,in_place,starts",
+    [
+        # one chunk, positions up to the capacity (the last overflows from step 1)
+        (5, 14, 2, 64, 64, 64, torch.bfloat16, "bf16", True, [0, 3, 17, 62, 63]),
+        # split sequence (in-kernel merge), empty chunks, new row in chunk 0 / mid / last
+        (3, 14, 2, 64, 2048, 2048, torch.bfloat16, "f32", False, [0, 700, 2040]),
+        # D = 128, groups of 4, fp16, no mask
+        (4, 8, 2, 128, 1024, 1024, torch.float16, "none", True, [5, 255, 256, 1000]),
+        # groups of 1
+        (2, 4, 4, 64, 600, 600, torch.bfloat16, "bf16", True, [100, 599]),
+        # new row past the mask: stored by the last chunk, not attended
+        (2, 14, 2, 64, 512, 300, torch.bfloat16, "bf16", False, [400, 10]),
+        # a wide batch: many chunks per sequence and many workgroups per batch
+        (40, 14, 2, 64, 4096, 4096, torch.bfloat16, "bf16", True, list(range(0, 4000, 100))),
+    ],
+)
+def test_rope_decode_attention_matches_store_then_attention(gpu, B, QH, KVH, D, cap, mask_len,
+                                                            dtype, mask_kind, in_place, starts):
+    # One kernel rotates, stores, advances and attends; the same three steps as
+    # rope_kv_store(advance=1) then decode attention, bit for bit, over three
+    # consecutive calls (counters re-armed each time).
+    from stateful_llm_compiler_hip.backends import hip_decode_attention, hip_rope_decode_attention
+
+    announce(f"rope_decode_attention B={B} QH={QH} KVH={KVH} D={D} cap={cap} mask={mask_len} "
+             f"{dtype} {mask_kind} in_place={in_place}")
+    g = generator(B * 7 + D + cap)
+    kb1 = _t(g, B, cap, KVH, D, dtype=dtype, device=gpu)
+    vb1 = _t(g, B, cap, KVH, D, dtype=dtype, device=gpu)
+    kb2, vb2 = kb1.clone(), vb1.clone()
+    start = torch.tensor(starts, device=gpu)
+    for step in range(3):
+        q = _t(g, B, 1, QH * D, dtype=dtype, device=gpu).view(B, 1, QH, D).transpose(1, 2)
+        k = _t(g, B, 1, KVH * D, dtype=dtype, device=gpu).view(B, 1, KVH, D).transpose(1, 2)
+        v = _t(g, B, 1, KVH * D, dtype=dtype, device=gpu).view(B, 1, KVH, D).transpose(1, 2)
+        cos = _t(g, B, 1, D, dtype=dtype, device=gpu)
+        sin = _t(g, B, 1, D, dtype=dtype, device=gpu)
+        if mask_kind == "none":
+            mask = None
+        else:
+            mdt = torch.float32 if mask_kind == "f32" else dtype
+            mask = (torch.randn(B, 1, 1, mask_len, generator=g) * 2).to(mdt).to(gpu)
+        flag1 = torch.zeros(1, dtype=torch.int32, device=gpu)
+        flag2 = torch.zeros(1, dtype=torch.int32, device=gpu)
+        pos1 = (start + step).clone()
+        out1 = pos1 if in_place else torch.full_like(pos1, -7)
+        o1 = hip_rope_decode_attention(q, k, v, cos, sin, kb1, vb1, pos1, out1, mask,
+                                       scale=D ** -0.5, overflow=flag1)
+        assert o1 is not None
+        pos2 = (start + step).clone()
+        q2 = hip_rope_kv_store(q, k, v, cos, sin, kb2, vb2, pos2, overflow=flag2, advance=1,
+                               lengths_out=pos2)
+        o2 = hip_decode_attention(q2, kb2, vb2, pos2, mask, scale=D ** -0.5)
+        torch.cuda.synchronize()
+        assert_bitwise_equal(o1, o2)
+        assert_bitwise_equal(kb1, kb2)
+        assert_bitwise_equal(vb1, vb2)
+        assert out1.tolist() == pos2.tolist() == (start + step + 1).tolist()
+        assert int(flag1.item()) == int(flag2.item())
+        if not in_place:
+            assert pos1.tolist() == (start + step).tolist()
+
+
+def test_rope_decode_attention_declines_unsupported(gpu):
+    # fp32 (no matrix-core kernel): nothing launched, None returned, lengths untouched.
+    from stateful_llm_compiler_hip.backends import hip_rope_decode_attention
+
+    announce("rope_decode_attention fp32 declined")
+    g = generator(5)
+    B, QH, KVH, D, cap = 2, 4, 2, 64, 16
+    q = _t(g, B, QH, 1, D, dtype=torch.float32, device=gpu)
+    k = _t(g, B, KVH, 1, D, dtype=torch.float32, device=gpu)
+    cos = _t(g, B, 1, D, dtype=torch.float32, device=gpu)
+    kb = _t(g, B, cap, KVH, D, dtype=torch.float32, device=gpu)
+    pos = torch.tensor([1, 2], device=gpu)
+    before = kb.clone()
+    assert hip_rope_decode_attention(q, k, k, cos, cos, kb, kb.clone(), pos, pos, None,
+                                     scale=0.125) is None
+    torch.cuda.synchronize()
+    assert pos.tolist() == [1, 2]
+    assert_bitwise_equal(kb, before)

@@ -30,20 +30,39 @@ def test_decode_graph_fuses_every_layer_chain():
     assert c["kernel.hip.norm_linear_group"] == layers + 1   # Q/K/V per layer + the LM head
     assert c["kernel.hip.norm_linear_swiglu"] == layers
     assert c["kernel.hip.linear_residual"] == 2 * layers
-    assert c["kernel.hip.rope_kv_store"] == layers
+    assert c["kernel.hip.rope_store_attention"] == layers
     for gone in ("kernel.hip.rms_norm", "kernel.hip.swiglu", "kernel.hip.add", "kernel.hip.rope",
-                 "kernel.hip.kv_store", "kernel.hip.linear"):
+                 "kernel.hip.kv_store", "kernel.hip.linear", "kernel.hip.rope_kv_store",
+                 "kernel.hip.decode_attention"):
         assert gone not in c, gone
     before = len(plain.module.functions[0].block.operations)
     after = len(fused.module.functions[0].block.operations)
     # per layer: norm+3 linears, norm+2 linears+swiglu, 2 x linear+add,
-    # rope+store, store+advance
-    assert before - after == layers * (3 + 3 + 2 + 1 + 1) + 1
-    assert sum(1 for op in fused.module.functions[0].block.operations
-               if op.name == "kernel.hip.rope_kv_store" and op.attributes.get("advance") == 1) == layers
+    # rope+store, store+advance, store+attention
+    assert before - after == layers * (3 + 3 + 2 + 1 + 1 + 1) + 1
+    fused_ops = [op for op in fused.module.functions[0].block.operations
+                 if op.name == "kernel.hip.rope_store_attention"]
+    assert all(op.attributes["advance"] == 1 and op.attributes["groups"] == 7
+               and len(op.operands) == 8 for op in fused_ops)
     assert "runtime.kv.advance" not in c
     stats = next(p for p in fused.passes if p.name == "fuse-decode-kernels").statistics
     assert stats["fused"]["kernel.hip.rope_kv_store"] == layers
+    assert stats["fused"]["kernel.hip.rope_store_attention"] == layers
+
+
+def test_store_feeding_another_reader_keeps_its_attention():
+    # The first layer's rotated query is returned too: that layer's store and
+    # attention stay apart, the other layer's fuse.
+    result = compile_module(build_decode_module(CONFIG, capacity=64), CompileOptions(fuse=False))
+    function = result.module.functions[0]
+    from stateful_llm_compiler_hip.passes.fusion import FuseDecodeKernelsPass
+    rope = next(op for op in function.block.operations if op.name == "kernel.hip.rope")
+    function.returns.append(rope.results[0])
+    FuseDecodeKernelsPass().run(result.module)
+    verify_module(result.module)
+    c = _counts(result.module)
+    assert c["kernel.hip.rope_store_attention"] == CONFIG.num_layers - 1
+    assert c["kernel.hip.decode_attention"] == 1 and c["kernel.hip.rope_kv_store"] == 1
 
 
 def test_vocabulary_sized_head_keeps_its_norm():
@@ -61,7 +80,8 @@ def test_prefill_graph_fuses_and_compat_mode_does_not():
                             CompileOptions(numerical_mode="pytorch_compatible"))
     names = set(_counts(compat.module))
     assert not names & {"kernel.hip.norm_linear_group", "kernel.hip.norm_linear_swiglu",
-                        "kernel.hip.linear_residual", "kernel.hip.rope_kv_store"}
+                        "kernel.hip.linear_residual", "kernel.hip.rope_kv_store",
+                        "kernel.hip.rope_store_attention"}
 
 
 def test_value_with_another_user_is_not_fused_away():

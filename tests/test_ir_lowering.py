@@ -122,15 +122,16 @@ def test_full_lowering_of_24_layer_graphs(mode):
     if mode == "fast":
         # The per-layer advance rides on the rope + store kernel.
         assert "runtime.kv.advance" not in counts
-        assert counts["kernel.hip.rope_kv_store"] == 24
+        # ... and the store, advance and attention run as one kernel.
+        assert counts["kernel.hip.rope_store_attention"] == 24
+        assert "kernel.hip.rope_kv_store" not in counts
         # Every layer's chains are fused; the vocabulary-sized LM head keeps
         # its own norm and linear.
         assert counts["kernel.hip.linear"] == 1 and counts["kernel.hip.rms_norm"] == 1
         assert counts["kernel.hip.norm_linear_group"] == 24
         assert counts["kernel.hip.norm_linear_swiglu"] == 24
         assert counts["kernel.hip.linear_residual"] == 48
-        assert counts["kernel.hip.rope_kv_store"] == 24
-        assert counts["kernel.hip.decode_attention"] == 24
+        assert "kernel.hip.decode_attention" not in counts
         assert not any(name.startswith("kernel.rocm_compat") for name in counts)
         plain = compile_module(build_decode_module(config, capacity=2048), CompileOptions(fuse=False))
         plain_counts = plain.coverage.lowered_by_name
