@@ -8,9 +8,9 @@
 //  * norm_linear_group   rms_norm -> up to three linears reading its output
 //                        (Q/K/V).  Every workgroup normalises the <= 32 input
 //                        rows into LDS with the rms_norm kernel's own row
-//                        routine, then streams its 16 weight rows.
+//                        routine, then streams its share of the weight rows.
 //  * norm_linear_swiglu  rms_norm -> gate and up linears -> swiglu.  A
-//                        workgroup owns 16 features of both projections and
+//                        workgroup owns a run of features of both projections and
 //                        applies SwiGLU to the rounded results.
 //  * linear_residual     linear -> residual add (O and down projections).
 //  * rope_kv_store       rope -> kv_store of the rotated keys and the values;
@@ -81,27 +81,36 @@ struct FusedArgs {
   void* y[kMaxMatrices];           // [rows, n_j] with row stride y_rs_j
   int n[kMaxMatrices];
   int64_t y_rs[kMaxMatrices];
-  int block_end[kMaxMatrices];     // cumulative 16-feature blocks
+  int feat;                        // features per workgroup (1..32)
+  int block_end[kMaxMatrices];     // cumulative workgroups per matrix
   const void* residual;            // [rows, n_0] with row stride r_rs
   int64_t r_rs;
-  int splits;                      // workgroups sharing one feature block's K
-  int region;                      // split-K scratch region of the calling stream
 };
 
-// ---- split-K across workgroups (narrow projections) ------------------------
-// A feature block whose K is split over `splits` workgroups: each publishes
-// its partial sums with agent-scope stores, bumps the block's counter, and
-// the workgroup that completes the count adds the partials in split order
-// (so the result does not depend on which finished last), applies the
-// epilogue and re-arms the counter.  The scratch lives in static device
-// memory, one region per stream (assigned on the host), so calls that run
-// concurrently on different streams do not share counters.
-constexpr int kSplitRegions = 16;
-constexpr int kSplitBlocks = 256;      // feature blocks per split call
-constexpr int kMaxSplits = 4;
-constexpr int kSplitFloats = kSplitBlocks * kMaxSplits * 2 * 256;  // MB <= 2: 2 MiB
-__device__ int g_split_counters[kSplitRegions][kSplitBlocks];
-__device__ float g_split_partials[kSplitRegions][kSplitFloats];
+// ---- one round of equal workgroups -------------------------------------------
+// A decode-sized projection streams its weights once; every CU should pull an
+// equal share, so a call runs about kTargetGroups workgroups of feat =
+// ceil(features / kTargetGroups) consecutive features each (one or two MFMA
+// tiles of 16 features, the rows past feat masked off by the buffer range).
+// Each workgroup's waves split K; a feature's sum (MFMA steps in k order per
+// wave, then the wave partials in wave order) does not depend on feat, so the
+// fused ops and the single linears they replace agree bit for bit.
+constexpr int kTargetGroups = 256;  // MI355X CUs
+constexpr int kMaxFeat = 32;
+int features_per_group(int64_t features) {
+  const int64_t f = (features + kTargetGroups - 1) / kTargetGroups;
+  return static_cast<int>(f < 1 ? 1 : (f > kMaxFeat ? kMaxFeat : f));
+}
+void assign_blocks(FusedArgs& a, int count) {
+  int64_t total = 0;
+  for (int i = 0; i < count; ++i) total += a.n[i];
+  a.feat = features_per_group(total);
+  int blocks = 0;
+  for (int i = 0; i < kMaxMatrices; ++i) {
+    if (i < count) blocks += (a.n[i] + a.feat - 1) / a.feat;
+    a.block_end[i] = blocks;
+  }
+}
 
 // LDS row stride of the normalised input, in elements: 8 extra elements move
 // consecutive rows 4 banks apart, so the 16-row operand reads do not collide.
@@ -109,7 +118,8 @@ __host__ __device__ constexpr int norm_row(int hidden) { return hidden + 8; }
 
 // NV: 16-byte vectors per lane of the norm prologue (0 = no norm, the input
 // rows are read from global memory like the decode linear kernel does).
-template <typename T, int MB, int KW, int U, int NV, int EPI>
+// TILES: 16-feature MFMA tiles per workgroup (feat <= 16 * TILES).
+template <typename T, int MB, int KW, int U, int NV, int EPI, int TILES>
 __global__ __launch_bounds__(KW * 64) void fused_rows_kernel(FusedArgs p) {
   constexpr int kWaves = KW;
   using MF = Mfma<T>;
@@ -122,35 +132,36 @@ __global__ __launch_bounds__(KW * 64) void fused_rows_kernel(FusedArgs p) {
   const int g = lane >> 4;
   const int K = p.hidden;
   const int M = p.rows;
+  const int F = p.feat;
 
-  // The matrix and feature block of this workgroup.
+  // The matrix and features [n0, n0 + F) of this workgroup.
   const int blk = blockIdx.x;
   const int j = blk < p.block_end[0] ? 0 : (blk < p.block_end[1] ? 1 : 2);
-  const int n0 = (blk - (j == 0 ? 0 : p.block_end[j - 1])) * 16;
+  const int n0 = (blk - (j == 0 ? 0 : p.block_end[j - 1])) * F;
   const int N = p.n[j];
+  const int w_rows = min(F, N - n0);
 
   const int xs_bytes = NV > 0 ? MB * 16 * norm_row(K) * 2 : 0;
   unsigned char* xs = smem;
-  float* partial = reinterpret_cast<float*>(smem + xs_bytes);  // [NW][kWaves][MB][64][4]
+  float* partial = reinterpret_cast<float*>(smem + xs_bytes);  // [NW][TILES][kWaves][MB][64][4]
 
-
-  // K range of this workgroup (its split), then of this wave.
-  const int all_steps = (K + 31) / 32;             // 32-wide MFMA k-steps
-  const int split = blockIdx.y;
-  const int per_split = (all_steps + p.splits - 1) / p.splits;
-  const int split_begin = split * per_split;
-  const int steps = min(all_steps, split_begin + per_split);
-  const int per_wave = (steps - split_begin + kWaves - 1) / kWaves;
-  const int s_begin = split_begin + wave * per_wave;
+  // K range of this wave.
+  const int steps = (K + 31) / 32;             // 32-wide MFMA k-steps
+  const int per_wave = (steps + kWaves - 1) / kWaves;
+  const int s_begin = wave * per_wave;
   const int s_end = min(s_begin + per_wave, steps);
 
-  const int w_rows = min(16, N - n0);
-  __amdgpu_buffer_rsrc_t rw[NW];
-  rw[0] = make_rsrc(static_cast<const T*>(p.w[j]) + static_cast<int64_t>(n0) * K,
-                    static_cast<int64_t>(w_rows) * K * 2);
-  if constexpr (NW == 2)
-    rw[1] = make_rsrc(static_cast<const T*>(p.w[1]) + static_cast<int64_t>(n0) * K,
-                      static_cast<int64_t>(w_rows) * K * 2);
+  __amdgpu_buffer_rsrc_t rw[NW][TILES];
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) {
+    const int rows_t = max(0, min(16, w_rows - 16 * t));
+#pragma unroll
+    for (int h = 0; h < NW; ++h) {
+      const void* base = p.w[NW == 2 ? h : j];
+      rw[h][t] = make_rsrc(static_cast<const T*>(base) + static_cast<int64_t>(n0 + 16 * t) * K,
+                           static_cast<int64_t>(rows_t) * K * 2);
+    }
+  }
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(
       p.x, (static_cast<int64_t>(M) - 1) * p.x_rs * 2 + static_cast<int64_t>(K) * 2);
   const int w_off = c * K * 2 + g * 16;
@@ -161,23 +172,27 @@ __global__ __launch_bounds__(KW * 64) void fused_rows_kernel(FusedArgs p) {
                       : static_cast<int>((i * 16 + c) * p.x_rs * 2) + g * 16;
   }
 
-  f32x4_t acc[NW][MB];
+  f32x4_t acc[NW][TILES][MB];
 #pragma unroll
   for (int h = 0; h < NW; ++h)
 #pragma unroll
-    for (int i = 0; i < MB; ++i) acc[h][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < TILES; ++t)
+#pragma unroll
+      for (int i = 0; i < MB; ++i) acc[h][t][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   // Weight (and, without the norm, input) operands U k-steps at a time, the
   // next batch in flight while the current one is multiplied.
-  uint4 wa[U][NW], wb[U][NW], xa[U][NV > 0 ? 1 : MB], xb[U][NV > 0 ? 1 : MB];
-  auto fetch = [&](int s0, uint4 (&wr)[U][NW], uint4 (&xr)[U][NV > 0 ? 1 : MB]) {
+  uint4 wa[U][NW][TILES], wb[U][NW][TILES], xa[U][NV > 0 ? 1 : MB], xb[U][NV > 0 ? 1 : MB];
+  auto fetch = [&](int s0, uint4 (&wr)[U][NW][TILES], uint4 (&xr)[U][NV > 0 ? 1 : MB]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int s = s0 + u;
       const bool ok = s < s_end && s * 32 + g * 8 < K;
 #pragma unroll
       for (int h = 0; h < NW; ++h)
-        wr[u][h] = ok ? buffer_load16(rw[h], w_off + s * 64) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < TILES; ++t)
+          wr[u][h][t] = ok ? buffer_load16(rw[h][t], w_off + s * 64) : make_uint4(0, 0, 0, 0);
       if constexpr (NV == 0) {
 #pragma unroll
         for (int i = 0; i < MB; ++i)
@@ -185,7 +200,8 @@ __global__ __launch_bounds__(KW * 64) void fused_rows_kernel(FusedArgs p) {
       }
     }
   };
-  auto multiply = [&](int s0, const uint4 (&wr)[U][NW], const uint4 (&xr)[U][NV > 0 ? 1 : MB]) {
+  auto multiply = [&](int s0, const uint4 (&wr)[U][NW][TILES],
+                      const uint4 (&xr)[U][NV > 0 ? 1 : MB]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int s = s0 + u;
@@ -201,7 +217,10 @@ __global__ __launch_bounds__(KW * 64) void fused_rows_kernel(FusedArgs p) {
         const auto a = __builtin_bit_cast(typename MF::vec, xv);
 #pragma unroll
         for (int h = 0; h < NW; ++h)
-          acc[h][i] = MF::run(a, __builtin_bit_cast(typename MF::vec, wr[u][h]), acc[h][i]);
+#pragma unroll
+          for (int t = 0; t < TILES; ++t)
+            acc[h][t][i] =
+                MF::run(a, __builtin_bit_cast(typename MF::vec, wr[u][h][t]), acc[h][t][i]);
       }
     }
   };
@@ -242,56 +261,33 @@ __global__ __launch_bounds__(KW * 64) void fused_rows_kernel(FusedArgs p) {
   }
 
   // C layout: lane (col c = feature, rows 4g..4g+3 = input rows of block i).
-  auto part = [&](int h, int v, int i, int l, int r) -> float& {
-    return partial[((((h * kWaves + v) * MB + i) * 64 + l) * 4) + r];
+  auto part = [&](int h, int t, int v, int i, int l, int r) -> float& {
+    return partial[(((((h * TILES + t) * kWaves + v) * MB + i) * 64 + l) * 4) + r];
   };
 #pragma unroll
   for (int h = 0; h < NW; ++h)
 #pragma unroll
-    for (int i = 0; i < MB; ++i)
+    for (int t = 0; t < TILES; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) part(h, wave, i, lane, r) = acc[h][i][r];
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) part(h, t, wave, i, lane, r) = acc[h][t][i][r];
   __syncthreads();
-  if (p.splits > 1) {
-    // Publish this split's sums (wave partials added in wave order).
-    float* mine = g_split_partials[p.region] + (blk * p.splits + split) * MB * 256;
-    for (int idx = tid; idx < MB * 64 * 4; idx += kWaves * 64) {
-      const int i = idx / 256, l = (idx / 4) % 64, r = idx % 4;
-      float sum = 0.0f;
-#pragma unroll
-      for (int v = 0; v < kWaves; ++v) sum += part(0, v, i, l, r);
-      __hip_atomic_store(mine + idx, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    __shared__ int last;
-    if (tid == 0) {
-      int* counter = &g_split_counters[p.region][blk];
-      const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last = before == p.splits - 1;
-      if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!last) return;
-  }
-  for (int idx = tid; idx < MB * 64 * 4; idx += kWaves * 64) {
-    const int i = idx / 256, l = (idx / 4) % 64, r = idx % 4;
-    const int n = n0 + (l & 15);
+  for (int idx = tid; idx < TILES * MB * 256; idx += kWaves * 64) {
+    const int t = idx / (MB * 256);
+    const int e = idx % (MB * 256);
+    const int i = e / 256, l = (e / 4) % 64, r = e % 4;
+    const int f = 16 * t + (l & 15);
+    const int n = n0 + f;
     const int m = i * 16 + 4 * (l >> 4) + r;
-    if (n >= N || m >= M) continue;
+    if (f >= w_rows || m >= M) continue;
     float sum = 0.0f;
-    if (p.splits > 1) {
-      const float* all = g_split_partials[p.region] + blk * p.splits * MB * 256;
-      for (int q = 0; q < p.splits; ++q)
-        sum += __hip_atomic_load(all + q * MB * 256 + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
 #pragma unroll
-      for (int v = 0; v < kWaves; ++v) sum += part(0, v, i, l, r);
-    }
+    for (int v = 0; v < kWaves; ++v) sum += part(0, t, v, i, l, r);
     if constexpr (EPI == kSwiglu) {
       float up = 0.0f;
 #pragma unroll
-      for (int v = 0; v < kWaves; ++v) up += part(1, v, i, l, r);
+      for (int v = 0; v < kWaves; ++v) up += part(1, t, v, i, l, r);
       const float gate = slc::round_to<T>(sum);
       static_cast<T*>(p.y[0])[m * p.y_rs[0] + n] =
           slc::from_f32<T>(slc::swiglu_value<T>(gate, slc::round_to<T>(up)));
@@ -311,9 +307,10 @@ int launch_rows(FusedArgs& a, hipStream_t stream) {
   const int blocks = a.block_end[kMaxMatrices - 1];
   const int nw = EPI == kSwiglu ? 2 : 1;
   const int kw = waves_for(a.hidden);
+  const int tiles = a.feat > 16 ? 2 : 1;
   auto go = [&](auto kernel, int mb) {
     const int xs_bytes = NV > 0 ? mb * 16 * norm_row(a.hidden) * 2 : 0;
-    const int bytes = xs_bytes + nw * kw * mb * 64 * 4 * 4;
+    const int bytes = xs_bytes + nw * tiles * kw * mb * 64 * 4 * 4;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
     if (e != hipSuccess) {
@@ -321,15 +318,19 @@ int launch_rows(FusedArgs& a, hipStream_t stream) {
                           hipGetErrorString(e));
       return static_cast<int>(e);
     }
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(a.splits)),
-                       dim3(kw * 64), static_cast<unsigned>(bytes), stream, a);
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kw * 64),
+                       static_cast<unsigned>(bytes), stream, a);
     return slc_host::check_launch("fused decode kernel");
   };
   // Prefetch depth: as deep as the registers allow (two weight streams for
-  // SwiGLU halve it).
+  // SwiGLU, and two tiles, divide it).
   constexpr int U1 = EPI == kSwiglu ? 4 : 8, U2 = EPI == kSwiglu ? 2 : 4;
-  if (a.rows <= 16) return go(fused_rows_kernel<T, 1, 8, U1, NV, EPI>, 1);
-  return go(fused_rows_kernel<T, 2, 8, U2, NV, EPI>, 2);
+  if (tiles == 2) {
+    if (a.rows <= 16) return go(fused_rows_kernel<T, 1, 8, U1 / 2, NV, EPI, 2>, 1);
+    return go(fused_rows_kernel<T, 2, 8, U2 / 2, NV, EPI, 2>, 2);
+  }
+  if (a.rows <= 16) return go(fused_rows_kernel<T, 1, 8, U1, NV, EPI, 1>, 1);
+  return go(fused_rows_kernel<T, 2, 8, U2, NV, EPI, 1>, 2);
 }
 
 // Wide projections (the vocabulary head): enough 16-feature blocks to fill
@@ -419,40 +420,8 @@ int launch_wide(FusedArgs& a, hipStream_t stream) {
   return slc_host::check_launch("decode linear (wide)");
 }
 
-// Split-K region of a stream: the first kSplitRegions distinct streams each
-// get one; later streams run without split-K (region -1).
-int split_region(hipStream_t stream) {
-  static std::mutex lock;
-  static hipStream_t owners[kSplitRegions];
-  static int used = 0;
-  std::lock_guard<std::mutex> guard(lock);
-  for (int i = 0; i < used; ++i)
-    if (owners[i] == stream) return i;
-  if (used == kSplitRegions) return -1;
-  owners[used] = stream;
-  return used++;
-}
-
-// Splits of K over workgroups for narrow projections (at most kSplitBlocks
-// feature blocks) with a long K (at least kSplitMinSteps k-steps; for short
-// K the cross-workgroup tail costs more than the split saves): up to
-// kMaxSplits, keeping at least 8 k-steps (one per wave) per split.  The count
-// depends on K alone, so a fused op and the single linears it replaces split
-// identically and agree bit for bit.
-constexpr int kSplitMinSteps = 64;
-int choose_splits(int blocks, int hidden, int epi, hipStream_t stream, int& region) {
-  region = 0;
-  const int steps = (hidden + 31) / 32;
-  if (epi == kSwiglu || blocks > kSplitBlocks || steps < kSplitMinSteps) return 1;
-  const int splits = kMaxSplits < steps / 8 ? kMaxSplits : steps / 8;
-  if (splits <= 1) return 1;
-  region = split_region(stream);
-  return region < 0 ? (region = 0, 1) : splits;
-}
-
 template <int EPI>
 int dispatch_rows(FusedArgs& a, int dtype, hipStream_t stream) {
-  a.splits = choose_splits(a.block_end[kMaxMatrices - 1], a.hidden, EPI, stream, a.region);
   const bool norm = a.norm_w != nullptr;
   const int nv = (a.hidden / 8 + 63) / 64;  // 16-byte vectors per lane
 #define SLC_ROWS(T)                                             \
@@ -602,12 +571,11 @@ int rows_linear(const void* x, int64_t x_rs, int64_t rows, int64_t K, int64_t N,
   a.y[0] = y;
   a.n[0] = static_cast<int>(N);
   a.y_rs[0] = y_rs;
-  const int blocks = static_cast<int>((N + 15) / 16);
-  a.block_end[0] = a.block_end[1] = a.block_end[2] = blocks;
-  if (blocks >= kWideBlocks) {
+  if ((N + 15) / 16 >= kWideBlocks) {
     return dtype == SLC_BF16 ? launch_wide<slc::bf16_t>(a, stream)
                              : launch_wide<slc::f16_t>(a, stream);
   }
+  assign_blocks(a, 1);
   return dispatch_rows<kStore>(a, dtype, stream);
 }
 
@@ -641,7 +609,6 @@ extern "C" int slc_hip_norm_linear_group(
   void* ys[3] = {y0, y1, y2};
   const int64_t ns[3] = {n0, n1, n2};
   const int64_t yrs[3] = {y0_rs, y1_rs, y2_rs};
-  int blocks = 0;
   for (int i = 0; i < kMaxMatrices; ++i) {
     if (i < count) {
       SLC_REQUIRE(ws[i] && ys[i] && ns[i] >= 1 && ns[i] <= (1 << 24) && yrs[i] >= ns[i],
@@ -651,10 +618,9 @@ extern "C" int slc_hip_norm_linear_group(
       a.y[i] = ys[i];
       a.n[i] = static_cast<int>(ns[i]);
       a.y_rs[i] = yrs[i];
-      blocks += static_cast<int>((ns[i] + 15) / 16);
     }
-    a.block_end[i] = blocks;
   }
+  assign_blocks(a, count);
   return dispatch_rows<kStore>(a, dtype, static_cast<hipStream_t>(stream));
 }
 
@@ -679,8 +645,7 @@ extern "C" int slc_hip_norm_linear_swiglu(const void* x, int64_t x_rs, const voi
   a.y[0] = y;
   a.n[0] = static_cast<int>(features);
   a.y_rs[0] = y_rs;
-  const int blocks = static_cast<int>((features + 15) / 16);
-  a.block_end[0] = a.block_end[1] = a.block_end[2] = blocks;
+  assign_blocks(a, 1);
   return dispatch_rows<kSwiglu>(a, dtype, static_cast<hipStream_t>(stream));
 }
 
@@ -706,8 +671,7 @@ extern "C" int slc_hip_linear_residual(const void* x, int64_t x_rs, int64_t rows
   a.y_rs[0] = y_rs;
   a.residual = residual;
   a.r_rs = residual_rs;
-  const int blocks = static_cast<int>((out_features + 15) / 16);
-  a.block_end[0] = a.block_end[1] = a.block_end[2] = blocks;
+  assign_blocks(a, 1);
   return dispatch_rows<kResidual>(a, dtype, static_cast<hipStream_t>(stream));
 }
 
