@@ -64,9 +64,10 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int 
 
 enum Epilogue { kStore = 0, kResidual = 1, kSwiglu = 2 };
 
-// Waves per workgroup (the K split).  (16 waves for long K measured twice as
-// slow on the down projection: a quarter of the registers per wave.)
-__host__ __device__ constexpr int waves_for(int) { return 8; }
+// Waves per workgroup (the K split): 16 for long K (the down projection,
+// 7.35 against 7.96 us with 8), else 8.  It depends on K alone, so the fused
+// ops and the single linears they replace split K the same way.
+__host__ __device__ constexpr int waves_for(int k) { return k >= 2048 ? 16 : 8; }
 constexpr int kMaxRows = 32;     // rows (batch x tokens) the fused kernels take
 constexpr int kMaxMatrices = 3;
 
@@ -85,7 +86,10 @@ struct FusedArgs {
   int block_end[kMaxMatrices];     // cumulative workgroups per matrix
   const void* residual;            // [rows, n_0] with row stride r_rs
   int64_t r_rs;
+  int alias_partials;              // partial sums reuse the normalised rows' LDS
 };
+
+constexpr int kLdsBytes = 160 * 1024;  // LDS per CU (gfx950)
 
 // ---- one round of equal workgroups -------------------------------------------
 // A decode-sized projection streams its weights once; every CU should pull an
@@ -143,7 +147,9 @@ __global__ __launch_bounds__(KW * 64) void fused_rows_kernel(FusedArgs p) {
 
   const int xs_bytes = NV > 0 ? MB * 16 * norm_row(K) * 2 : 0;
   unsigned char* xs = smem;
-  float* partial = reinterpret_cast<float*>(smem + xs_bytes);  // [NW][TILES][kWaves][MB][64][4]
+  // [NW][TILES][kWaves][MB][64][4]; after the normalised rows, or over them
+  // when both do not fit (then written only once every wave is done with them).
+  float* partial = reinterpret_cast<float*>(smem + (p.alias_partials ? 0 : xs_bytes));
 
   // K range of this wave.
   const int steps = (K + 31) / 32;             // 32-wide MFMA k-steps
@@ -260,6 +266,7 @@ __global__ __launch_bounds__(KW * 64) void fused_rows_kernel(FusedArgs p) {
     s0 += U;
   }
 
+  if (NV > 0 && p.alias_partials) __syncthreads();
   // C layout: lane (col c = feature, rows 4g..4g+3 = input rows of block i).
   auto part = [&](int h, int t, int v, int i, int l, int r) -> float& {
     return partial[(((((h * TILES + t) * kWaves + v) * MB + i) * 64 + l) * 4) + r];
@@ -310,7 +317,10 @@ int launch_rows(FusedArgs& a, hipStream_t stream) {
   const int tiles = a.feat > 16 ? 2 : 1;
   auto go = [&](auto kernel, int mb) {
     const int xs_bytes = NV > 0 ? mb * 16 * norm_row(a.hidden) * 2 : 0;
-    const int bytes = xs_bytes + nw * tiles * kw * mb * 64 * 4 * 4;
+    const int part_bytes = nw * tiles * kw * mb * 64 * 4 * 4;
+    a.alias_partials = xs_bytes + part_bytes > kLdsBytes;
+    const int bytes = a.alias_partials ? (xs_bytes > part_bytes ? xs_bytes : part_bytes)
+                                       : xs_bytes + part_bytes;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
     if (e != hipSuccess) {
@@ -325,6 +335,16 @@ int launch_rows(FusedArgs& a, hipStream_t stream) {
   // Prefetch depth: as deep as the registers allow (two weight streams for
   // SwiGLU, and two tiles, divide it).
   constexpr int U1 = EPI == kSwiglu ? 4 : 8, U2 = EPI == kSwiglu ? 2 : 4;
+  // 16 waves: half the k-steps per wave, half the prefetch depth.
+  constexpr int V1 = U1 / 2, V2 = U2 / 2;
+  if (kw == 16) {
+    if (tiles == 2) {
+      if (a.rows <= 16) return go(fused_rows_kernel<T, 1, 16, V1 / 2, NV, EPI, 2>, 1);
+      return go(fused_rows_kernel<T, 2, 16, (V2 > 1 ? V2 / 2 : 1), NV, EPI, 2>, 2);
+    }
+    if (a.rows <= 16) return go(fused_rows_kernel<T, 1, 16, V1, NV, EPI, 1>, 1);
+    return go(fused_rows_kernel<T, 2, 16, V2, NV, EPI, 1>, 2);
+  }
   if (tiles == 2) {
     if (a.rows <= 16) return go(fused_rows_kernel<T, 1, 8, U1 / 2, NV, EPI, 2>, 1);
     return go(fused_rows_kernel<T, 2, 8, U2 / 2, NV, EPI, 2>, 2);

@@ -38,7 +38,8 @@ def _check_linear_bf16(actual, x, w, b):
 @pytest.mark.parametrize("rows", [1, 8, 33, 64, 128, 1000])
 @pytest.mark.parametrize(
     "k,n,bias",
-    [(896, 896, True), (896, 128, True), (896, 4864, False), (4864, 896, False)],
+    [(896, 896, True), (896, 128, True), (896, 4864, False), (4864, 896, False),
+     (2048, 6000, True)],
 )
 def test_linear_bf16_qwen_shapes(gpu, rows, k, n, bias):
     from stateful_llm_compiler_hip.backends import hip_linear

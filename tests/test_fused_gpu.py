@@ -33,13 +33,16 @@ def _t(g, *shape, dtype=torch.bfloat16, scale=1.0, device):
 
 @pytest.mark.parametrize("rows", ROWS)
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_norm_linear_group_matches_norm_then_linears(gpu, rows, dtype):
-    announce(f"norm_linear_group rows={rows} {dtype}")
+@pytest.mark.parametrize("hidden,ns", [(896, (896, 128, 128)), (2048, (4096, 512, 520))])
+def test_norm_linear_group_matches_norm_then_linears(gpu, rows, dtype, hidden, ns):
+    # The second shape: 16 waves (long K), two MFMA tiles per workgroup in the
+    # fused call against one in the single linears.
+    announce(f"norm_linear_group rows={rows} {dtype} hidden={hidden} ns={ns}")
     g = generator(rows)
-    h = _t(g, rows, 1, 896, dtype=dtype, device=gpu)
-    nw = _t(g, 896, dtype=dtype, scale=0.5, device=gpu) + 1
-    ws = [_t(g, n, 896, dtype=dtype, scale=0.02, device=gpu) for n in (896, 128, 128)]
-    bs = [_t(g, n, dtype=dtype, scale=0.1, device=gpu) for n in (896, 128, 128)]
+    h = _t(g, rows, 1, hidden, dtype=dtype, device=gpu)
+    nw = _t(g, hidden, dtype=dtype, scale=0.5, device=gpu) + 1
+    ws = [_t(g, n, hidden, dtype=dtype, scale=0.02, device=gpu) for n in ns]
+    bs = [_t(g, n, dtype=dtype, scale=0.1, device=gpu) for n in ns]
     got = hip_norm_linear_group(h, nw, ws, bs, epsilon=1e-6)
     x = hip_rms_norm(h, nw, epsilon=1e-6, round_before_weight=True)
     want = [hip_linear(x, w, b) for w, b in zip(ws, bs)]
@@ -52,13 +55,14 @@ def test_norm_linear_group_matches_norm_then_linears(gpu, rows, dtype):
 
 
 @pytest.mark.parametrize("rows", ROWS)
-def test_norm_linear_swiglu_matches_the_mlp_front(gpu, rows):
-    announce(f"norm_linear_swiglu rows={rows}")
+@pytest.mark.parametrize("hidden,features", [(896, 4864), (2048, 5000)])
+def test_norm_linear_swiglu_matches_the_mlp_front(gpu, rows, hidden, features):
+    announce(f"norm_linear_swiglu rows={rows} hidden={hidden} features={features}")
     g = generator(100 + rows)
-    h = _t(g, rows, 1, 896, device=gpu)
-    nw = _t(g, 896, scale=0.5, device=gpu) + 1
-    wg = _t(g, 4864, 896, scale=0.02, device=gpu)
-    wu = _t(g, 4864, 896, scale=0.02, device=gpu)
+    h = _t(g, rows, 1, hidden, device=gpu)
+    nw = _t(g, hidden, scale=0.5, device=gpu) + 1
+    wg = _t(g, features, hidden, scale=0.02, device=gpu)
+    wu = _t(g, features, hidden, scale=0.02, device=gpu)
     got = hip_norm_linear_swiglu(h, nw, wg, wu, epsilon=1e-6)
     x = hip_rms_norm(h, nw, epsilon=1e-6, round_before_weight=True)
     want = hip_swiglu(hip_linear(x, wg), hip_linear(x, wu))
@@ -67,7 +71,7 @@ def test_norm_linear_swiglu_matches_the_mlp_front(gpu, rows):
 
 
 @pytest.mark.parametrize("rows", ROWS)
-@pytest.mark.parametrize("n,k", [(896, 896), (896, 4864), (100, 64)])
+@pytest.mark.parametrize("n,k", [(896, 896), (896, 4864), (100, 64), (6000, 2048)])
 def test_linear_residual_matches_linear_then_add(gpu, rows, n, k):
     announce(f"linear_residual rows={rows} n={n} k={k}")
     g = generator(200 + rows + n)
