@@ -64,10 +64,11 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int 
 
 enum Epilogue { kStore = 0, kResidual = 1, kSwiglu = 2 };
 
-// Waves per workgroup (the K split): 16 for long K (the down projection,
-// 7.35 against 7.96 us with 8), else 8.  It depends on K alone, so the fused
-// ops and the single linears they replace split K the same way.
-__host__ __device__ constexpr int waves_for(int k) { return k >= 2048 ? 16 : 8; }
+// Waves per workgroup (the K split): 16 from K = 512 (more loads in flight
+// per CU: Qwen2 decode SwiGLU 8.1 against 8.9 us with 8, down projection 7.3
+// against 8.0), else 8.  It depends on K alone, so the fused ops and the
+// single linears they replace split K the same way.
+__host__ __device__ constexpr int waves_for(int k) { return k >= 512 ? 16 : 8; }
 constexpr int kMaxRows = 32;     // rows (batch x tokens) the fused kernels take
 constexpr int kMaxMatrices = 3;
 
