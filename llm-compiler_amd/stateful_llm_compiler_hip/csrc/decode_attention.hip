@@ -392,17 +392,20 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   // ROPE: the query arrives unrotated and is rotated here; every lane also
   // holds its slices of the new token's rotated key and its value (each
   // rotation pair, dims d and d + D/2, is the lane's slices kk and kk + KK/2).
+  // (The rotation itself waits until the first tiles are requested: the tile
+  // loads must not queue behind these operands.)
   typename M::vec qv[KK];
-  uint4 knew[ROPE ? KK : 1], vnew[ROPE ? KK : 1];
+  uint4 qraw[KK];
+  constexpr int KR = ROPE ? KK : 1;
+  uint4 knew[KR], vnew[KR], cs[KR], sn[KR];
   {
     const int head = kvh * groups + c;
-    uint4 raw[KK];
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
-      raw[kk] = make_uint4(0, 0, 0, 0);
+      qraw[kk] = make_uint4(0, 0, 0, 0);
       if (c < groups) {
-        raw[kk] = *reinterpret_cast<const uint4*>(query + b * q_sb + head * q_sh +
-                                                  kk * 32 + 8 * g);
+        qraw[kk] = *reinterpret_cast<const uint4*>(query + b * q_sb + head * q_sh +
+                                                   kk * 32 + 8 * g);
       }
     }
     if constexpr (ROPE) {
@@ -410,7 +413,6 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
       const T* vr = static_cast<const T*>(rs.value) + b * rs.v_sb + kvh * rs.v_sh;
       const T* cr = static_cast<const T*>(rs.cosine) + b * rs.c_sb;
       const T* sr = static_cast<const T*>(rs.sine) + b * rs.s_sb;
-      uint4 cs[KK], sn[KK];
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
         const int d = kk * 32 + 8 * g;
@@ -419,11 +421,10 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
         cs[kk] = *reinterpret_cast<const uint4*>(cr + d);
         sn[kk] = *reinterpret_cast<const uint4*>(sr + d);
       }
-      rope_slices<T, KK>(raw, cs, sn);
-      rope_slices<T, KK>(knew, cs, sn);
-    }
+    } else {
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) qv[kk] = as_vec<T>(raw[kk]);
+      for (int kk = 0; kk < KK; ++kk) qv[kk] = as_vec<T>(qraw[kk]);
+    }
   }
 
   const char* kbase = reinterpret_cast<const char*>(key_buffer + b * kv_sb + kvh * kv_sh);
@@ -518,33 +519,41 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   end64 = end64 < capacity ? end64 : capacity;
   const int end = static_cast<int>(end64);  // host guarantees capacity < 2^30
   LenAdvance adv{nullptr, 0, nullptr, 0, nullptr, capacity};
+  // ROPE: rotate the new key and write its row (and the value's) from the
+  // workgroup of the chunk holding it (the last chunk when it lies past the
+  // mask); that workgroup's own tile loads of the row are replaced by the
+  // registers (patch below), so no workgroup depends on when the write lands.
+  auto store_new_row = [&]() {
+    if constexpr (ROPE) {
+      rope_slices<T, KK>(knew, cs, sn);
+      const bool in_range = pos >= 0 && pos < capacity;
+      const int64_t owner =
+          in_range ? min(pos / chunk_tokens, static_cast<int64_t>(nchunks) - 1) : 0;
+      if (in_range && chunk == owner && wave == 0 && c == 0) {
+        char* krow = reinterpret_cast<char*>(const_cast<T*>(key_buffer) + b * kv_sb + kvh * kv_sh) +
+                     pos * static_cast<int64_t>(kv_ss) * 2;
+        char* vrow =
+            reinterpret_cast<char*>(const_cast<T*>(value_buffer) + b * kv_sb + kvh * kv_sh) +
+            pos * static_cast<int64_t>(kv_ss) * 2;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+          *reinterpret_cast<uint4*>(krow + kk * 64 + 16 * g) = knew[kk];
+          *reinterpret_cast<uint4*>(vrow + kk * 64 + 16 * g) = vnew[kk];
+        }
+      }
+      if (!in_range && chunk == 0 && kvh == 0 && tid == 0 && rs.overflow != nullptr)
+        *rs.overflow = 1;
+    }
+  };
   if constexpr (ROPE) {
     adv = LenAdvance{rs.counters + b, kv_heads * nchunks, rs.lengths_out + b, pos + 1,
                      rs.overflow, capacity};
-    // The new row is written by the workgroup of the chunk holding it (the
-    // last chunk when it lies past the mask); that workgroup's own tile
-    // loads of the row are replaced by the registers (patch below), so no
-    // workgroup depends on when the write lands.
-    const bool in_range = pos >= 0 && pos < capacity;
-    const int64_t owner = in_range ? min(pos / chunk_tokens, static_cast<int64_t>(nchunks) - 1) : 0;
-    if (in_range && chunk == owner && wave == 0 && c == 0) {
-      char* krow = reinterpret_cast<char*>(const_cast<T*>(key_buffer) + b * kv_sb + kvh * kv_sh) +
-                   pos * static_cast<int64_t>(kv_ss) * 2;
-      char* vrow = reinterpret_cast<char*>(const_cast<T*>(value_buffer) + b * kv_sb + kvh * kv_sh) +
-                   pos * static_cast<int64_t>(kv_ss) * 2;
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        *reinterpret_cast<uint4*>(krow + kk * 64 + 16 * g) = knew[kk];
-        *reinterpret_cast<uint4*>(vrow + kk * 64 + 16 * g) = vnew[kk];
-      }
-    }
-    if (!in_range && chunk == 0 && kvh == 0 && tid == 0 && rs.overflow != nullptr)
-      *rs.overflow = 1;
   }
   if (nchunks > 1 && chunk_start >= end) {
     // Nothing of this batch in the chunk: an empty partial (max -inf, sum 0),
     // which the merge weighs by zero.  A sequence with no token at all thus
     // merges to 0/0 = NaN, like the reference's softmax over an all -inf row.
+    store_new_row();
     if (tid < groups) {
       const int64_t p = (b * q_heads + kvh * groups + tid) * nchunks + chunk;
       publish(part_ml + 2 * p, -INFINITY, counters);
@@ -560,6 +569,12 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   Tile ta, tb;
   load_tile(t_first, ta, chunk_end);
   load_tile(t_first + kStride, tb, chunk_end);
+  if constexpr (ROPE) {
+    rope_slices<T, KK>(qraw, cs, sn);
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) qv[kk] = as_vec<T>(qraw[kk]);
+    store_new_row();
+  }
 
   auto compute_tile = [&](int t0, const Tile& tile) {
     // S^T tile: two 16-token MFMA blocks; lane holds tokens 16j+4g+r, head c.
