@@ -16,6 +16,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 from __future__ import annotations
 
 import argparse
+import itertools
 import json
 import os
 import sys
@@ -274,12 +275,18 @@ def bench_kernels() -> dict:
         w = torch.randn(n, kk, device=dev, generator=g, dtype=bf) * 0.02
         us = _time_graph(lambda: hip_linear(x, w), reps=10)
         mfma(f"linear_m{m}_n{n}_k{kk}", us, 2 * m * n * kk, f"M{m} N{n} K{kk}")
-    # decode-shaped linears (M = 8): weight streaming
+    # decode-shaped linears (M = 8): weight streaming.  Each graph holds 60
+    # calls cycling over enough weight copies (> 256 MB, the Infinity Cache)
+    # that every call streams its weights from HBM; a graph of a few calls
+    # would time the graph launch instead of the kernel.
     for n, kk in ((4864, 896), (896, 4864), (151936, 896)):
         x = torch.randn(8, kk, device=dev, generator=g, dtype=bf)
-        w = torch.randn(n, kk, device=dev, generator=g, dtype=bf) * 0.02
-        us = _time_graph(lambda: hip_linear(x, w), reps=10)
+        copies = max(1, -(-(300 << 20) // (n * kk * 2)))
+        ws = [torch.randn(n, kk, device=dev, generator=g, dtype=bf) * 0.02 for _ in range(copies)]
+        turn = itertools.cycle(range(copies))
+        us = _time_graph(lambda: hip_linear(x, ws[next(turn)]), reps=60, outer=3)
         hbm(f"linear_m8_n{n}_k{kk}", us, (n * kk + 8 * kk + 8 * n) * 2, f"M8 N{n} K{kk}")
+        del ws
 
     # rms_norm 32768 x 896
     x = torch.randn(32768, 896, device=dev, generator=g, dtype=bf)
