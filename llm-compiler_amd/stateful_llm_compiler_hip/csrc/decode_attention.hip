@@ -175,6 +175,11 @@ struct RopeStore {
   const void* cosine;
   const void* sine;
   int64_t k_sb, k_sh, v_sb, v_sh, c_sb, s_sb;
+  // The KV buffers again, for the new row's write (the kernel's buffer
+  // arguments are read-only views; the only row written is one this
+  // workgroup does not use from memory, see the tile patch).
+  void* key_out;
+  void* value_out;
   int64_t* lengths_out;
   int* overflow;
   int* counters;  // per-batch advance counters of the stream's region
@@ -530,10 +535,10 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
       const int64_t owner =
           in_range ? min(pos / chunk_tokens, static_cast<int64_t>(nchunks) - 1) : 0;
       if (in_range && chunk == owner && wave == 0 && c == 0) {
-        char* krow = reinterpret_cast<char*>(const_cast<T*>(key_buffer) + b * kv_sb + kvh * kv_sh) +
+        char* krow = reinterpret_cast<char*>(static_cast<T*>(rs.key_out) + b * kv_sb + kvh * kv_sh) +
                      pos * static_cast<int64_t>(kv_ss) * 2;
         char* vrow =
-            reinterpret_cast<char*>(const_cast<T*>(value_buffer) + b * kv_sb + kvh * kv_sh) +
+            reinterpret_cast<char*>(static_cast<T*>(rs.value_out) + b * kv_sb + kvh * kv_sh) +
             pos * static_cast<int64_t>(kv_ss) * 2;
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
@@ -1243,9 +1248,9 @@ extern "C" int slc_hip_rope_decode_attention(
               (long long)need, (long long)workspace_bytes);
   const int64_t st[9] = {q_stride_b,    q_stride_h,    kv_stride_b,  kv_stride_s, kv_stride_h,
                          mask_stride_b, mask_stride_s, out_stride_b, out_stride_h};
-  RopeStore rope{key,          value,        cosine,       sine,        k_stride_b,
+  RopeStore rope{key,          value,        cosine,       sine,         k_stride_b,
                  k_stride_h,   v_stride_b,   v_stride_h,   cos_stride_b, sin_stride_b,
-                 lengths_out,  overflow,     nullptr};
+                 key_buffer,   value_buffer, lengths_out,  overflow,     nullptr};
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define SLC_ROPE_CALL(TT, DD)                                                                  \
   launch_mfma<TT, DD>(query, key_buffer, value_buffer, lengths, SLC_I64, mask, mask_dtype,     \
