@@ -21,7 +21,6 @@
 // the waves, the MFMA order and the partial-sum order, hence the same bits.
 // Semantics: src/stateful_llm_compiler/execution.py:674-692 (rms_norm),
 // triton_executor.py:159-176 (linear), :741-767 (rope), :743-781 (kv store).
-#include <mutex>
 
 #include "common.hpp"
 #include "op_math.hpp"
