@@ -28,6 +28,7 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
 template <typename T>
 struct Mfma;
@@ -59,6 +60,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
 __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int offset) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 0));
 }
+// Per-lane offset plus a wave-uniform (scalar) one.
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int offset,
+                                               int uniform) {
+  return __builtin_bit_cast(uint4,
+                            __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, uniform, 0));
+}
 
 constexpr int kBK = 64;            // K elements per tile (128 bytes of bf16)
 constexpr int kChunks = kBK / 8;   // 16-byte chunks per tile row
@@ -68,7 +75,16 @@ __device__ __forceinline__ int lds_offset(int row, int chunk) {
   return row * (kBK * 2) + ((chunk ^ (row & 7)) << 4);
 }
 
-template <typename T, int BM, int BN, int WM, int WN>
+// KFULL: K is a multiple of the 64-wide k-tile, so no load needs a k check
+// (rows past M / N fall outside the buffer ranges and read zero), every
+// per-lane offset is fixed for the whole loop and the k-tile offset is a
+// scalar: the main loop carries no per-load VALU work (with the checks it ran
+// about five VALU instructions per MFMA, as much issue time as the MFMAs).
+// VST: N and the output row stride are multiples of 8 (16-byte aligned rows):
+// each wave stages its output tile through LDS and writes it with 16-byte
+// stores (8 per lane instead of 64 two-byte ones) through a buffer resource
+// whose range ends at the workgroup's last valid output element.
+template <typename T, int BM, int BN, int WM, int WN, bool KFULL, bool VST>
 __global__ __launch_bounds__(256) void linear_mfma_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
     T* __restrict__ y, int M, int N, int K, int64_t x_rs, int64_t y_rs) {
@@ -106,7 +122,27 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(
       make_rsrc(w + static_cast<int64_t>(n0) * K, w_rows > 0 ? w_rows * K * 2 : 0);
 
   uint4 xr[XPT], wr[WPT];
+  static_assert(!KFULL || (XCH % 256 == 0 && WCH % 256 == 0), "whole chunks per thread");
+  int xoff[XPT], woff[WPT];
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int ch = tid + 256 * i;
+    xoff[i] = static_cast<int>((ch / kChunks) * x_rs + (ch % kChunks) * 8) * 2;
+  }
+#pragma unroll
+  for (int i = 0; i < WPT; ++i) {
+    const int ch = tid + 256 * i;
+    woff[i] = ((ch / kChunks) * K + (ch % kChunks) * 8) * 2;
+  }
   auto fetch = [&](int k0) {
+    if constexpr (KFULL) {
+      const int kb = __builtin_amdgcn_readfirstlane(k0 * 2);
+#pragma unroll
+      for (int i = 0; i < XPT; ++i) xr[i] = buffer_load16(rx, xoff[i], kb);
+#pragma unroll
+      for (int i = 0; i < WPT; ++i) wr[i] = buffer_load16(rw, woff[i], kb);
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
       const int ch = tid + 256 * i;
@@ -177,6 +213,40 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(
     __syncthreads();
   }
 
+  if constexpr (VST) {
+    // The loop ended on a barrier, so the LDS is free: wave-private staging
+    // of its TM x TN tile as T, rows padded to keep 16-byte alignment.
+    constexpr int kCPad = TN + 8;
+    static_assert(TM * kCPad * 2 * 4 <= 2 * (XB + WB), "staging fits the LDS");
+    uint16_t* cs = reinterpret_cast<uint16_t*>(smem) + wave * TM * kCPad;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = n0 + wn * TN + j * 16 + c;
+      const float bv = bias != nullptr && n < N ? slc::to_f32(bias[n]) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          cs[(i * 16 + 4 * g + r) * kCPad + j * 16 + c] =
+              slc::from_f32<T>(acc[i][j][r] + bv).bits;
+    }
+    const int rows = M - m0 < BM ? M - m0 : BM;
+    const __amdgpu_buffer_rsrc_t ry =
+        make_rsrc(y + m0 * y_rs, (static_cast<int64_t>(rows) - 1) * y_rs * 2 + N * 2);
+    constexpr int kPerRow = TN / 8;  // 16-byte chunks per staged row
+#pragma unroll
+    for (int q = 0; q < TM * kPerRow / 64; ++q) {
+      const int id = q * 64 + lane;
+      const int row = id / kPerRow, chunk = id % kPerRow;
+      const int m_local = wm * TM + row;
+      const int n = n0 + wn * TN + chunk * 8;
+      const uint4 v = *reinterpret_cast<const uint4*>(cs + row * kCPad + chunk * 8);
+      if (m_local < rows && n < N)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v), ry,
+                                               static_cast<int>(m_local * y_rs + n) * 2, 0, 0);
+    }
+    return;
+  }
   // Epilogue: lane (col c, rows 4g..4g+3) of each 16 x 16 fragment.
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
@@ -334,7 +404,23 @@ template <typename T, int BM, int BN, int WM, int WN>
 int launch_mfma(const void* x, const void* w, const void* bias, void* y, int M,
                 int N, int K, int64_t x_rs, int64_t y_rs, hipStream_t stream) {
   const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
-  hipLaunchKernelGGL((linear_mfma_kernel<T, BM, BN, WM, WN>), grid, dim3(256), 0,
+  const bool vst = N % 8 == 0 && y_rs % 8 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0 &&
+                   static_cast<int64_t>(BM) * y_rs * 2 < (int64_t{1} << 31);
+  if (K % kBK == 0 && vst) {
+    hipLaunchKernelGGL((linear_mfma_kernel<T, BM, BN, WM, WN, true, true>), grid, dim3(256), 0,
+                       stream, static_cast<const T*>(x), static_cast<const T*>(w),
+                       static_cast<const T*>(bias), static_cast<T*>(y), M, N, K,
+                       x_rs, y_rs);
+    return slc_host::check_launch("slc_hip_linear");
+  }
+  if (K % kBK == 0) {
+    hipLaunchKernelGGL((linear_mfma_kernel<T, BM, BN, WM, WN, true, false>), grid, dim3(256), 0,
+                       stream, static_cast<const T*>(x), static_cast<const T*>(w),
+                       static_cast<const T*>(bias), static_cast<T*>(y), M, N, K,
+                       x_rs, y_rs);
+    return slc_host::check_launch("slc_hip_linear");
+  }
+  hipLaunchKernelGGL((linear_mfma_kernel<T, BM, BN, WM, WN, false, false>), grid, dim3(256), 0,
                      stream, static_cast<const T*>(x), static_cast<const T*>(w),
                      static_cast<const T*>(bias), static_cast<T*>(y), M, N, K,
                      x_rs, y_rs);

@@ -218,3 +218,19 @@ def test_prefill_fp16_head_dim_128_generic(gpu):
     announce("prefill fp16 D=128 (generic)")
     actual, expected = _prefill_case(gpu, 1, 40, torch.float16, 9, mask_kind="none", causal=True, q_heads=4, head_dim=128)
     assert_bf16_close(actual, expected)
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 200, 128), (129, 136, 64), (77, 8, 192)])
+def test_linear_bf16_partial_tiles(gpu, m, n, k):
+    # Row and column tiles cut by M and N (N a multiple of 8: the 16-byte
+    # store epilogue), K a multiple of the 64-wide k-tile.
+    from stateful_llm_compiler_hip.backends import hip_linear
+
+    announce(f"linear bf16 partial tiles M={m} N={n} K={k}")
+    g = generator(m + n + k)
+    x = torch.randn(m, k, generator=g).bfloat16()
+    w = (torch.randn(n, k, generator=g) * 0.05).bfloat16()
+    b = (torch.randn(n, generator=g) * 0.05).bfloat16()
+    y = hip_linear(x.to(gpu), w.to(gpu), b.to(gpu))
+    torch.cuda.synchronize()
+    _check_linear_bf16(y, x, w, b)
