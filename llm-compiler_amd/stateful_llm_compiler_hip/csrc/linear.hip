@@ -85,19 +85,19 @@ __device__ __forceinline__ int lds_offset(int row, int chunk) {
 // stores (8 per lane instead of 64 two-byte ones) through a buffer resource
 // whose range ends at the workgroup's last valid output element.
 template <typename T, int BM, int BN, int WM, int WN, bool KFULL, bool VST>
-__global__ __launch_bounds__(256) void linear_mfma_kernel(
+__global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
     T* __restrict__ y, int M, int N, int K, int64_t x_rs, int64_t y_rs) {
   using MF = Mfma<T>;
-  static_assert(WM * WN == 4, "four waves per workgroup");
+  constexpr int NT = WM * WN * 64;  // threads per workgroup
   constexpr int TM = BM / WM;  // rows per wave
   constexpr int TN = BN / WN;  // cols per wave
   constexpr int FM = TM / 16;
   constexpr int FN = TN / 16;
   constexpr int XCH = BM * kChunks;  // 16-byte chunks per X tile
   constexpr int WCH = BN * kChunks;
-  constexpr int XPT = (XCH + 255) / 256;  // chunks per thread
-  constexpr int WPT = (WCH + 255) / 256;
+  constexpr int XPT = (XCH + NT - 1) / NT;  // chunks per thread
+  constexpr int WPT = (WCH + NT - 1) / NT;
   constexpr int XB = BM * kBK * 2;  // bytes per X tile
   constexpr int WB = BN * kBK * 2;
 
@@ -122,16 +122,16 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(
       make_rsrc(w + static_cast<int64_t>(n0) * K, w_rows > 0 ? w_rows * K * 2 : 0);
 
   uint4 xr[XPT], wr[WPT];
-  static_assert(!KFULL || (XCH % 256 == 0 && WCH % 256 == 0), "whole chunks per thread");
+  static_assert(!KFULL || (XCH % NT == 0 && WCH % NT == 0), "whole chunks per thread");
   int xoff[XPT], woff[WPT];
 #pragma unroll
   for (int i = 0; i < XPT; ++i) {
-    const int ch = tid + 256 * i;
+    const int ch = tid + NT * i;
     xoff[i] = static_cast<int>((ch / kChunks) * x_rs + (ch % kChunks) * 8) * 2;
   }
 #pragma unroll
   for (int i = 0; i < WPT; ++i) {
-    const int ch = tid + 256 * i;
+    const int ch = tid + NT * i;
     woff[i] = ((ch / kChunks) * K + (ch % kChunks) * 8) * 2;
   }
   auto fetch = [&](int k0) {
@@ -145,7 +145,7 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(
     }
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
-      const int ch = tid + 256 * i;
+      const int ch = tid + NT * i;
       const int row = ch / kChunks, col = (ch % kChunks) * 8;
       const bool ok = ch < XCH && row < x_rows && k0 + col < K;
       xr[i] = ok ? buffer_load16(rx, static_cast<int>(row * x_rs + k0 + col) * 2)
@@ -153,7 +153,7 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(
     }
 #pragma unroll
     for (int i = 0; i < WPT; ++i) {
-      const int ch = tid + 256 * i;
+      const int ch = tid + NT * i;
       const int row = ch / kChunks, col = (ch % kChunks) * 8;
       const bool ok = ch < WCH && row < w_rows && k0 + col < K;
       wr[i] = ok ? buffer_load16(rw, (row * K + k0 + col) * 2) : make_uint4(0, 0, 0, 0);
@@ -164,13 +164,13 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(
     unsigned char* ws = xs + XB;
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
-      const int ch = tid + 256 * i;
+      const int ch = tid + NT * i;
       if (ch < XCH)
         *reinterpret_cast<uint4*>(xs + lds_offset(ch / kChunks, ch % kChunks)) = xr[i];
     }
 #pragma unroll
     for (int i = 0; i < WPT; ++i) {
-      const int ch = tid + 256 * i;
+      const int ch = tid + NT * i;
       if (ch < WCH)
         *reinterpret_cast<uint4*>(ws + lds_offset(ch / kChunks, ch % kChunks)) = wr[i];
     }
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(
     // The loop ended on a barrier, so the LDS is free: wave-private staging
     // of its TM x TN tile as T, rows padded to keep 16-byte alignment.
     constexpr int kCPad = TN + 8;
-    static_assert(TM * kCPad * 2 * 4 <= 2 * (XB + WB), "staging fits the LDS");
+    static_assert(TM * kCPad * 2 * WM * WN <= 2 * (XB + WB), "staging fits the LDS");
     uint16_t* cs = reinterpret_cast<uint16_t*>(smem) + wave * TM * kCPad;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
@@ -407,20 +407,20 @@ int launch_mfma(const void* x, const void* w, const void* bias, void* y, int M,
   const bool vst = N % 8 == 0 && y_rs % 8 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0 &&
                    static_cast<int64_t>(BM) * y_rs * 2 < (int64_t{1} << 31);
   if (K % kBK == 0 && vst) {
-    hipLaunchKernelGGL((linear_mfma_kernel<T, BM, BN, WM, WN, true, true>), grid, dim3(256), 0,
+    hipLaunchKernelGGL((linear_mfma_kernel<T, BM, BN, WM, WN, true, true>), grid, dim3(WM * WN * 64), 0,
                        stream, static_cast<const T*>(x), static_cast<const T*>(w),
                        static_cast<const T*>(bias), static_cast<T*>(y), M, N, K,
                        x_rs, y_rs);
     return slc_host::check_launch("slc_hip_linear");
   }
   if (K % kBK == 0) {
-    hipLaunchKernelGGL((linear_mfma_kernel<T, BM, BN, WM, WN, true, false>), grid, dim3(256), 0,
+    hipLaunchKernelGGL((linear_mfma_kernel<T, BM, BN, WM, WN, true, false>), grid, dim3(WM * WN * 64), 0,
                        stream, static_cast<const T*>(x), static_cast<const T*>(w),
                        static_cast<const T*>(bias), static_cast<T*>(y), M, N, K,
                        x_rs, y_rs);
     return slc_host::check_launch("slc_hip_linear");
   }
-  hipLaunchKernelGGL((linear_mfma_kernel<T, BM, BN, WM, WN, false, false>), grid, dim3(256), 0,
+  hipLaunchKernelGGL((linear_mfma_kernel<T, BM, BN, WM, WN, false, false>), grid, dim3(WM * WN * 64), 0,
                      stream, static_cast<const T*>(x), static_cast<const T*>(w),
                      static_cast<const T*>(bias), static_cast<T*>(y), M, N, K,
                      x_rs, y_rs);
