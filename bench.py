@@ -288,6 +288,72 @@ def bench_kernels() -> dict:
         hbm(f"linear_m8_n{n}_k{kk}", us, (n * kk + 8 * kk + 8 * n) * 2, f"M8 N{n} K{kk}")
         del ws
 
+    # the fused decode-step kernels at batch 8 (Qwen2-0.5B layer shapes), each
+    # graph of 60 calls cycling over weight / KV copies past the Infinity Cache
+    from stateful_llm_compiler_hip.backends import (
+        hip_linear_residual, hip_norm_linear_group, hip_norm_linear_swiglu,
+        hip_rope_decode_attention,
+    )
+
+    def copies_for(nbytes):
+        return max(2, -(-(300 << 20) // nbytes))
+
+    hs = torch.randn(8, 1, 896, device=dev, generator=g, dtype=bf)
+    nw = torch.rand(896, device=dev, generator=g).to(bf) + 0.5
+    res = torch.randn(8, 1, 896, device=dev, generator=g, dtype=bf)
+    wsz = 2 * 896 * (896 + 128 + 128)
+    qkv = [[torch.randn(n, 896, device=dev, generator=g, dtype=bf) * 0.02 for n in (896, 128, 128)]
+           for _ in range(copies_for(wsz))]
+    qkv_b = [torch.randn(n, device=dev, generator=g, dtype=bf) * 0.02 for n in (896, 128, 128)]
+    turn = itertools.cycle(range(len(qkv)))
+    us = _time_graph(lambda: hip_norm_linear_group(hs, nw, qkv[next(turn)], qkv_b, epsilon=1e-6),
+                     reps=60, outer=3)
+    hbm("decode_norm_qkv", us, wsz + 2 * 8 * 896 * 2 + 2 * 8 * 1152, "M8 norm + Q/K/V 896->896+128+128")
+    del qkv
+    wsz = 2 * 2 * 4864 * 896
+    gu = [(torch.randn(4864, 896, device=dev, generator=g, dtype=bf) * 0.02,
+           torch.randn(4864, 896, device=dev, generator=g, dtype=bf) * 0.02)
+          for _ in range(copies_for(wsz))]
+    turn = itertools.cycle(range(len(gu)))
+    us = _time_graph(lambda: hip_norm_linear_swiglu(hs, nw, *gu[next(turn)], epsilon=1e-6),
+                     reps=60, outer=3)
+    hbm("decode_norm_swiglu", us, wsz + 2 * 8 * 896 + 2 * 8 * 4864, "M8 norm + gate/up 896->4864 + SwiGLU")
+    del gu
+    for name, n_in, n_out in (("decode_o_residual", 896, 896), ("decode_down_residual", 4864, 896)):
+        wsz = 2 * n_in * n_out
+        xs = torch.randn(8, 1, n_in, device=dev, generator=g, dtype=bf)
+        ws = [torch.randn(n_out, n_in, device=dev, generator=g, dtype=bf) * 0.02
+              for _ in range(copies_for(wsz))]
+        turn = itertools.cycle(range(len(ws)))
+        us = _time_graph(lambda: hip_linear_residual(xs, ws[next(turn)], None, res), reps=60, outer=3)
+        hbm(name, us, wsz + 2 * 8 * (n_in + 2 * n_out), f"M8 {n_in}->{n_out} + residual")
+        del ws
+    # RoPE + KV store + advance + attention at the decode step's shape: batch 8,
+    # 600 tokens of a 2048-long mask (lengths into a separate tensor, so every
+    # call sees the same 600)
+    cap, length = 2048, 600
+    kv_bytes = 2 * 8 * cap * KVH * D * 2
+    kvs = [(torch.randn(8, cap, KVH, D, device=dev, generator=g, dtype=bf),
+            torch.randn(8, cap, KVH, D, device=dev, generator=g, dtype=bf))
+           for _ in range(copies_for(kv_bytes))]
+    qd = torch.randn(8, 1, QH, D, device=dev, generator=g, dtype=bf).transpose(1, 2)
+    kd = torch.randn(8, 1, KVH, D, device=dev, generator=g, dtype=bf).transpose(1, 2)
+    cs = torch.randn(8, 1, D, device=dev, generator=g, dtype=bf)
+    lens = torch.full((8,), length, device=dev, dtype=torch.int64)
+    lens_out = torch.empty_like(lens)
+    dmask = torch.zeros(8, 1, 1, cap, device=dev, dtype=bf)
+    turn = itertools.cycle(range(len(kvs)))
+
+    def rope_attention():
+        kb, vb = kvs[next(turn)]
+        return hip_rope_decode_attention(qd, kd, kd, cs, cs, kb, vb, lens, lens_out, dmask,
+                                         scale=D**-0.5)
+
+    us = _time_graph(rope_attention, reps=60, outer=3)
+    hbm("decode_rope_attention", us, 8 * (length + 1) * KVH * D * 2 * 2 + 8 * cap * 2,
+        "B8 QH14 KVH2 D64, 600 of a 2048 mask: RoPE + KV store + advance + attention")
+    del kvs
+
     # rms_norm 32768 x 896
     x = torch.randn(32768, 896, device=dev, generator=g, dtype=bf)
     wn = torch.randn(896, device=dev, generator=g, dtype=bf)
