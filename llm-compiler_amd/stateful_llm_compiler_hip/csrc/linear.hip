@@ -110,8 +110,28 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
   const int g = lane >> 4;
   const int wm = wave / WN;
   const int wn = wave % WN;
-  const int n0 = blockIdx.x * BN;
-  const int m0 = blockIdx.y * BM;
+  // Tile order for the L2s: workgroup ids go round-robin to the 8 XCDs, each
+  // with its own L2, so consecutive ids are first gathered per XCD (id i of
+  // the first 8 * floor(tiles / 8) goes to slot (i % 8) * floor(tiles / 8) +
+  // i / 8, the rest keep theirs: a bijection), then slots run in groups of
+  // kGroupM M-tiles, N-tile-major inside a group, so the workgroups one XCD
+  // holds at a time share their X and W tiles in its L2.
+  int m_blk, n_blk;
+  {
+    constexpr int kXcds = 8, kGroupM = 8;
+    const int n_tiles = gridDim.x, m_tiles = gridDim.y;
+    const int total = n_tiles * m_tiles;
+    const int id = blockIdx.y * n_tiles + blockIdx.x;
+    const int per = total / kXcds;
+    const int t = id < per * kXcds ? (id % kXcds) * per + id / kXcds : id;
+    const int span = kGroupM * n_tiles;
+    const int first_m = (t / span) * kGroupM;
+    const int gm = m_tiles - first_m < kGroupM ? m_tiles - first_m : kGroupM;
+    m_blk = first_m + (t % span) % gm;
+    n_blk = (t % span) / gm;
+  }
+  const int n0 = n_blk * BN;
+  const int m0 = m_blk * BM;
 
   // Buffer resources over the workgroup's rows: rows past M / N read zero.
   const int64_t x_rows = M - m0 < BM ? M - m0 : BM;
