@@ -35,6 +35,14 @@ template <>
 struct VecOf<float, 4> {
   using type = uint4;
 };
+template <>
+struct VecOf<slc::bf16_t, 8> {
+  using type = uint4;
+};
+template <>
+struct VecOf<slc::f16_t, 8> {
+  using type = uint4;
+};
 
 template <typename T, int VEC>
 __device__ __forceinline__ void load_vec(const T* p, float (&out)[VEC]) {
@@ -110,12 +118,20 @@ __global__ __launch_bounds__(256) void rope_kernel(
 
 template <typename T>
 int launch(const void* q, const void* k, const void* c, const void* s,
-           void* qo, void* ko, int64_t batch, RopeArgs a, bool vec4,
+           void* qo, void* ko, int64_t batch, RopeArgs a, int vec,
            hipStream_t stream) {
-  const int vec = vec4 ? 4 : 1;
   const int64_t total = batch * (a.q_heads + a.kv_heads) * a.tokens * (a.half / vec);
   const dim3 grid(static_cast<unsigned>(slc_host::ceil_div(total, 256)));
-  if (vec4) {
+  if constexpr (sizeof(T) == 2) {
+    if (vec == 8) {
+      hipLaunchKernelGGL((rope_kernel<T, 8>), grid, dim3(256), 0, stream,
+                         static_cast<const T*>(q), static_cast<const T*>(k),
+                         static_cast<const T*>(c), static_cast<const T*>(s),
+                         static_cast<T*>(qo), static_cast<T*>(ko), a, total);
+      return slc_host::check_launch("slc_hip_rope");
+    }
+  }
+  if (vec == 4) {
     hipLaunchKernelGGL((rope_kernel<T, 4>), grid, dim3(256), 0, stream,
                        static_cast<const T*>(q), static_cast<const T*>(k),
                        static_cast<const T*>(c), static_cast<const T*>(s),
@@ -164,17 +180,19 @@ extern "C" int slc_hip_rope(const void* query, const void* key,
                              cos_sb, cos_st, sin_sb, sin_st, qo_sb, qo_sh,
                              qo_st,  ko_sb,  ko_sh, ko_st, head_dim / 2};
   for (int64_t st : strides) bits |= static_cast<uint64_t>(st * es);
-  const bool vec4 = (bits % vbytes) == 0;
+  // 16-byte vectors (8 dims of a 2-byte dtype) when every row start and
+  // half allows, else 4 dims, else single elements.
+  const int vec = es == 2 && bits % 16 == 0 ? 8 : ((bits % vbytes) == 0 ? 4 : 1);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case SLC_BF16:
       return launch<slc::bf16_t>(query, key, cosine, sine, query_out, key_out,
-                                 batch, a, vec4, s);
+                                 batch, a, vec, s);
     case SLC_F16:
       return launch<slc::f16_t>(query, key, cosine, sine, query_out, key_out,
-                                batch, a, vec4, s);
+                                batch, a, vec, s);
     default:
       return launch<float>(query, key, cosine, sine, query_out, key_out, batch,
-                           a, vec4, s);
+                           a, vec, s);
   }
 }
