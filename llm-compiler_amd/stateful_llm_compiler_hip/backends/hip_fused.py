@@ -27,6 +27,7 @@ from .hip_ops import hip_add, hip_swiglu
 from .hip_rmsnorm import hip_rms_norm
 
 MAX_FUSED_ROWS = 32
+_UNSUPPORTED = -2  # SLC_ERR_UNSUPPORTED
 _MATRICES = 3
 
 
@@ -70,6 +71,9 @@ def hip_norm_linear_group(
         raise ValueError("HIP norm_linear_group: 1 to 3 weights, one bias entry each")
     for weight in weights:
         _check_weight(weight, tensor, "norm_linear_group")
+    if (norm_weight is not None and not norm_weight.is_cuda) or any(
+            b is not None and not b.is_cuda for b in biases):
+        raise ValueError("HIP norm_linear_group: norm weight and biases must be on the GPU")
     norm = norm_weight is not None
     if not _fusable_rows(tensor, norm=norm):
         x = hip_rms_norm(tensor, norm_weight, epsilon=epsilon, round_before_weight=True) if norm else tensor
@@ -110,6 +114,8 @@ def hip_norm_linear_swiglu(
 
     _check_weight(gate_weight, tensor, "norm_linear_swiglu")
     _check_weight(up_weight, tensor, "norm_linear_swiglu")
+    if not norm_weight.is_cuda:
+        raise ValueError("HIP norm_linear_swiglu: norm weight must be on the GPU")
     if gate_weight.shape != up_weight.shape:
         raise ValueError("HIP norm_linear_swiglu: gate and up weights differ in shape")
     if not _fusable_rows(tensor, norm=True):
@@ -141,9 +147,17 @@ def hip_linear_residual(
     out_shape = (*tensor.shape[:-1], weight.shape[0])
     if tuple(residual.shape) != out_shape or residual.dtype != tensor.dtype:
         raise ValueError("HIP linear_residual: residual must match the linear output")
-    if not _fusable_rows(tensor, norm=False) or not residual.is_contiguous():
-        return hip_add(residual, hip_linear(tensor, weight, bias))
+    if not residual.is_cuda or (bias is not None and not bias.is_cuda):
+        raise ValueError("HIP linear_residual: residual and bias must be on the GPU")
     hidden = tensor.shape[-1]
+    rows = tensor.numel() // hidden if hidden else 0
+    # Decode-sized rows take the fused row kernel; prefill-sized rows the tile
+    # kernel with the residual in its store epilogue, when it takes the shape.
+    prefill = (rows > MAX_FUSED_ROWS and tensor.is_cuda and tensor.is_contiguous()
+               and residual.is_contiguous() and tensor.dtype in (torch.bfloat16, torch.float16)
+               and (bias is None or (bias.dtype == tensor.dtype and bias.is_contiguous())))
+    if not prefill and (not _fusable_rows(tensor, norm=False) or not residual.is_contiguous()):
+        return hip_add(residual, hip_linear(tensor, weight, bias))
     features = weight.shape[0]
     out = torch.empty(out_shape, device=tensor.device, dtype=tensor.dtype)
     status = _native.library().slc_hip_linear_residual(
@@ -152,6 +166,8 @@ def hip_linear_residual(
         features, out.data_ptr(), features, _native.dtype_tag(tensor.dtype),
         _native.current_stream(tensor.device),
     )
+    if status == _UNSUPPORTED:
+        return hip_add(residual, hip_linear(tensor, weight, bias))
     _native.check(status, "slc_hip_linear_residual")
     return out
 

@@ -168,6 +168,11 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Decode-sized linear shared by slc_hip_linear and the fused decode ops
 // (defined with those kernels).
+// Prefill-sized linear + residual add (linear.hip); SLC_ERR_UNSUPPORTED when
+// its kernel does not take the shape.
+int gemm_residual(const void* x, int64_t x_rs, int64_t rows, int64_t K, int64_t N,
+                  const void* w, const void* bias, const void* residual, int64_t r_rs, void* y,
+                  int64_t y_rs, int dtype, hipStream_t stream);
 bool rows_linear_eligible(const void* x, int64_t x_rs, int64_t rows, int64_t K, int64_t N,
                           int dtype);
 int rows_linear(const void* x, int64_t x_rs, int64_t rows, int64_t K, int64_t N,

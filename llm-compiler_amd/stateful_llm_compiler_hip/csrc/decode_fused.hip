@@ -675,6 +675,14 @@ extern "C" int slc_hip_linear_residual(const void* x, int64_t x_rs, int64_t rows
                                        const void* residual, int64_t residual_rs, void* y,
                                        int64_t y_rs, int dtype, void* stream) {
   const char* what = "slc_hip_linear_residual";
+  if (rows > kMaxRows) {
+    // Prefill-sized: the tile kernel with the residual in its store epilogue.
+    SLC_REQUIRE(x && weight && residual && y && in_features >= 1 && out_features >= 1,
+                "%s: bad operands", what);
+    return slc_host::gemm_residual(x, x_rs, rows, in_features, out_features, weight, bias,
+                                   residual, residual_rs, y, y_rs, dtype,
+                                   static_cast<hipStream_t>(stream));
+  }
   if (int rc = check_rows(what, x, x_rs, rows, in_features, dtype, false)) return rc;
   SLC_REQUIRE(weight && residual && y && out_features >= 1 && out_features <= (1 << 24) &&
                   y_rs >= out_features && residual_rs >= out_features,

@@ -87,7 +87,8 @@ __device__ __forceinline__ int lds_offset(int row, int chunk) {
 template <typename T, int BM, int BN, int WM, int WN, bool KFULL, bool VST>
 __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
-    T* __restrict__ y, int M, int N, int K, int64_t x_rs, int64_t y_rs) {
+    T* __restrict__ y, int M, int N, int K, int64_t x_rs, int64_t y_rs,
+    const T* __restrict__ residual, int64_t r_rs) {
   using MF = Mfma<T>;
   constexpr int NT = WM * WN * 64;  // threads per workgroup
   constexpr int TM = BM / WM;  // rows per wave
@@ -253,6 +254,11 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
     const int rows = M - m0 < BM ? M - m0 : BM;
     const __amdgpu_buffer_rsrc_t ry =
         make_rsrc(y + m0 * y_rs, (static_cast<int64_t>(rows) - 1) * y_rs * 2 + N * 2);
+    // With a residual (VST only): y = residual + round(x.w^T + bias), rounded
+    // again, as the separate add does.
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(
+        residual != nullptr ? residual + m0 * r_rs : y,
+        residual != nullptr ? (static_cast<int64_t>(rows) - 1) * r_rs * 2 + N * 2 : 0);
     constexpr int kPerRow = TN / 8;  // 16-byte chunks per staged row
 #pragma unroll
     for (int q = 0; q < TM * kPerRow / 64; ++q) {
@@ -260,7 +266,22 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
       const int row = id / kPerRow, chunk = id % kPerRow;
       const int m_local = wm * TM + row;
       const int n = n0 + wn * TN + chunk * 8;
-      const uint4 v = *reinterpret_cast<const uint4*>(cs + row * kCPad + chunk * 8);
+      uint4 v = *reinterpret_cast<const uint4*>(cs + row * kCPad + chunk * 8);
+      if (residual != nullptr) {
+        const uint4 rv = buffer_load16(rr, static_cast<int>(m_local * r_rs + n) * 2);
+        const uint16_t* lin = reinterpret_cast<const uint16_t*>(&v);
+        const uint16_t* res = reinterpret_cast<const uint16_t*>(&rv);
+        uint4 o;
+        uint16_t* out = reinterpret_cast<uint16_t*>(&o);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          T a, r;
+          a.bits = lin[e];
+          r.bits = res[e];
+          out[e] = slc::from_f32<T>(slc::to_f32(r) + slc::to_f32(a)).bits;
+        }
+        v = o;
+      }
       if (m_local < rows && n < N)
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v), ry,
                                                static_cast<int>(m_local * y_rs + n) * 2, 0, 0);
@@ -420,9 +441,12 @@ __global__ __launch_bounds__(256) void linear_generic_kernel(
   }
 }
 
+constexpr int kNoResidualPath = -2;  // the residual epilogue needs the 16-byte store path
+
 template <typename T, int BM, int BN, int WM, int WN>
 int launch_mfma(const void* x, const void* w, const void* bias, void* y, int M,
-                int N, int K, int64_t x_rs, int64_t y_rs, hipStream_t stream) {
+                int N, int K, int64_t x_rs, int64_t y_rs, hipStream_t stream,
+                const void* residual = nullptr, int64_t r_rs = 0) {
   const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
   const bool vst = N % 8 == 0 && y_rs % 8 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0 &&
                    static_cast<int64_t>(BM) * y_rs * 2 < (int64_t{1} << 31);
@@ -430,20 +454,21 @@ int launch_mfma(const void* x, const void* w, const void* bias, void* y, int M,
     hipLaunchKernelGGL((linear_mfma_kernel<T, BM, BN, WM, WN, true, true>), grid, dim3(WM * WN * 64), 0,
                        stream, static_cast<const T*>(x), static_cast<const T*>(w),
                        static_cast<const T*>(bias), static_cast<T*>(y), M, N, K,
-                       x_rs, y_rs);
+                       x_rs, y_rs, static_cast<const T*>(residual), r_rs);
     return slc_host::check_launch("slc_hip_linear");
   }
+  if (residual != nullptr) return kNoResidualPath;
   if (K % kBK == 0) {
     hipLaunchKernelGGL((linear_mfma_kernel<T, BM, BN, WM, WN, true, false>), grid, dim3(WM * WN * 64), 0,
                        stream, static_cast<const T*>(x), static_cast<const T*>(w),
                        static_cast<const T*>(bias), static_cast<T*>(y), M, N, K,
-                       x_rs, y_rs);
+                       x_rs, y_rs, static_cast<const T*>(nullptr), int64_t{0});
     return slc_host::check_launch("slc_hip_linear");
   }
   hipLaunchKernelGGL((linear_mfma_kernel<T, BM, BN, WM, WN, false, false>), grid, dim3(WM * WN * 64), 0,
                      stream, static_cast<const T*>(x), static_cast<const T*>(w),
                      static_cast<const T*>(bias), static_cast<T*>(y), M, N, K,
-                     x_rs, y_rs);
+                     x_rs, y_rs, static_cast<const T*>(nullptr), int64_t{0});
   return slc_host::check_launch("slc_hip_linear");
 }
 
@@ -472,6 +497,34 @@ int launch_generic(const void* x, const void* w, const void* bias, void* y, int 
 }
 
 }  // namespace
+
+namespace slc_host {
+
+// Prefill-sized linear + residual add in one kernel (the tile kernel's
+// 16-byte store epilogue adds the residual): y = residual + round(x.w^T +
+// bias), rounded again, bit for bit the linear then the add.  Returns
+// SLC_ERR_UNSUPPORTED (nothing launched) for shapes that epilogue cannot take.
+int gemm_residual(const void* x, int64_t x_rs, int64_t rows, int64_t K, int64_t N,
+                  const void* w, const void* bias, const void* residual, int64_t r_rs, void* y,
+                  int64_t y_rs, int dtype, hipStream_t stream) {
+  const uint64_t bits = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                        reinterpret_cast<uintptr_t>(residual) | reinterpret_cast<uintptr_t>(y);
+  const bool ok = (dtype == SLC_BF16 || dtype == SLC_F16) && rows > 64 && (bits & 15) == 0 &&
+                  K % kBK == 0 && N % 8 == 0 && x_rs % 8 == 0 && y_rs % 8 == 0 &&
+                  r_rs % 8 == 0 && N * K * 2 < (int64_t{1} << 31) &&
+                  128 * x_rs * 2 < (int64_t{1} << 31) && 128 * y_rs * 2 < (int64_t{1} << 31) &&
+                  128 * r_rs * 2 < (int64_t{1} << 31) && rows < (int64_t{1} << 31);
+  if (!ok) return SLC_ERR_UNSUPPORTED;
+  const int M = static_cast<int>(rows), n = static_cast<int>(N), k = static_cast<int>(K);
+  const int rc = dtype == SLC_BF16
+                     ? launch_mfma<slc::bf16_t, 128, 128, 2, 2>(x, w, bias, y, M, n, k, x_rs, y_rs,
+                                                                stream, residual, r_rs)
+                     : launch_mfma<slc::f16_t, 128, 128, 2, 2>(x, w, bias, y, M, n, k, x_rs, y_rs,
+                                                               stream, residual, r_rs);
+  return rc == kNoResidualPath ? SLC_ERR_UNSUPPORTED : rc;
+}
+
+}  // namespace slc_host
 
 extern "C" int slc_hip_linear(const void* input, const void* weight,
                               const void* bias, void* output, int dtype,

@@ -263,3 +263,32 @@ def test_rope_decode_attention_declines_unsupported(gpu):
     torch.cuda.synchronize()
     assert pos.tolist() == [1, 2]
     assert_bitwise_equal(kb, before)
+
+
+@pytest.mark.parametrize("rows,n,k,bias", [(300, 896, 896, False), (4096, 896, 4864, False),
+                                           (129, 136, 64, True), (300, 100, 64, False)])
+def test_linear_residual_prefill_rows(gpu, rows, n, k, bias):
+    # Prefill-sized rows: the tile kernel adds the residual in its store
+    # epilogue (N = 100 is not a multiple of 8: the two-op path), bit for bit
+    # the linear then the add.
+    announce(f"linear_residual prefill rows={rows} n={n} k={k} bias={bias}")
+    g = generator(rows + n + k)
+    x = _t(g, rows, k, device=gpu)
+    w = _t(g, n, k, scale=0.02, device=gpu)
+    r = _t(g, rows, n, device=gpu)
+    b = _t(g, n, scale=0.1, device=gpu) if bias else None
+    got = hip_linear_residual(x, w, b, r)
+    want = hip_add(r, hip_linear(x, w, b))
+    torch.cuda.synchronize()
+    assert_bitwise_equal(got, want)
+
+
+def test_fused_ops_reject_host_operands(gpu):
+    announce("fused ops reject host operands")
+    g = generator(3)
+    x = _t(g, 4, 896, device=gpu)
+    w = _t(g, 896, 896, scale=0.02, device=gpu)
+    with pytest.raises(ValueError):
+        hip_linear_residual(x, w, None, torch.zeros(4, 896, dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        hip_norm_linear_group(x, torch.ones(896, dtype=torch.bfloat16), [w], [None], epsilon=1e-6)
