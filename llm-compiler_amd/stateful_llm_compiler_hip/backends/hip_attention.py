@@ -12,6 +12,7 @@ from __future__ import annotations
 import torch
 
 from .. import _native
+from .hip_ops import check_flag
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
@@ -176,6 +177,7 @@ def hip_rope_decode_attention(
     tensors = [query, key, value, cosine, sine, key_buffer, value_buffer, lengths, lengths_out]
     if attention_mask is not None:
         tensors.append(attention_mask)
+    check_flag(overflow, "HIP rope decode attention")
     if not all(tensor.is_cuda for tensor in tensors):
         return None
     if (

@@ -23,7 +23,7 @@ import torch
 
 from .. import _native
 from .hip_linear import hip_linear
-from .hip_ops import hip_add, hip_swiglu
+from .hip_ops import check_flag, hip_add, hip_swiglu
 from .hip_rmsnorm import hip_rms_norm
 
 MAX_FUSED_ROWS = 32
@@ -195,6 +195,7 @@ def hip_rope_kv_store(
     tensors = (query, key, value, cosine, sine, key_buffer, value_buffer, positions)
     if not all(t.is_cuda for t in tensors):
         raise ValueError("HIP rope_kv_store: all tensors must be on the GPU")
+    check_flag(overflow, "HIP rope_kv_store")
     if query.ndim != 4 or key.ndim != 4 or value.shape != key.shape:
         raise ValueError("HIP rope_kv_store: q/k/v must be [B, H, T, D] with matching k/v")
     if any(t.stride(-1) != 1 for t in (query, key, value, cosine, sine)):

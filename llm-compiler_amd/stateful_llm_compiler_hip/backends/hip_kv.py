@@ -10,6 +10,7 @@ from __future__ import annotations
 import torch
 
 from .. import _native
+from .hip_ops import check_flag
 
 
 def hip_kv_store(
@@ -33,6 +34,7 @@ def hip_kv_store(
         for tensor in (key_buffer, value_buffer, key, value, positions)
     ):
         raise ValueError("HIP KV store: all tensors must be on the GPU")
+    check_flag(overflow, "HIP KV store")
     if (
         key_buffer.shape != value_buffer.shape
         or key.shape != value.shape

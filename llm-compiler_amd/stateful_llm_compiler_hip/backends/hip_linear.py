@@ -20,7 +20,7 @@ def hip_linear(
 ) -> torch.Tensor:
     """2-D or 3-D ``tensor`` [..., K] times ``weight`` [N, K]^T (+ ``bias`` [N])."""
 
-    if not tensor.is_cuda or not weight.is_cuda:
+    if not tensor.is_cuda or not weight.is_cuda or (bias is not None and not bias.is_cuda):
         raise ValueError("HIP linear: tensors must be on the GPU")
     if tensor.ndim not in {2, 3} or weight.ndim != 2:
         raise ValueError("HIP linear: input must be 2-D or 3-D and weight 2-D")

@@ -14,6 +14,13 @@ from .. import _native
 _FLOATS = (torch.float16, torch.bfloat16, torch.float32)
 
 
+def check_flag(flag: torch.Tensor | None, what: str) -> None:
+    """An optional device flag: an int32 GPU tensor of at least one element."""
+
+    if flag is not None and (not flag.is_cuda or flag.dtype != torch.int32 or flag.numel() < 1):
+        raise ValueError(f"{what}: the overflow flag must be an int32 GPU tensor")
+
+
 def _require_gpu(*tensors: torch.Tensor, what: str) -> None:
     if not all(t.is_cuda for t in tensors):
         raise ValueError(f"{what}: all tensors must be on the GPU")
@@ -109,6 +116,10 @@ def hip_kv_advance(
     _require_gpu(lengths, what="HIP kv advance")
     if lengths.dtype != torch.int64 or lengths.ndim != 1 or not lengths.is_contiguous():
         raise ValueError("HIP kv advance: lengths must be a contiguous 1-D int64 tensor")
+    if out is not None and (not out.is_cuda or out.dtype != torch.int64
+                            or out.shape != lengths.shape or not out.is_contiguous()):
+        raise ValueError("HIP kv advance: out must be a contiguous int64 GPU tensor like lengths")
+    check_flag(overflow, "HIP kv advance")
     result = torch.empty_like(lengths) if out is None else out
     status = _native.library().slc_hip_kv_advance(
         lengths.data_ptr(), result.data_ptr(), lengths.shape[0], int(delta), int(capacity),
@@ -132,7 +143,8 @@ def hip_argmax(logits: torch.Tensor, *, out: torch.Tensor | None = None) -> torc
     flat = logits.reshape(-1, cols)
     if out is None:
         out = torch.empty(flat.shape[0], device=logits.device, dtype=torch.int64)
-    elif out.dtype != torch.int64 or not out.is_contiguous() or out.numel() != flat.shape[0]:
+    elif (not out.is_cuda or out.dtype != torch.int64 or not out.is_contiguous()
+          or out.numel() != flat.shape[0]):
         raise ValueError("HIP argmax: out must be a contiguous int64 tensor with one entry per row")
     status = _native.library().slc_hip_argmax(
         flat.data_ptr(), out.data_ptr(), _native.dtype_tag(logits.dtype), flat.shape[0], cols,
