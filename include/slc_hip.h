@@ -289,6 +289,22 @@ SLC_API int slc_hip_rope_kv_store(
     int64_t sin_sb, int64_t sin_st, int64_t qo_sb, int64_t qo_sh, int64_t qo_st, void* stream);
 
 /*
+ * linear_swiglu: y = swiglu(round(x . w_gate^T), round(x . w_up^T)) for
+ * prefill-sized rows (> 64), in one kernel: the Qwen2 MLP front after its
+ * norm (qwen2.py:253-256), replacing two kernel.triton.linear calls and the
+ * elementwise SwiGLU (triton_linear.py:87-148) with bit-identical results.
+ * x [rows, in_features] (row stride in_stride_row), w_gate/w_up [features,
+ * in_features] contiguous, y [rows, features] (row stride out_stride_row);
+ * bf16 or fp16.  Returns SLC_ERR_UNSUPPORTED (nothing launched) for rows <= 64,
+ * in_features not a multiple of 64, features or strides not multiples of 8,
+ * or rows not 16-byte aligned.
+ */
+SLC_API int slc_hip_linear_swiglu(const void* input, int64_t in_stride_row, int64_t rows,
+                                  int64_t in_features, int64_t features, const void* w_gate,
+                                  const void* w_up, void* output, int64_t out_stride_row,
+                                  int dtype, void* stream);
+
+/*
  * rope_decode_attention: one decode token's RoPE, KV store, length advance and
  * GQA attention in one kernel.  Replaces rope_kv_store (with advance = 1)
  * followed by slc_hip_decode_attention of the rotated query over the advanced

@@ -120,6 +120,9 @@ def hip_norm_linear_swiglu(
         raise ValueError("HIP norm_linear_swiglu: gate and up weights differ in shape")
     if not _fusable_rows(tensor, norm=True):
         x = hip_rms_norm(tensor, norm_weight, epsilon=epsilon, round_before_weight=True)
+        fused = _linear_swiglu(x, gate_weight, up_weight)
+        if fused is not None:
+            return fused
         return hip_swiglu(hip_linear(x, gate_weight), hip_linear(x, up_weight))
     hidden = tensor.shape[-1]
     features = gate_weight.shape[0]
@@ -131,6 +134,29 @@ def hip_norm_linear_swiglu(
         _native.current_stream(tensor.device),
     )
     _native.check(status, "slc_hip_norm_linear_swiglu")
+    return out
+
+
+def _linear_swiglu(x: torch.Tensor, gate_weight: torch.Tensor,
+                   up_weight: torch.Tensor) -> torch.Tensor | None:
+    """Prefill-sized ``swiglu(linear(x, gate), linear(x, up))`` in one kernel,
+    or None (nothing launched) when that kernel does not take the shape."""
+
+    hidden = x.shape[-1]
+    rows = x.numel() // hidden if hidden else 0
+    if (not x.is_cuda or not x.is_contiguous() or rows <= 64
+            or x.dtype not in (torch.bfloat16, torch.float16)):
+        return None
+    features = gate_weight.shape[0]
+    out = torch.empty((*x.shape[:-1], features), device=x.device, dtype=x.dtype)
+    status = _native.library().slc_hip_linear_swiglu(
+        x.data_ptr(), hidden, rows, hidden, features, gate_weight.data_ptr(),
+        up_weight.data_ptr(), out.data_ptr(), features, _native.dtype_tag(x.dtype),
+        _native.current_stream(x.device),
+    )
+    if status == _UNSUPPORTED:
+        return None
+    _native.check(status, "slc_hip_linear_swiglu")
     return out
 
 

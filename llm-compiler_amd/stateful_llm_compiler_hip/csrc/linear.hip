@@ -22,6 +22,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "op_math.hpp"
 
 namespace {
 
@@ -84,11 +85,16 @@ __device__ __forceinline__ int lds_offset(int row, int chunk) {
 // each wave stages its output tile through LDS and writes it with 16-byte
 // stores (8 per lane instead of 64 two-byte ones) through a buffer resource
 // whose range ends at the workgroup's last valid output element.
-template <typename T, int BM, int BN, int WM, int WN, bool KFULL, bool VST>
+// DUAL (with KFULL and VST): the gate/up projections and SwiGLU in one pass.
+// A workgroup's BN columns are BN / 2 features of w (gate) followed by the
+// same features of w2 (up); its epilogue stages the rounded tile in LDS and
+// writes y = swiglu(gate, up) for those BN / 2 features (no bias).
+template <typename T, int BM, int BN, int WM, int WN, bool KFULL, bool VST, bool DUAL = false>
 __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
     T* __restrict__ y, int M, int N, int K, int64_t x_rs, int64_t y_rs,
-    const T* __restrict__ residual, int64_t r_rs) {
+    const T* __restrict__ residual, int64_t r_rs, const T* __restrict__ w2 = nullptr) {
+  static_assert(!DUAL || (KFULL && VST), "the fused SwiGLU uses the K-multiple store path");
   using MF = Mfma<T>;
   constexpr int NT = WM * WN * 64;  // threads per workgroup
   constexpr int TM = BM / WM;  // rows per wave
@@ -131,16 +137,20 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
     m_blk = first_m + (t % span) % gm;
     n_blk = (t % span) / gm;
   }
-  const int n0 = n_blk * BN;
+  // DUAL: n0 is the first feature, BN / 2 of them per workgroup.
+  const int n0 = n_blk * (DUAL ? BN / 2 : BN);
   const int m0 = m_blk * BM;
 
   // Buffer resources over the workgroup's rows: rows past M / N read zero.
   const int64_t x_rows = M - m0 < BM ? M - m0 : BM;
-  const int64_t w_rows = N - n0 < BN ? N - n0 : BN;
+  const int64_t w_rows = DUAL ? (N - n0 < BN / 2 ? N - n0 : BN / 2) : (N - n0 < BN ? N - n0 : BN);
   const __amdgpu_buffer_rsrc_t rx =
       make_rsrc(x + m0 * x_rs, x_rows > 0 ? (x_rows - 1) * x_rs * 2 + K * 2 : 0);
   const __amdgpu_buffer_rsrc_t rw =
       make_rsrc(w + static_cast<int64_t>(n0) * K, w_rows > 0 ? w_rows * K * 2 : 0);
+  // The up rows (DUAL): W-tile rows BN / 2 .. BN - 1.
+  const __amdgpu_buffer_rsrc_t rw2 =
+      make_rsrc(DUAL ? w2 + static_cast<int64_t>(n0) * K : w, DUAL && w_rows > 0 ? w_rows * K * 2 : 0);
 
   uint4 xr[XPT], wr[WPT];
   static_assert(!KFULL || (XCH % NT == 0 && WCH % NT == 0), "whole chunks per thread");
@@ -153,15 +163,21 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
 #pragma unroll
   for (int i = 0; i < WPT; ++i) {
     const int ch = tid + NT * i;
-    woff[i] = ((ch / kChunks) * K + (ch % kChunks) * 8) * 2;
+    const int row = DUAL ? (ch / kChunks) % (BN / 2) : ch / kChunks;
+    woff[i] = (row * K + (ch % kChunks) * 8) * 2;
   }
+  // DUAL: chunk set i covers W-tile rows NT * i / kChunks ..; the first half
+  // of the sets are gate rows, the rest up rows (a compile-time split).
+  static_assert(!DUAL || (WPT % 2 == 0 && (WPT / 2) * NT == (BN / 2) * kChunks),
+                "gate and up rows split evenly over the chunk sets");
   auto fetch = [&](int k0) {
     if constexpr (KFULL) {
       const int kb = __builtin_amdgcn_readfirstlane(k0 * 2);
 #pragma unroll
       for (int i = 0; i < XPT; ++i) xr[i] = buffer_load16(rx, xoff[i], kb);
 #pragma unroll
-      for (int i = 0; i < WPT; ++i) wr[i] = buffer_load16(rw, woff[i], kb);
+      for (int i = 0; i < WPT; ++i)
+        wr[i] = buffer_load16(DUAL && i >= WPT / 2 ? rw2 : rw, woff[i], kb);
       return;
     }
 #pragma unroll
@@ -234,6 +250,50 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
     __syncthreads();
   }
 
+  if constexpr (DUAL) {
+    // The whole BM x BN tile, rounded to T, in LDS (the loop ended on a
+    // barrier), then SwiGLU of each feature's gate (column j) and up (column
+    // BN / 2 + j) values, 8 features per 16-byte store.
+    constexpr int kRow = BN + 8;
+    static_assert(BM * kRow * 2 <= 2 * (XB + WB), "staging fits the LDS");
+    uint16_t* cs = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          cs[(wm * TM + i * 16 + 4 * g + r) * kRow + wn * TN + j * 16 + c] =
+              slc::from_f32<T>(acc[i][j][r]).bits;
+    __syncthreads();
+    const int rows = M - m0 < BM ? M - m0 : BM;
+    const __amdgpu_buffer_rsrc_t ry =
+        make_rsrc(y + m0 * y_rs, (static_cast<int64_t>(rows) - 1) * y_rs * 2 + N * 2);
+    constexpr int kPerRow = BN / 2 / 8;
+#pragma unroll
+    for (int q = 0; q < BM * kPerRow / NT; ++q) {
+      const int id = q * NT + tid;
+      const int row = id / kPerRow, chunk = id % kPerRow;
+      const uint4 gv = *reinterpret_cast<const uint4*>(cs + row * kRow + chunk * 8);
+      const uint4 uv = *reinterpret_cast<const uint4*>(cs + row * kRow + BN / 2 + chunk * 8);
+      const uint16_t* gb = reinterpret_cast<const uint16_t*>(&gv);
+      const uint16_t* ub = reinterpret_cast<const uint16_t*>(&uv);
+      uint4 o;
+      uint16_t* ob = reinterpret_cast<uint16_t*>(&o);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        T ge, ue;
+        ge.bits = gb[e];
+        ue.bits = ub[e];
+        ob[e] = slc::from_f32<T>(slc::swiglu_value<T>(slc::to_f32(ge), slc::to_f32(ue))).bits;
+      }
+      const int n = n0 + chunk * 8;
+      if (row < rows && n < N)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, o), ry,
+                                               static_cast<int>(row * y_rs + n) * 2, 0, 0);
+    }
+    return;
+  }
   if constexpr (VST) {
     // The loop ended on a barrier, so the LDS is free: wave-private staging
     // of its TM x TN tile as T, rows padded to keep 16-byte alignment.
@@ -524,7 +584,50 @@ int gemm_residual(const void* x, int64_t x_rs, int64_t rows, int64_t K, int64_t 
   return rc == kNoResidualPath ? SLC_ERR_UNSUPPORTED : rc;
 }
 
+// Prefill-sized gate/up projections with SwiGLU in one kernel: y =
+// swiglu(round(x.w_gate^T), round(x.w_up^T)), bit for bit the two linears
+// then the elementwise op.  SLC_ERR_UNSUPPORTED (nothing launched) for shapes
+// its epilogue cannot take.
+int gemm_swiglu(const void* x, int64_t x_rs, int64_t rows, int64_t K, int64_t N,
+                const void* w_gate, const void* w_up, void* y, int64_t y_rs, int dtype,
+                hipStream_t stream) {
+  const uint64_t bits = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_gate) |
+                        reinterpret_cast<uintptr_t>(w_up) | reinterpret_cast<uintptr_t>(y);
+  const bool ok = (dtype == SLC_BF16 || dtype == SLC_F16) && rows > 64 && (bits & 15) == 0 &&
+                  K % kBK == 0 && N % 8 == 0 && x_rs % 8 == 0 && y_rs % 8 == 0 &&
+                  N * K * 2 < (int64_t{1} << 31) && 128 * x_rs * 2 < (int64_t{1} << 31) &&
+                  128 * y_rs * 2 < (int64_t{1} << 31) && rows < (int64_t{1} << 31);
+  if (!ok) return SLC_ERR_UNSUPPORTED;
+  const int M = static_cast<int>(rows), n = static_cast<int>(N), k = static_cast<int>(K);
+  const dim3 grid((n + 63) / 64, (M + 127) / 128);
+#define SLC_DUAL(TT)                                                                         \
+  hipLaunchKernelGGL((linear_mfma_kernel<TT, 128, 128, 2, 2, true, true, true>), grid,       \
+                     dim3(256), 0, stream, static_cast<const TT*>(x),                         \
+                     static_cast<const TT*>(w_gate), static_cast<const TT*>(nullptr),         \
+                     static_cast<TT*>(y), M, n, k, x_rs, y_rs, static_cast<const TT*>(nullptr), \
+                     int64_t{0}, static_cast<const TT*>(w_up))
+  if (dtype == SLC_BF16) {
+    SLC_DUAL(slc::bf16_t);
+  } else {
+    SLC_DUAL(slc::f16_t);
+  }
+#undef SLC_DUAL
+  return check_launch("slc_hip_linear_swiglu");
+}
+
 }  // namespace slc_host
+
+extern "C" int slc_hip_linear_swiglu(const void* input, int64_t in_stride_row, int64_t rows,
+                                     int64_t in_features, int64_t features, const void* w_gate,
+                                     const void* w_up, void* output, int64_t out_stride_row,
+                                     int dtype, void* stream) {
+  SLC_REQUIRE(rows >= 0 && in_features > 0 && features > 0,
+              "slc_hip_linear_swiglu: bad sizes");
+  if (rows == 0) return SLC_OK;
+  SLC_REQUIRE(input && w_gate && w_up && output, "slc_hip_linear_swiglu: null pointer");
+  return slc_host::gemm_swiglu(input, in_stride_row, rows, in_features, features, w_gate, w_up,
+                               output, out_stride_row, dtype, static_cast<hipStream_t>(stream));
+}
 
 extern "C" int slc_hip_linear(const void* input, const void* weight,
                               const void* bias, void* output, int dtype,
