@@ -289,6 +289,21 @@ SLC_API int slc_hip_rope_kv_store(
     int64_t sin_sb, int64_t sin_st, int64_t qo_sb, int64_t qo_sh, int64_t qo_st, void* stream);
 
 /*
+ * linear_group: y_j = linear(x, w_j, b_j) for count = 1..3 matrices [n_j,
+ * in_features] (the Q/K/V projections of one input) at prefill-sized rows
+ * (> 64), in one launch; each output bit for bit that of slc_hip_linear
+ * (kernel.triton.linear, triton_linear.py:87-148).  bf16 or fp16.  Returns
+ * SLC_ERR_UNSUPPORTED (nothing launched) for rows <= 64, in_features not a
+ * multiple of 64, n_j or strides not multiples of 8, or unaligned rows.
+ */
+SLC_API int slc_hip_linear_group(const void* input, int64_t in_stride_row, int64_t rows,
+                                 int64_t in_features, int count, const void* w0,
+                                 const void* b0, void* y0, int64_t n0, int64_t y0_rs,
+                                 const void* w1, const void* b1, void* y1, int64_t n1,
+                                 int64_t y1_rs, const void* w2, const void* b2, void* y2,
+                                 int64_t n2, int64_t y2_rs, int dtype, void* stream);
+
+/*
  * linear_swiglu: y = swiglu(round(x . w_gate^T), round(x . w_up^T)) for
  * prefill-sized rows (> 64), in one kernel: the Qwen2 MLP front after its
  * norm (qwen2.py:253-256), replacing two kernel.triton.linear calls and the

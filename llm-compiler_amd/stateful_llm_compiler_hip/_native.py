@@ -64,6 +64,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "slc_hip_norm_linear_swiglu": (_I, [_P, _L, _P, _F, _L, _L, _L, _P, _P, _P, _L, _I, _P]),
     "slc_hip_linear_residual": (_I, [_P, _L, _L, _L, _L, _P, _P, _P, _L, _P, _L, _I, _P]),
     "slc_hip_rope_kv_store": (_I, [_P] * 11 + [_L, _I] + [_L] * 6 + [_L] * 16 + [_P]),
+    "slc_hip_linear_group": (
+        _I, [_P, _L, _L, _L, _I] + [_P, _P, _P, _L, _L] * 3 + [_I, _P]),
     "slc_hip_linear_swiglu": (_I, [_P, _L, _L, _L, _L, _P, _P, _P, _L, _I, _P]),
     "slc_hip_rope_decode_attention": (
         _I, [_P] * 11 + [_I, _P, _P, _L, _I] + [_L] * 6 + [_L] * 15 + [_F, _P]),

@@ -77,6 +77,9 @@ def hip_norm_linear_group(
     norm = norm_weight is not None
     if not _fusable_rows(tensor, norm=norm):
         x = hip_rms_norm(tensor, norm_weight, epsilon=epsilon, round_before_weight=True) if norm else tensor
+        grouped = _linear_group(x, weights, biases)
+        if grouped is not None:
+            return grouped
         return [hip_linear(x, w, b) for w, b in zip(weights, biases)]
     hidden = tensor.shape[-1]
     rows = tensor.numel() // hidden
@@ -135,6 +138,37 @@ def hip_norm_linear_swiglu(
     )
     _native.check(status, "slc_hip_norm_linear_swiglu")
     return out
+
+
+def _linear_group(x: torch.Tensor, weights: Sequence[torch.Tensor],
+                  biases: Sequence[torch.Tensor | None]) -> list[torch.Tensor] | None:
+    """Prefill-sized ``[linear(x, w, b) ...]`` in one launch, or None (nothing
+    launched) when that kernel does not take the shapes."""
+
+    hidden = x.shape[-1]
+    rows = x.numel() // hidden if hidden else 0
+    if (not x.is_cuda or not x.is_contiguous() or rows <= 64
+            or x.dtype not in (torch.bfloat16, torch.float16)
+            or any(b is not None and (b.dtype != x.dtype or not b.is_contiguous()) for b in biases)):
+        return None
+    outputs = [torch.empty((*x.shape[:-1], w.shape[0]), device=x.device, dtype=x.dtype)
+               for w in weights]
+    per_matrix: list[object] = []
+    for i in range(_MATRICES):
+        if i < len(weights):
+            b = biases[i]
+            per_matrix += [weights[i].data_ptr(), None if b is None else b.data_ptr(),
+                           outputs[i].data_ptr(), weights[i].shape[0], weights[i].shape[0]]
+        else:
+            per_matrix += [None, None, None, 0, 0]
+    status = _native.library().slc_hip_linear_group(
+        x.data_ptr(), hidden, rows, hidden, len(weights), *per_matrix,
+        _native.dtype_tag(x.dtype), _native.current_stream(x.device),
+    )
+    if status == _UNSUPPORTED:
+        return None
+    _native.check(status, "slc_hip_linear_group")
+    return outputs
 
 
 def _linear_swiglu(x: torch.Tensor, gate_weight: torch.Tensor,

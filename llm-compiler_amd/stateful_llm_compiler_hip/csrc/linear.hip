@@ -85,16 +85,30 @@ __device__ __forceinline__ int lds_offset(int row, int chunk) {
 // each wave stages its output tile through LDS and writes it with 16-byte
 // stores (8 per lane instead of 64 two-byte ones) through a buffer resource
 // whose range ends at the workgroup's last valid output element.
+// Up to three projections of one input in one launch (GROUP): N-tiles
+// [tile_end[j-1], tile_end[j]) belong to matrix j.
+struct LinearGroup {
+  const void* w[3];
+  const void* bias[3];
+  void* y[3];
+  int n[3];
+  int64_t y_rs[3];
+  int tile_end[3];
+};
+
 // DUAL (with KFULL and VST): the gate/up projections and SwiGLU in one pass.
 // A workgroup's BN columns are BN / 2 features of w (gate) followed by the
 // same features of w2 (up); its epilogue stages the rounded tile in LDS and
 // writes y = swiglu(gate, up) for those BN / 2 features (no bias).
-template <typename T, int BM, int BN, int WM, int WN, bool KFULL, bool VST, bool DUAL = false>
+template <typename T, int BM, int BN, int WM, int WN, bool KFULL, bool VST, bool DUAL = false,
+          bool GROUP = false>
 __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
-    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
-    T* __restrict__ y, int M, int N, int K, int64_t x_rs, int64_t y_rs,
-    const T* __restrict__ residual, int64_t r_rs, const T* __restrict__ w2 = nullptr) {
+    const T* __restrict__ x, const T* __restrict__ w_arg, const T* __restrict__ bias_arg,
+    T* __restrict__ y_arg, int M, int N_arg, int K, int64_t x_rs, int64_t y_rs_arg,
+    const T* __restrict__ residual, int64_t r_rs, const T* __restrict__ w2 = nullptr,
+    LinearGroup grp = {}) {
   static_assert(!DUAL || (KFULL && VST), "the fused SwiGLU uses the K-multiple store path");
+  static_assert(!GROUP || (KFULL && VST && !DUAL), "grouped projections use the store path");
   using MF = Mfma<T>;
   constexpr int NT = WM * WN * 64;  // threads per workgroup
   constexpr int TM = BM / WM;  // rows per wave
@@ -136,6 +150,21 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
     const int gm = m_tiles - first_m < kGroupM ? m_tiles - first_m : kGroupM;
     m_blk = first_m + (t % span) % gm;
     n_blk = (t % span) / gm;
+  }
+  // GROUP: the matrix of this N-tile and the tile's index inside it.
+  const T* w = w_arg;
+  const T* bias = bias_arg;
+  T* y = y_arg;
+  int N = N_arg;
+  int64_t y_rs = y_rs_arg;
+  if constexpr (GROUP) {
+    const int j = n_blk < grp.tile_end[0] ? 0 : (n_blk < grp.tile_end[1] ? 1 : 2);
+    n_blk -= j == 0 ? 0 : grp.tile_end[j - 1];
+    w = static_cast<const T*>(grp.w[j]);
+    bias = static_cast<const T*>(grp.bias[j]);
+    y = static_cast<T*>(grp.y[j]);
+    N = grp.n[j];
+    y_rs = grp.y_rs[j];
   }
   // DUAL: n0 is the first feature, BN / 2 of them per workgroup.
   const int n0 = n_blk * (DUAL ? BN / 2 : BN);
@@ -615,7 +644,71 @@ int gemm_swiglu(const void* x, int64_t x_rs, int64_t rows, int64_t K, int64_t N,
   return check_launch("slc_hip_linear_swiglu");
 }
 
+// Prefill-sized projections of one input (Q/K/V) in one launch, each matrix
+// bit for bit its own linear.  SLC_ERR_UNSUPPORTED (nothing launched) for
+// shapes the store epilogue cannot take.
+int gemm_group(const void* x, int64_t x_rs, int64_t rows, int64_t K, int count,
+               const void* const* w, const void* const* bias, void* const* y,
+               const int64_t* n, const int64_t* y_rs, int dtype, hipStream_t stream) {
+  bool ok = (dtype == SLC_BF16 || dtype == SLC_F16) && rows > 64 && count >= 1 && count <= 3 &&
+            K % kBK == 0 && x_rs % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+            128 * x_rs * 2 < (int64_t{1} << 31) && rows < (int64_t{1} << 31);
+  LinearGroup g{};
+  int tiles = 0;
+  for (int j = 0; j < 3; ++j) {
+    if (j < count) {
+      ok = ok && w[j] != nullptr && y[j] != nullptr && n[j] >= 1 && n[j] % 8 == 0 &&
+           y_rs[j] % 8 == 0 && y_rs[j] >= n[j] && n[j] * K * 2 < (int64_t{1} << 31) &&
+           128 * y_rs[j] * 2 < (int64_t{1} << 31) &&
+           ((reinterpret_cast<uintptr_t>(w[j]) | reinterpret_cast<uintptr_t>(y[j])) & 15) == 0;
+      if (!ok) break;
+      g.w[j] = w[j];
+      g.bias[j] = bias[j];
+      g.y[j] = y[j];
+      g.n[j] = static_cast<int>(n[j]);
+      g.y_rs[j] = y_rs[j];
+      tiles += static_cast<int>((n[j] + 127) / 128);
+    }
+    g.tile_end[j] = tiles;
+  }
+  if (!ok) return SLC_ERR_UNSUPPORTED;
+  const int M = static_cast<int>(rows), k = static_cast<int>(K);
+  const dim3 grid(static_cast<unsigned>(tiles), (M + 127) / 128);
+#define SLC_GROUP(TT)                                                                          \
+  hipLaunchKernelGGL((linear_mfma_kernel<TT, 128, 128, 2, 2, true, true, false, true>), grid, \
+                     dim3(256), 0, stream, static_cast<const TT*>(x),                           \
+                     static_cast<const TT*>(nullptr), static_cast<const TT*>(nullptr),          \
+                     static_cast<TT*>(nullptr), M, 0, k, x_rs, int64_t{0},                      \
+                     static_cast<const TT*>(nullptr), int64_t{0}, static_cast<const TT*>(nullptr), g)
+  if (dtype == SLC_BF16) {
+    SLC_GROUP(slc::bf16_t);
+  } else {
+    SLC_GROUP(slc::f16_t);
+  }
+#undef SLC_GROUP
+  return check_launch("slc_hip_linear_group");
+}
+
 }  // namespace slc_host
+
+extern "C" int slc_hip_linear_group(const void* input, int64_t in_stride_row, int64_t rows,
+                                    int64_t in_features, int count, const void* w0,
+                                    const void* b0, void* y0, int64_t n0, int64_t y0_rs,
+                                    const void* w1, const void* b1, void* y1, int64_t n1,
+                                    int64_t y1_rs, const void* w2, const void* b2, void* y2,
+                                    int64_t n2, int64_t y2_rs, int dtype, void* stream) {
+  SLC_REQUIRE(rows >= 0 && in_features > 0 && count >= 1 && count <= 3,
+              "slc_hip_linear_group: bad sizes");
+  if (rows == 0) return SLC_OK;
+  SLC_REQUIRE(input != nullptr, "slc_hip_linear_group: null input");
+  const void* ws[3] = {w0, w1, w2};
+  const void* bs[3] = {b0, b1, b2};
+  void* ys[3] = {y0, y1, y2};
+  const int64_t ns[3] = {n0, n1, n2};
+  const int64_t rss[3] = {y0_rs, y1_rs, y2_rs};
+  return slc_host::gemm_group(input, in_stride_row, rows, in_features, count, ws, bs, ys, ns, rss,
+                              dtype, static_cast<hipStream_t>(stream));
+}
 
 extern "C" int slc_hip_linear_swiglu(const void* input, int64_t in_stride_row, int64_t rows,
                                      int64_t in_features, int64_t features, const void* w_gate,

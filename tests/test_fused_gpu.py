@@ -311,3 +311,25 @@ def test_norm_linear_swiglu_prefill_rows(gpu, rows, hidden, features):
     want = hip_swiglu(hip_linear(x, wg), hip_linear(x, wu))
     torch.cuda.synchronize()
     assert_bitwise_equal(got, want)
+
+
+@pytest.mark.parametrize("rows,hidden,ns,bias", [(300, 896, (896, 128, 128), True),
+                                                 (4096, 896, (896, 128, 128), True),
+                                                 (129, 64, (200, 8), False),
+                                                 (100, 64, (96, 100), True)])
+def test_norm_linear_group_prefill_rows(gpu, rows, hidden, ns, bias):
+    # Prefill-sized rows: the norm, then the projections in one grouped launch
+    # (a width of 100 is not a multiple of 8: one launch per matrix), bit for
+    # bit the single linears.
+    announce(f"norm_linear_group prefill rows={rows} hidden={hidden} ns={ns} bias={bias}")
+    g = generator(rows + hidden + len(ns))
+    h = _t(g, rows, 1, hidden, device=gpu)
+    nw = _t(g, hidden, scale=0.5, device=gpu) + 1
+    ws = [_t(g, n, hidden, scale=0.05, device=gpu) for n in ns]
+    bs = [_t(g, n, scale=0.1, device=gpu) if bias else None for n in ns]
+    got = hip_norm_linear_group(h, nw, ws, bs, epsilon=1e-6)
+    x = hip_rms_norm(h, nw, epsilon=1e-6, round_before_weight=True)
+    want = [hip_linear(x, w, b) for w, b in zip(ws, bs)]
+    torch.cuda.synchronize()
+    for a, b in zip(got, want):
+        assert_bitwise_equal(a, b)
