@@ -520,6 +520,38 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
     const unsigned char* vt = kt + kV2TileBytes;
     const unsigned char* mt = kt + 2 * kV2TileBytes;  // mask tile, rows = queries
     const int k0 = t * kKeys;
+    if constexpr (MK != 0) {
+      // A mask tile that is -inf throughout (the part of a causal mask past
+      // the diagonal) adds exp2(-inf) = 0 to every sum and no new maximum:
+      // the tile is skipped (for finite scores the result is bit-identical;
+      // an infinite or NaN score under such a tile, which would make the
+      // reference's row NaN, is not looked at).  Every consumer wave reads
+      // the same tile, so all take the same branch; the barrier above is the
+      // only one per tile.
+      // First the element of the last query row and the first key (the last
+      // of a causal tile to become -inf; finite in almost any other mask):
+      // only when it is -inf is the whole tile read.
+      const unsigned char* corner = mt + (kV2Queries - 1) * kMaskRow + ((0 ^ ((kV2Queries - 1) & 7)) << 4);
+      const uint32_t cbits = ME == 4 ? *reinterpret_cast<const uint32_t*>(corner)
+                                     : *reinterpret_cast<const uint16_t*>(corner);
+      const uint32_t cninf = ME == 4 ? 0xff800000u : (MK == SLC_BF16 + 1 ? 0xff80u : 0xfc00u);
+      bool live = cbits != cninf;
+#pragma unroll
+      for (int off = lane * 16; !__any(live) && off < kMaskTile; off += 64 * 16) {
+        const uint4 v = *reinterpret_cast<const uint4*>(mt + off);
+        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (ME == 4) {
+            live |= w4[e] != 0xff800000u;
+          } else {
+            const uint32_t ninf = MK == SLC_BF16 + 1 ? 0xff80ff80u : 0xfc00fc00u;
+            live |= w4[e] != ninf;
+          }
+        }
+      }
+      if (!__any(live)) continue;
+    }
 
     // S^T blocks: 4 key blocks x 4 query blocks.
     f32x4_t st[4][4];
