@@ -64,3 +64,38 @@ def test_product_never_imports_the_oracle():
     for source in package.rglob("*.py"):
         text = source.read_text()
         assert "import oracle" not in text and "from oracle" not in text, source
+
+
+def test_fused_entry_points_decline_or_reject_before_any_device_call():
+    # Host-side argument logic of the fused entry points, exercised without a
+    # GPU: the shape checks run before any HIP call, so dummy (never
+    # dereferenced) pointers are enough.  -2 = SLC_ERR_UNSUPPORTED (the caller
+    # runs the unfused ops), -1 = SLC_ERR_INVALID_ARGUMENT.
+    if not _native.LIBRARY_PATH.exists():
+        pytest.fail(f"{_native.LIBRARY_PATH} missing: run __graft_entry__.build()")
+    lib = _native.library()
+    p = 0x1000  # 4 KiB-aligned, never dereferenced on these paths
+    bf16, f32 = 2, 0
+    # gate/up + SwiGLU: rows <= 64, K not a multiple of 64, N not a multiple of 8
+    assert lib.slc_hip_linear_swiglu(p, 896, 64, 896, 4864, p, p, p, 4864, bf16, None) == -2
+    assert lib.slc_hip_linear_swiglu(p, 72, 300, 72, 4864, p, p, p, 4864, bf16, None) == -2
+    assert lib.slc_hip_linear_swiglu(p, 896, 300, 896, 100, p, p, p, 100, bf16, None) == -2
+    assert lib.slc_hip_linear_swiglu(None, 896, 300, 896, 4864, p, p, p, 4864, bf16, None) == -1
+    assert lib.slc_hip_linear_swiglu(p, 896, 0, 896, 4864, p, p, p, 4864, bf16, None) == 0
+    # grouped projections: a width that is not a multiple of 8; fp32
+    assert lib.slc_hip_linear_group(p, 896, 300, 896, 2, p, None, p, 896, 896,
+                                    p, None, p, 100, 100, None, None, None, 0, 0,
+                                    bf16, None) == -2
+    assert lib.slc_hip_linear_group(p, 896, 300, 896, 1, p, None, p, 896, 896,
+                                    None, None, None, 0, 0, None, None, None, 0, 0,
+                                    f32, None) == -2
+    assert lib.slc_hip_linear_group(p, 896, 300, 896, 4, p, None, p, 896, 896,
+                                    None, None, None, 0, 0, None, None, None, 0, 0,
+                                    bf16, None) == -1
+    # RoPE decode attention: fp32 and head_dim 80 are not its kernel's cases
+    args = [p] * 10 + [None, 0, p, None, 0]
+    sizes = [4, 14, 2, 64, 256, 256]
+    strides = [896, 64, 128, 64, 128, 64, 64, 64, 32768, 128, 64, 0, 0, 896, 64]
+    assert lib.slc_hip_rope_decode_attention(*args, f32, *sizes, *strides, 0.125, None) == -2
+    sizes_d80 = [4, 14, 2, 80, 256, 256]
+    assert lib.slc_hip_rope_decode_attention(*args, bf16, *sizes_d80, *strides, 0.125, None) == -2
