@@ -232,7 +232,7 @@ def _time_graph(fn, reps: int = 20, outer: int = 5) -> float:
 
 
 def bench_kernels() -> dict:
-    """The other hot-path ops at their SURVEY config-3/4 shapes, each against
+    """The other hot-path ops at their benchmark-config (3 and 4) shapes, each against
     the roofline that bounds it (bf16; synthetic N(0,1) data)."""
 
     from stateful_llm_compiler_hip.backends import (
