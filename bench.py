@@ -390,8 +390,7 @@ def bench_decode_tokens(seed: int = 5) -> dict:
     The decode step (all 24 layers + LM head + argmax) is one HIP-graph replay
     of the fully lowered KernelIR function."""
 
-    from oracle.qwen2_model import causal_mask  # only builds the input mask
-    from stateful_llm_compiler_hip.qwen2 import Qwen2Config, init_weights
+    from stateful_llm_compiler_hip.qwen2 import Qwen2Config, causal_prefill_mask, init_weights
     from stateful_llm_compiler_hip.runtime import Qwen2Runtime
 
     device = torch.device("cuda:0")
@@ -401,7 +400,7 @@ def bench_decode_tokens(seed: int = 5) -> dict:
                            device="cuda:0", validate=False)
     g = torch.Generator(device="cpu").manual_seed(seed)
     ids = torch.randint(0, config.vocab_size, (MODEL_BATCH, PROMPT), generator=g).to(device)
-    mask = causal_mask(MODEL_BATCH, PROMPT).to(device)
+    mask = causal_prefill_mask(MODEL_BATCH, PROMPT, device=device)
     pos = torch.arange(PROMPT, device=device).view(1, -1).expand(MODEL_BATCH, -1).contiguous()
 
     runtime.prefill(ids, mask, pos)  # warm-up (kernel loading, allocator)

@@ -56,6 +56,19 @@ enum slc_dtype {
  * arguments; nothing was launched and the caller runs the unfused ops. */
 enum slc_status { SLC_OK = 0, SLC_ERR_INVALID_ARGUMENT = -1, SLC_ERR_UNSUPPORTED = -2 };
 
+/*
+ * Softmax order of the attention entry points.
+ *   SLC_SOFTMAX_ONLINE : single pass; the running (unnormalised) probabilities
+ *                        are rounded to the I/O dtype for the P.V product and
+ *                        the sum divides the fp32 result (flash-attention form).
+ *   SLC_SOFTMAX_EXACT  : the reference executor's order (execution.py:319-327,
+ *                        softmax(...).to(dtype) then matmul): probabilities
+ *                        are normalised in fp32, then rounded, then P.V.
+ *                        K and V are still read once (decode) / the key tiles
+ *                        twice from LDS-staged tiles (prefill).
+ */
+enum slc_softmax_order { SLC_SOFTMAX_ONLINE = 0, SLC_SOFTMAX_EXACT = 1 };
+
 /* Library version (major*10000 + minor*100 + patch). */
 SLC_API int slc_hip_version(void);
 
@@ -115,11 +128,23 @@ SLC_API int slc_hip_kv_store(void* key_buffer, void* value_buffer, const void* k
  *   output       : [batch, q_heads, 1, head_dim], strides (out_sb, out_sh),
  *                  same dtype as query
  *   workspace    : device scratch of at least
- *                  slc_hip_decode_attention_workspace_size(...) bytes
- *                  (may be NULL when that size is 0)
+ *                  slc_hip_decode_attention_workspace_size(...) bytes (split
+ *                  partials; may be NULL when that size is 0)
+ *   counters     : caller-owned int array of at least
+ *                  slc_hip_decode_attention_counter_count(batch, kv_heads)
+ *                  elements (cross-workgroup arrival counters): zero-fill it
+ *                  once when it is allocated; every call leaves it zero
+ *                  again.  Calls that share counters or a workspace must not
+ *                  run concurrently (calls on one stream never do); give each
+ *                  stream (or each captured graph that may replay
+ *                  concurrently) its own.
  * Token s of batch b is attended iff s < min(lengths[b], mask_len, capacity).
  * kv head of query head h is h / (q_heads / kv_heads).
- * split_tokens selects the split-sequence chunk (0 = automatic).
+ * split_tokens selects the split-sequence chunk (0 = automatic; ignored by
+ * the exact order, which runs one chunk per (batch, kv head)).
+ * softmax_order: SLC_SOFTMAX_ONLINE or SLC_SOFTMAX_EXACT; the exact order
+ * takes min(mask_len, capacity) up to
+ * slc_hip_decode_attention_exact_max_tokens(head_dim, dtype) tokens.
  */
 SLC_API int64_t slc_hip_decode_attention_workspace_size(int64_t batch, int64_t q_heads,
                                                 int64_t head_dim,
@@ -127,15 +152,22 @@ SLC_API int64_t slc_hip_decode_attention_workspace_size(int64_t batch, int64_t q
                                                 int64_t kv_heads, int dtype,
                                                 int64_t split_tokens);
 
+SLC_API int64_t slc_hip_decode_attention_counter_count(int64_t batch, int64_t kv_heads);
+
 SLC_API int slc_hip_decode_attention(
     const void* query, const void* key_buffer, const void* value_buffer,
     const void* lengths, int lengths_dtype, const void* mask, int mask_dtype,
-    void* output, void* workspace, int64_t workspace_bytes, int dtype,
+    void* output, void* workspace, int64_t workspace_bytes, int* counters,
+    int64_t num_counters, int dtype,
     int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
     int64_t capacity, int64_t mask_len, int64_t q_stride_b, int64_t q_stride_h,
     int64_t kv_stride_b, int64_t kv_stride_s, int64_t kv_stride_h,
     int64_t mask_stride_b, int64_t mask_stride_s, int64_t out_stride_b,
-    int64_t out_stride_h, float scale, int64_t split_tokens, void* stream);
+    int64_t out_stride_h, float scale, int64_t split_tokens, int softmax_order,
+    void* stream);
+
+/* Longest mask the SLC_SOFTMAX_EXACT order takes (INT64_MAX: no limit). */
+SLC_API int64_t slc_hip_decode_attention_exact_max_tokens(int64_t head_dim, int dtype);
 
 /*
  * rms_norm over the last axis:
@@ -190,6 +222,7 @@ SLC_API int slc_hip_linear(const void* input, const void* weight,
  *           mask_dtype, or NULL (= zeros)
  *   causal: nonzero removes keys after each query (the op's causal=True)
  *   output [B, QH, T, D] with (o_sb, o_sh, o_st) strides, dtype of query
+ *   softmax_order: SLC_SOFTMAX_ONLINE or SLC_SOFTMAX_EXACT (any length)
  * kv head of query head h is h / (QH / KVH).
  */
 SLC_API int slc_hip_prefill_attention(
@@ -199,7 +232,7 @@ SLC_API int slc_hip_prefill_attention(
     int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh, int64_t k_st,
     int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t m_sb, int64_t m_sq,
     int64_t m_sk, int64_t o_sb, int64_t o_sh, int64_t o_st, float scale,
-    void* stream);
+    int softmax_order, void* stream);
 
 /*
  * Ops that complete a Qwen2 step without eager PyTorch kernels.  None has a
@@ -214,7 +247,13 @@ SLC_API int slc_hip_prefill_attention(
  *                                                           (qwen2.py:136-149)
  *   kv_advance : lengths_out = lengths_in + delta (may alias); sets *overflow
  *                when a length leaves [0, capacity]          (execution.py:421-443)
- *   argmax     : output[r] = index of the first maximum of row r
+ *   argmax     : output[r] = index of the first maximum of row r (NaN counts
+ *                as the maximum, as in torch.argmax).  With a scratch
+ *                workspace of slc_hip_argmax_workspace_size(rows) bytes and
+ *                `rows` counters (caller-owned, zero-filled once, left zeroed
+ *                by every call; neither shared by concurrent calls) wide rows
+ *                are split over several workgroups; with NULL each row is one
+ *                workgroup.  Same result.
  */
 SLC_API int slc_hip_embedding(const int64_t* ids, const void* table, void* output,
                               int dtype, int64_t rows, int64_t hidden, int64_t vocab,
@@ -230,8 +269,11 @@ SLC_API int slc_hip_rope_table(const int64_t* positions, const float* inv_freq,
 SLC_API int slc_hip_kv_advance(const int64_t* lengths_in, int64_t* lengths_out,
                                int64_t batch, int64_t delta, int64_t capacity,
                                int* overflow, void* stream);
+SLC_API int64_t slc_hip_argmax_workspace_size(int64_t rows);
 SLC_API int slc_hip_argmax(const void* logits, int64_t* output, int dtype, int64_t rows,
-                           int64_t cols, int64_t row_stride, void* stream);
+                           int64_t cols, int64_t row_stride, void* workspace,
+                           int64_t workspace_bytes, int* counters, int64_t num_counters,
+                           void* stream);
 
 /*
  * Fused decode-step ops (no single counterpart in the reference: each one
@@ -262,7 +304,11 @@ SLC_API int slc_hip_argmax(const void* logits, int64_t* output, int dtype, int64
  *                       allowed), flagging *overflow past the capacity, as
  *                       slc_hip_kv_advance does after the store (the
  *                       runtime.kv.advance that follows the store in the
- *                       decode graph, execution.py:741-767).
+ *                       decode graph, execution.py:741-767).  The advance
+ *                       rides on the store kernel when `counters` (>= 1 int,
+ *                       caller-owned, zero-filled once, left zeroed, not
+ *                       shared by concurrent calls) is given, else it is a
+ *                       second launch.
  */
 SLC_API int slc_hip_norm_linear_group(
     const void* x, int64_t x_rs, const void* norm_weight, float epsilon, int64_t rows,
@@ -286,7 +332,8 @@ SLC_API int slc_hip_rope_kv_store(
     int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t tokens, int64_t head_dim,
     int64_t capacity, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh,
     int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t cos_sb, int64_t cos_st,
-    int64_t sin_sb, int64_t sin_st, int64_t qo_sb, int64_t qo_sh, int64_t qo_st, void* stream);
+    int64_t sin_sb, int64_t sin_st, int64_t qo_sb, int64_t qo_sh, int64_t qo_st, int* counters,
+    int64_t num_counters, void* stream);
 
 /*
  * linear_group: y_j = linear(x, w_j, b_j) for count = 1..3 matrices [n_j,
@@ -336,19 +383,23 @@ SLC_API int slc_hip_linear_swiglu(const void* input, int64_t in_stride_row, int6
  * [B, D] (the token's rows); buffers [B, capacity, kv_heads, D] with strides
  * as in slc_hip_decode_attention; lengths int64; the workspace is
  * slc_hip_decode_attention_workspace_size(batch, q_heads, head_dim, mask_len,
- * kv_heads, dtype, 0) bytes.  Returns SLC_ERR_UNSUPPORTED (nothing launched)
- * for shapes, dtypes or alignments its kernel does not take.
+ * kv_heads, dtype, 0) bytes and the counters are
+ * slc_hip_decode_attention_counter_count(batch, kv_heads) ints, owned as
+ * described there (the counters also carry the length advance).  softmax_order as in slc_hip_decode_attention.
+ * Returns SLC_ERR_UNSUPPORTED (nothing launched) for shapes, dtypes,
+ * alignments or (exact order) mask lengths its kernel does not take.
  */
 SLC_API int slc_hip_rope_decode_attention(
     const void* query, const void* key, const void* value, const void* cosine,
     const void* sine, void* key_buffer, void* value_buffer, const int64_t* lengths,
     int64_t* lengths_out, int* overflow, const void* mask, int mask_dtype, void* output,
-    void* workspace, int64_t workspace_bytes, int dtype, int64_t batch, int64_t q_heads,
+    void* workspace, int64_t workspace_bytes, int* counters, int64_t num_counters, int dtype,
+    int64_t batch, int64_t q_heads,
     int64_t kv_heads, int64_t head_dim, int64_t capacity, int64_t mask_len, int64_t q_stride_b,
     int64_t q_stride_h, int64_t k_stride_b, int64_t k_stride_h, int64_t v_stride_b,
     int64_t v_stride_h, int64_t cos_stride_b, int64_t sin_stride_b, int64_t kv_stride_b,
     int64_t kv_stride_s, int64_t kv_stride_h, int64_t mask_stride_b, int64_t mask_stride_s,
-    int64_t out_stride_b, int64_t out_stride_h, float scale, void* stream);
+    int64_t out_stride_b, int64_t out_stride_h, float scale, int softmax_order, void* stream);
 
 #ifdef __cplusplus
 }

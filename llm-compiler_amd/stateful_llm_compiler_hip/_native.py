@@ -28,6 +28,9 @@ SLC_BF16 = 2
 SLC_I32 = 3
 SLC_I64 = 4
 
+# slc_softmax_order
+SOFTMAX_ORDERS = {"online": 0, "exact": 1}
+
 _DTYPE_TAGS = {
     torch.float32: SLC_F32,
     torch.float16: SLC_F16,
@@ -56,29 +59,32 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "slc_hip_swiglu": (_I, [_P, _P, _P, _I, _L, _P]),
     "slc_hip_rope_table": (_I, [_P, _P, _P, _P, _I, _L, _L, _L, _L, _P]),
     "slc_hip_kv_advance": (_I, [_P, _P, _L, _L, _L, _P, _P]),
-    "slc_hip_argmax": (_I, [_P, _P, _I, _L, _L, _L, _P]),
+    "slc_hip_argmax_workspace_size": (_L, [_L]),
+    "slc_hip_argmax": (_I, [_P, _P, _I, _L, _L, _L, _P, _L, _P, _L, _P]),
     "slc_hip_norm_linear_group": (
         _I,
         [_P, _L, _P, _F, _L, _L, _I] + [_P, _P, _P, _L, _L] * 3 + [_I, _P],
     ),
     "slc_hip_norm_linear_swiglu": (_I, [_P, _L, _P, _F, _L, _L, _L, _P, _P, _P, _L, _I, _P]),
     "slc_hip_linear_residual": (_I, [_P, _L, _L, _L, _L, _P, _P, _P, _L, _P, _L, _I, _P]),
-    "slc_hip_rope_kv_store": (_I, [_P] * 11 + [_L, _I] + [_L] * 6 + [_L] * 16 + [_P]),
+    "slc_hip_rope_kv_store": (_I, [_P] * 11 + [_L, _I] + [_L] * 6 + [_L] * 16 + [_P, _L, _P]),
     "slc_hip_linear_group": (
         _I, [_P, _L, _L, _L, _I] + [_P, _P, _P, _L, _L] * 3 + [_I, _P]),
     "slc_hip_linear_swiglu": (_I, [_P, _L, _L, _L, _L, _P, _P, _P, _L, _I, _P]),
     "slc_hip_rope_decode_attention": (
-        _I, [_P] * 11 + [_I, _P, _P, _L, _I] + [_L] * 6 + [_L] * 15 + [_F, _P]),
+        _I, [_P] * 11 + [_I, _P, _P, _L, _P, _L, _I] + [_L] * 6 + [_L] * 15 + [_F, _I, _P]),
     "slc_hip_decode_attention_workspace_size": (
         _L,
         [_L, _L, _L, _L, _L, _I, _L],
     ),
     "slc_hip_decode_attention": (
         _I,
-        [_P, _P, _P, _P, _I, _P, _I, _P, _P, _L, _I]
+        [_P, _P, _P, _P, _I, _P, _I, _P, _P, _L, _P, _L, _I]
         + [_L] * 15
-        + [_F, _L, _P],
+        + [_F, _L, _I, _P],
     ),
+    "slc_hip_decode_attention_exact_max_tokens": (_L, [_L, _I]),
+    "slc_hip_decode_attention_counter_count": (_L, [_L, _L]),
     "slc_hip_rms_norm": (
         _I,
         [_P, _P, _P, _I, _I, _I, _I, _L, _L, _L, _L, _F, _I, _P],
@@ -89,7 +95,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "slc_hip_prefill_attention": (
         _I,
-        [_P, _P, _P, _P, _I, _P, _I, _L, _L, _L, _L, _L, _I] + [_L] * 15 + [_F, _P],
+        [_P, _P, _P, _P, _I, _P, _I, _L, _L, _L, _L, _L, _I] + [_L] * 15 + [_F, _I, _P],
     ),
     "slc_hip_rope": (
         _I,
@@ -156,3 +162,69 @@ def check(status: int, what: str) -> None:
     if status != 0:
         message = library().slc_hip_last_error().decode(errors="replace")
         raise KernelLaunchError(f"{what} failed (status {status}): {message}")
+
+
+def softmax_order_tag(order: str) -> int:
+    try:
+        return SOFTMAX_ORDERS[order]
+    except KeyError as error:
+        raise ValueError(f"softmax order must be one of {sorted(SOFTMAX_ORDERS)}, got {order!r}") from error
+
+
+class DeviceWorkspace:
+    """Caller-owned device memory of the kernels that combine work across
+    workgroups: one zero-filled int32 counter array, shared by every kernel
+    kind (each kernel leaves its counters zero again), and scratch buffers
+    per kernel kind for partial results.  Kernels that run in order (one
+    stream, or one captured graph) can share a workspace; kernels that may run
+    concurrently need separate ones.  Buffers that were outgrown stay alive (a
+    captured graph may still hold their address)."""
+
+    def __init__(self, device: torch.device | str) -> None:
+        self.device = torch.device(device)
+        self._counters: torch.Tensor | None = None
+        self._scratch: dict[str, torch.Tensor] = {}
+        self._retired: list[torch.Tensor] = []
+
+    def counters(self, count: int) -> torch.Tensor:
+        """Zeroed int32 counters, at least ``count`` (and at least 1) of them."""
+
+        current = self._counters
+        if current is None or current.numel() < count:
+            if current is not None:
+                self._retired.append(current)
+            size = max(int(count), 2 * (current.numel() if current is not None else 0), 64)
+            self._counters = torch.zeros(size, dtype=torch.int32, device=self.device)
+        return self._counters
+
+    def scratch(self, name: str, nbytes: int) -> torch.Tensor | None:
+        """Scratch bytes of a kernel kind (no initial contents), or None."""
+
+        if nbytes <= 0:
+            return None
+        buffer = self._scratch.get(name)
+        if buffer is None or buffer.numel() < nbytes:
+            if buffer is not None:
+                self._retired.append(buffer)
+            size = max(int(nbytes), 2 * (buffer.numel() if buffer is not None else 0))
+            buffer = torch.empty(size, dtype=torch.uint8, device=self.device)
+            self._scratch[name] = buffer
+        return buffer
+
+
+_stream_workspaces: dict[tuple[int, int], DeviceWorkspace] = {}
+
+
+def stream_workspace(device: torch.device) -> DeviceWorkspace:
+    """The workspace of PyTorch's current stream on ``device``, for callers
+    that do not own one (calls on one stream never overlap)."""
+
+    stream = current_stream(device)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, stream)
+    with _lock:
+        workspace = _stream_workspaces.get(key)
+        if workspace is None:
+            workspace = DeviceWorkspace(torch.device("cuda", index))
+            _stream_workspaces[key] = workspace
+    return workspace

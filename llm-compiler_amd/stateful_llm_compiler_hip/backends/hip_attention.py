@@ -15,13 +15,21 @@ from .. import _native
 from .hip_ops import check_flag
 
 
-def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
-    """Split-sequence partials; PyTorch's caching allocator makes this cheap and
-    keeps it legal inside HIP graph capture."""
+def _workspace(lib, device: torch.device, nbytes: int, batch: int, kv_heads: int,
+               workspace: _native.DeviceWorkspace | None) -> tuple[torch.Tensor | None, torch.Tensor, int]:
+    """Split-sequence partials and arrival counters: the caller's workspace,
+    else the current stream's."""
 
-    if nbytes <= 0:
-        return None
-    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    owner = workspace if workspace is not None else _native.stream_workspace(device)
+    count = int(lib.slc_hip_decode_attention_counter_count(batch, kv_heads))
+    return owner.scratch("decode_attention", nbytes), owner.counters(count), count
+
+
+def exact_max_tokens(head_dim: int, dtype: torch.dtype) -> int:
+    """Longest mask the exact softmax order takes for this shape."""
+
+    return int(_native.library().slc_hip_decode_attention_exact_max_tokens(
+        head_dim, _native.dtype_tag(dtype)))
 
 
 def hip_decode_attention(
@@ -33,6 +41,8 @@ def hip_decode_attention(
     *,
     scale: float,
     split_tokens: int = 0,
+    softmax_order: str = "online",
+    workspace: _native.DeviceWorkspace | None = None,
 ) -> torch.Tensor:
     """B x H x 1 x D GQA decode attention over a B x Cap x KVH x D buffer.
 
@@ -42,8 +52,15 @@ def hip_decode_attention(
     permuted to BSHD) is accepted.  ``lengths`` is int64 (the runtime's
     dtype) or int32.  ``attention_mask`` is B x 1 x 1 x S additive, or None
     for an all-zero mask over the whole capacity.
+
+    ``softmax_order``: "online" (the reference Triton kernel's single-pass
+    form, the default) or "exact" (normalise, round, then P.V -- the
+    reference executor's order; masks up to ``exact_max_tokens`` long).
+    ``workspace``: the caller's ``DeviceWorkspace`` (else the current
+    stream's); calls that may run concurrently need separate ones.
     """
 
+    order = _native.softmax_order_tag(softmax_order)
     tensors = [query, key_buffer, value_buffer, lengths]
     if attention_mask is not None:
         tensors.append(attention_mask)
@@ -107,7 +124,7 @@ def hip_decode_attention(
         batch, query_heads, head_dim, mask_len, kv_heads, dtype, split_tokens
     )
     stream = _native.current_stream(query.device)
-    workspace = _workspace(query.device, nbytes)
+    buffer, counters, count = _workspace(lib, query.device, nbytes, batch, kv_heads, workspace)
     if attention_mask is None:
         mask_ptr, mask_dtype, mask_sb, mask_ss = None, 0, 0, 0
     else:
@@ -123,8 +140,10 @@ def hip_decode_attention(
         mask_ptr,
         mask_dtype,
         output.data_ptr(),
-        None if workspace is None else workspace.data_ptr(),
+        None if buffer is None else buffer.data_ptr(),
         nbytes,
+        counters.data_ptr(),
+        count,
         dtype,
         batch,
         query_heads,
@@ -143,6 +162,7 @@ def hip_decode_attention(
         output.stride(1),
         float(scale),
         int(split_tokens),
+        order,
         stream,
     )
     _native.check(status, "slc_hip_decode_attention")
@@ -163,6 +183,8 @@ def hip_rope_decode_attention(
     *,
     scale: float,
     overflow: torch.Tensor | None = None,
+    softmax_order: str = "online",
+    workspace: _native.DeviceWorkspace | None = None,
 ) -> torch.Tensor | None:
     """One decode token's RoPE, KV store at ``lengths``, length advance by one
     (into ``lengths_out``, which may be ``lengths``) and GQA attention, in one
@@ -172,7 +194,10 @@ def hip_rope_decode_attention(
     query [B, QH, 1, D] and key/value [B, KVH, 1, D] unrotated projections,
     cosine/sine [B, 1, D].  Returns None, having done nothing, when the fused
     kernel does not take the case (the caller then runs the two ops).
+    ``softmax_order`` and ``workspace`` as in ``hip_decode_attention``.
     """
+
+    order = _native.softmax_order_tag(softmax_order)
 
     tensors = [query, key, value, cosine, sine, key_buffer, value_buffer, lengths, lengths_out]
     if attention_mask is not None:
@@ -216,7 +241,7 @@ def hip_rope_decode_attention(
     nbytes = lib.slc_hip_decode_attention_workspace_size(
         batch, query_heads, head_dim, mask_len, kv_heads, dtype, 0
     )
-    workspace = _workspace(query.device, nbytes)
+    buffer, counters, count = _workspace(lib, query.device, nbytes, batch, kv_heads, workspace)
     if attention_mask is None:
         mask_ptr, mask_dtype, mask_sb, mask_ss = None, 0, 0, 0
     else:
@@ -228,12 +253,12 @@ def hip_rope_decode_attention(
         key_buffer.data_ptr(), value_buffer.data_ptr(), lengths.data_ptr(),
         lengths_out.data_ptr(), None if overflow is None else overflow.data_ptr(),
         mask_ptr, mask_dtype, output.data_ptr(),
-        None if workspace is None else workspace.data_ptr(), nbytes, dtype,
+        None if buffer is None else buffer.data_ptr(), nbytes, counters.data_ptr(), count, dtype,
         batch, query_heads, kv_heads, head_dim, capacity, mask_len,
         query.stride(0), query.stride(1), key.stride(0), key.stride(1),
         value.stride(0), value.stride(1), cosine.stride(0), sine.stride(0),
         key_buffer.stride(0), key_buffer.stride(1), key_buffer.stride(2),
-        mask_sb, mask_ss, output.stride(0), output.stride(1), float(scale),
+        mask_sb, mask_ss, output.stride(0), output.stride(1), float(scale), order,
         _native.current_stream(query.device),
     )
     if status == _UNSUPPORTED:

@@ -245,12 +245,15 @@ def hip_rope_kv_store(
     overflow: torch.Tensor | None = None,
     advance: int = 0,
     lengths_out: torch.Tensor | None = None,
+    workspace: _native.DeviceWorkspace | None = None,
 ) -> torch.Tensor:
     """``q_rot, k_rot = rope(query, key, cosine, sine)``; store ``k_rot`` and
     ``value`` rows at ``positions[b] + t`` of the [B, Cap, H, D] buffers;
     return ``q_rot``.  With ``advance > 0`` also write
     ``lengths_out = positions + advance`` (``lengths_out`` may be
-    ``positions``), as the kv advance after the store would."""
+    ``positions``), as the kv advance after the store would; the advance
+    counts the store's workgroups in ``workspace`` (else the current
+    stream's)."""
 
     tensors = (query, key, value, cosine, sine, key_buffer, value_buffer, positions)
     if not all(t.is_cuda for t in tensors):
@@ -286,6 +289,10 @@ def hip_rope_kv_store(
         if lengths_out is not None and lengths_out.data_ptr() == positions.data_ptr():
             raise ValueError("HIP rope_kv_store: in-place advance needs contiguous positions")
         positions = positions.contiguous()
+    counter = None
+    if lengths_out is not None:
+        owner = workspace if workspace is not None else _native.stream_workspace(query.device)
+        counter = owner.counters(1)
     status = _native.library().slc_hip_rope_kv_store(
         query.data_ptr(), key.data_ptr(), value.data_ptr(), cosine.data_ptr(), sine.data_ptr(),
         q_out.data_ptr(), key_buffer.data_ptr(), value_buffer.data_ptr(), positions.data_ptr(),
@@ -298,6 +305,7 @@ def hip_rope_kv_store(
         value.stride(0), value.stride(1), value.stride(2),
         cosine.stride(0), cosine.stride(1), sine.stride(0), sine.stride(1),
         q_out.stride(0), q_out.stride(1), q_out.stride(2),
+        None if counter is None else counter.data_ptr(), 0 if counter is None else counter.numel(),
         _native.current_stream(query.device),
     )
     _native.check(status, "slc_hip_rope_kv_store")

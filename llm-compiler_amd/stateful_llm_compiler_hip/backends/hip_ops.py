@@ -130,11 +130,13 @@ def hip_kv_advance(
     return result
 
 
-def hip_argmax(logits: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
+def hip_argmax(logits: torch.Tensor, *, out: torch.Tensor | None = None,
+               workspace: _native.DeviceWorkspace | None = None) -> torch.Tensor:
     """Index of the first maximum along the last axis (int64).
 
     ``out`` (contiguous int64 with one element per row) receives the result in
-    place, e.g. a decode loop's token buffer."""
+    place, e.g. a decode loop's token buffer.  ``workspace`` (else the
+    current stream's) lets wide rows split over several workgroups."""
 
     _require_gpu(logits, what="HIP argmax")
     if logits.dtype not in _FLOATS or logits.stride(-1) != 1:
@@ -146,9 +148,15 @@ def hip_argmax(logits: torch.Tensor, *, out: torch.Tensor | None = None) -> torc
     elif (not out.is_cuda or out.dtype != torch.int64 or not out.is_contiguous()
           or out.numel() != flat.shape[0]):
         raise ValueError("HIP argmax: out must be a contiguous int64 tensor with one entry per row")
-    status = _native.library().slc_hip_argmax(
+    lib = _native.library()
+    nbytes = lib.slc_hip_argmax_workspace_size(flat.shape[0])
+    owner = workspace if workspace is not None else _native.stream_workspace(logits.device)
+    buffer = owner.scratch("argmax", nbytes)
+    counters = owner.counters(flat.shape[0])
+    status = lib.slc_hip_argmax(
         flat.data_ptr(), out.data_ptr(), _native.dtype_tag(logits.dtype), flat.shape[0], cols,
-        flat.stride(0), _native.current_stream(logits.device),
+        flat.stride(0), None if buffer is None else buffer.data_ptr(), nbytes,
+        counters.data_ptr(), counters.numel(), _native.current_stream(logits.device),
     )
     _native.check(status, "slc_hip_argmax")
     return out.view(logits.shape[:-1])

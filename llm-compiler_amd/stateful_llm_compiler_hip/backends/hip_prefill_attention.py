@@ -23,9 +23,16 @@ def hip_prefill_attention(
     *,
     scale: float,
     causal: bool = False,
+    softmax_order: str = "online",
 ) -> torch.Tensor:
-    """B x QH x T x D attention over B x KVH x T x D keys/values."""
+    """B x QH x T x D attention over B x KVH x T x D keys/values.
 
+    ``softmax_order``: "online" (single pass, the reference Triton kernel's
+    form) or "exact" (two passes: the row max and sum first, then the
+    normalised probabilities rounded to the I/O dtype weigh V -- the
+    reference executor's order, execution.py:720-739)."""
+
+    order = _native.softmax_order_tag(softmax_order)
     tensors = [query, key, value] + ([attention_mask] if attention_mask is not None else [])
     if not all(tensor.is_cuda for tensor in tensors):
         raise ValueError("HIP prefill attention: all tensors must be on the GPU")
@@ -89,6 +96,7 @@ def hip_prefill_attention(
         *ms,
         *output.stride()[:3],
         float(scale),
+        order,
         _native.current_stream(query.device),
     )
     _native.check(status, "slc_hip_prefill_attention")

@@ -28,6 +28,12 @@ class CompileOptions:
     # Fuse decode-step op chains into single kernels (fast mode only; the
     # fused kernels are bit-identical to the chains they replace).
     fuse: bool = True
+    # Softmax order of the HIP attention kernels in fast mode ("exact" or
+    # "online"; see lowering.SOFTMAX_ORDERS).
+    attention_softmax: str = "exact"
+    # GEMM family: None follows the numerical mode; "pytorch_compatible" in
+    # fast mode runs the linears on PyTorch's ROCm BLAS call.
+    linear_backend: str | None = None
 
 
 @dataclass
@@ -53,7 +59,9 @@ def compile_module(module: Module, options: CompileOptions | None = None) -> Com
     if options.rmsnorm_profile is not None:
         manager.add(SelectRMSNormLoweringPass(RMSNormCostModel.load(options.rmsnorm_profile),
                                               fallback=options.rmsnorm_fallback))
-    manager.add(LowerToKernelIRPass(numerical_mode=options.numerical_mode))
+    manager.add(LowerToKernelIRPass(numerical_mode=options.numerical_mode,
+                                    attention_softmax=options.attention_softmax,
+                                    linear_backend=options.linear_backend))
     if options.fuse and options.numerical_mode == "fast":
         manager.add(FuseDecodeKernelsPass())
     results = manager.run(module)

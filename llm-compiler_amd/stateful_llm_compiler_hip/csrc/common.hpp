@@ -135,14 +135,7 @@ void mark_kernel_end(hipStream_t stream);
 // kernel must be idempotent for its inputs (it only rewrites its outputs).
 int timed_repeats();
 
-// Per-stream regions of static device scratch (counters, partials) for
-// kernels that combine work across workgroups in their last workgroup: the
-// first kStreamRegions distinct streams of each kind own one region each
-// (calls on one stream run in order, so a region is never used by two calls
-// at once); further streams get -1 and take a path without such scratch.
-constexpr int kStreamRegions = 16;
-enum RegionKind { kRegionArgmax = 0, kRegionRopeStore = 1, kRegionKinds = 2 };
-int stream_region(RegionKind kind, hipStream_t stream);
+
 
 inline int dtype_size(int dtype) {
   switch (dtype) {

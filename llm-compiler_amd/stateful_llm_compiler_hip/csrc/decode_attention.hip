@@ -26,7 +26,10 @@
 //    the extra launch.)
 //  * Loops stop at the batch's own length, not at the capacity.
 // Other dtypes/shapes take a straightforward wave-per-token kernel.
+#include <algorithm>
+#include <climits>
 #include <mutex>
+#include <type_traits>
 
 #include "common.hpp"
 #include "op_math.hpp"
@@ -120,29 +123,29 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int 
 }
 
 // ---- merge inside the split kernel ------------------------------------------
-// With a counter region (one per stream, static device memory) every split
-// workgroup publishes its partial with agent-scope stores, waits for them to
-// complete and bumps its (batch, kv-head)'s counter; the workgroup that
-// completes the count merges the partials (agent-scope loads: they bypass the
-// non-coherent per-XCD caches) and re-arms the counter.  No release fence is
-// needed: the count is bumped only after this workgroup's stores completed.
-// The merge weighs the chunks exactly as the separate merge kernel does, so
-// both paths give bit-identical outputs.
-constexpr int kCounterRegions = 16;
-constexpr int kCounterPairs = 8192;  // (batch, kv-head) pairs per region
-__device__ int g_merge_counters[kCounterRegions][kCounterPairs];
-// Per-batch length-advance counters of the RoPE + store variant.
-__device__ int g_advance_counters[kCounterRegions][kCounterPairs];
-
-__device__ __forceinline__ void publish(float* p, float v, const int* counters) {
-  if (counters != nullptr) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  } else {
-    *p = v;
-  }
+// The caller's counter array holds one counter per (batch, kv-head) (and one
+// per batch for the RoPE variant's length advance); it is zero-filled once by
+// its owner and every kernel leaves it zero again.  Every
+// split workgroup publishes its partial with agent-scope stores, meets its
+// waves at a barrier, and one thread bumps the (batch, kv-head)'s counter
+// with an agent-scope acquire-release add: the release orders the whole
+// workgroup's stores (made visible to that thread by the barrier) before the
+// count, and the acquire of the workgroup that completes the count orders its
+// later loads of the partials after every other workgroup's release.  The
+// merge weighs the chunks exactly as the separate merge kernel does, so both
+// paths give bit-identical outputs.  Two calls that share counters must not
+// run concurrently (calls on one stream never do).
+__device__ __forceinline__ void publish(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ float fetch_partial(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int count_arrival(int* counter) {
+  return __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void rearm(int* counter) {
+  __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 constexpr int kFusedMergeUnroll = 8;
@@ -161,7 +164,7 @@ struct LenAdvance {
 
 __device__ __forceinline__ void finish_advance(const LenAdvance& adv, int before) {
   if (adv.counter == nullptr || before != adv.total - 1) return;
-  __hip_atomic_store(adv.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  rearm(adv.counter);
   *adv.out = adv.next;
   if (adv.overflow != nullptr && (adv.next > adv.capacity || adv.next < 0)) *adv.overflow = 1;
 }
@@ -182,7 +185,7 @@ struct RopeStore {
   void* value_out;
   int64_t* lengths_out;
   int* overflow;
-  int* counters;  // per-batch advance counters of the stream's region
+  int* counters;  // per-batch advance counters (caller's counter array)
 };
 
 // Qwen2 half rotation of one lane's slices: slice kk pairs with kk + KK/2
@@ -225,17 +228,13 @@ __device__ __forceinline__ void merge_if_last(const float* part_o, const float* 
                                               int nchunks, const LenAdvance& adv) {
   const int tid = threadIdx.x;
   __shared__ int is_last;
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores landed
-  __syncthreads();
+  __syncthreads();  // every wave's partial stores precede thread 0's release
   if (tid == 0) {
     int* counter = counters + b * kv_heads + kvh;
-    // Both counters in flight together.
-    const int len_before = adv.counter != nullptr
-        ? __hip_atomic_fetch_add(adv.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-        : 0;
-    const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int len_before = adv.counter != nullptr ? count_arrival(adv.counter) : 0;
+    const int before = count_arrival(counter);
     is_last = before == nchunks - 1;
-    if (is_last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (is_last) rearm(counter);
     finish_advance(adv, len_before);
   }
   __syncthreads();
@@ -343,7 +342,15 @@ constexpr float kRescaleThreshold = 8.0f;
 
 // MK: mask element type (0 = no mask, else an slc_dtype tag + 1), a template
 // parameter so the load path has no data-dependent branches.
-template <typename T, int D, int MK, bool L64, bool ROPE>
+// EXACT: the reference executor's softmax order -- the probabilities are
+// normalised in fp32 and then rounded to the I/O dtype for the P.V product
+// (execution.py:319-327: softmax(...).to(query.dtype) then matmul) -- instead
+// of rounding the running (unnormalised) probabilities.  One chunk per
+// (batch, kv-head): pass 1 streams K, keeps each lane's rounded scores in LDS
+// (dynamic shared memory, 1 KB per 32-token tile) and forms the row max and
+// sum; pass 2 streams V and weighs it with the normalised, rounded
+// probabilities.  K and V are each read once.
+template <typename T, int D, int MK, bool L64, bool ROPE, bool EXACT>
 __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     const T* __restrict__ query, const T* __restrict__ key_buffer,
     const T* __restrict__ value_buffer, const void* __restrict__ lengths,
@@ -360,6 +367,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   constexpr int DB = D / 16;            // 16-dim output blocks
 
   __shared__ __attribute__((aligned(16))) unsigned char smem[Layout::kBytes];
+  extern __shared__ uint4 score_lds[];  // EXACT: [tile][lane] rounded scores
 
   const int chunk = blockIdx.x;
   const int kvh = blockIdx.y;
@@ -470,7 +478,9 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   // scores) through buffer resources bounded at the chunk end.  K and V use
   // the same lane layout: lane (row c, k-slice g) of 16-row block j holds
   // dims kk*32+8g..+7 of token t0+16j+c.
-  auto load_tile = [&](int t0, Tile& tile, int bound) {
+  // Which: 3 = K and V, 1 = K only, 2 = V only (the EXACT passes).
+  auto load_tile = [&](int t0, Tile& tile, int bound, auto which) {
+    constexpr int kWhich = decltype(which)::value;
     const int rows = bound - t0;
     const int nbytes = rows > 0 ? rows * row_bytes : 0;
     const int64_t shift = static_cast<int64_t>(t0) * row_bytes;
@@ -480,8 +490,8 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
-        tile.k[j][kk] = buffer_load16(rk, koff[j] + kk * 64);
-        tile.v[j][kk] = buffer_load16(rv, koff[j] + kk * 64);
+        if constexpr ((kWhich & 1) != 0) tile.k[j][kk] = buffer_load16(rk, koff[j] + kk * 64);
+        if constexpr ((kWhich & 2) != 0) tile.v[j][kk] = buffer_load16(rv, koff[j] + kk * 64);
       }
     if constexpr (MK != 0) {
       const __amdgpu_buffer_rsrc_t rm =
@@ -561,8 +571,8 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     store_new_row();
     if (tid < groups) {
       const int64_t p = (b * q_heads + kvh * groups + tid) * nchunks + chunk;
-      publish(part_ml + 2 * p, -INFINITY, counters);
-      publish(part_ml + 2 * p + 1, 0.0f, counters);
+      publish(part_ml + 2 * p, -INFINITY);
+      publish(part_ml + 2 * p + 1, 0.0f);
     }
     if (counters != nullptr)
       merge_if_last<T, D>(part_o, part_ml, output, counters, smem, b, kvh, q_heads, kv_heads,
@@ -571,9 +581,13 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   }
   const int chunk_end = min(chunk_start + chunk_tokens, end);
 
+  using KV = std::integral_constant<int, 3>;
+  using KOnly = std::integral_constant<int, 1>;
+  using VOnly = std::integral_constant<int, 2>;
+  using First = std::conditional_t<EXACT, KOnly, KV>;
   Tile ta, tb;
-  load_tile(t_first, ta, chunk_end);
-  load_tile(t_first + kStride, tb, chunk_end);
+  load_tile(t_first, ta, chunk_end, First{});
+  load_tile(t_first + kStride, tb, chunk_end, First{});
   if constexpr (ROPE) {
     rope_slices<T, KK>(qraw, cs, sn);
 #pragma unroll
@@ -581,9 +595,11 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     store_new_row();
   }
 
-  auto compute_tile = [&](int t0, const Tile& tile) {
-    // S^T tile: two 16-token MFMA blocks; lane holds tokens 16j+4g+r, head c.
-    float s[8];
+  // S^T tile: two 16-token MFMA blocks; lane holds tokens 16j+4g+r, head c.
+  // q.k and its scaling are materialised in the tensor dtype, as the
+  // reference's bf16 matmul and multiply do (r); softmax stays fp32, in log2
+  // units (s = r * log2 e + mask * log2 e; -inf past the chunk end).
+  auto tile_scores = [&](int t0, const Tile& tile, float (&s)[8], u16x8& r_bits) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       f32x4_t st = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -591,14 +607,17 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
       for (int kk = 0; kk < KK; ++kk) st = M::run(as_vec<T>(tile.k[j][kk]), qv[kk], st);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        // q.k and its scaling are materialised in the tensor dtype, as the
-        // reference's bf16 matmul and multiply do; softmax stays fp32.
-        float v = slc::round_to<T>(slc::round_to<T>(st[r]) * scale) * kLog2e;
+        const float rounded = slc::round_to<T>(slc::round_to<T>(st[r]) * scale);
+        r_bits.v[4 * j + r] = bits_of<T>(rounded);
+        float v = rounded * kLog2e;
         if constexpr (MK != 0) v += tile.mk[4 * j + r];
         s[4 * j + r] = t0 + 16 * j + 4 * g + r < chunk_end ? v : -INFINITY;
       }
     }
-
+  };
+  // Running max / sum (and the accumulator, when there is one) with a lazy
+  // rescale.
+  auto update_max = [&](const float (&s)[8]) {
     float mx = s[0];
 #pragma unroll
     for (int i = 1; i < 8; ++i) mx = fmaxf(mx, s[i]);
@@ -607,26 +626,18 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
       const float m_new = fmaxf(m_run, mx);
       const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.0f : m_new));
       l_run *= alpha;
+      if constexpr (!EXACT) {
 #pragma unroll
-      for (int db = 0; db < DB; ++db) acc[db] = acc[db] * alpha;
+        for (int db = 0; db < DB; ++db) acc[db] = acc[db] * alpha;
+      }
       m_run = m_new;
     }
-    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-    u16x8 pbits;
-    float psum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float p = fast_exp2(s[i] - m_use);
-      psum += p;
-      pbits.v[i] = bits_of<T>(p);
-    }
-    l_run += psum;
-    const typename M::vec pv = __builtin_bit_cast(typename M::vec, pbits);
-
-    // O^T[dim, head] += V^T . P^T.  V^T is produced in registers: V rows times
-    // a 0/1 selector (one MFMA per 16 tokens x 16 dims) land as lane
-    // (dim c, tokens 4g..4g+3) -- exactly the token slots of the P operand.
-    // The products are exact (x * 1 + 0), so converting back is lossless.
+  };
+  // O^T[dim, head] += V^T . P^T.  V^T is produced in registers: V rows times
+  // a 0/1 selector (one MFMA per 16 tokens x 16 dims) land as lane
+  // (dim c, tokens 4g..4g+3) -- exactly the token slots of the P operand.
+  // The products are exact (x * 1 + 0), so converting back is lossless.
+  auto accumulate_pv = [&](const Tile& tile, const typename M::vec& pv) {
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
       const f32x4_t zero = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -640,6 +651,53 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
       }
       acc[db] = M::run(__builtin_bit_cast(typename M::vec, a), pv, acc[db]);
     }
+  };
+
+  auto compute_tile = [&](int t0, const Tile& tile) {
+    float s[8];
+    u16x8 r_bits;
+    tile_scores(t0, tile, s, r_bits);
+    update_max(s);
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+    u16x8 pbits;
+    float psum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float p = fast_exp2(s[i] - m_use);
+      psum += p;
+      pbits.v[i] = bits_of<T>(p);
+    }
+    l_run += psum;
+    accumulate_pv(tile, __builtin_bit_cast(typename M::vec, pbits));
+  };
+  // EXACT pass 1: scores to LDS, running max and sum (no accumulator).
+  auto score_tile = [&](int t0, const Tile& tile) {
+    float s[8];
+    u16x8 r_bits;
+    tile_scores(t0, tile, s, r_bits);
+    score_lds[(t0 / kTile) * 64 + lane] = __builtin_bit_cast(uint4, r_bits);
+    update_max(s);
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+    float psum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) psum += fast_exp2(s[i] - m_use);
+    l_run += psum;
+  };
+  // EXACT pass 2: p = exp2(s - m - log2 l) = exp(score - max) / sum, rounded.
+  float norm_shift = 0.0f;
+  auto weigh_tile = [&](int t0, const Tile& tile) {
+    const u16x8 r_bits = __builtin_bit_cast(u16x8, score_lds[(t0 / kTile) * 64 + lane]);
+    u16x8 pbits;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      T rb;
+      rb.bits = r_bits.v[i];
+      float v = slc::to_f32(rb) * kLog2e;
+      if constexpr (MK != 0) v += tile.mk[i];
+      const bool valid = t0 + 16 * (i >> 2) + 4 * g + (i & 3) < chunk_end;
+      pbits.v[i] = valid ? bits_of<T>(fast_exp2(v - norm_shift)) : 0;
+    }
+    accumulate_pv(tile, __builtin_bit_cast(typename M::vec, pbits));
   };
 
   // Two tiles in flight per wave: while tile A is consumed, tile B (issued
@@ -663,27 +721,56 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
       }
     }
   };
-  for (int t0 = t_first; t0 < chunk_end; t0 += 2 * kStride) {
-    patch(t0, ta);
-    compute_tile(t0, ta);
-    load_tile(t0 + 2 * kStride, ta, chunk_end);
-    if (t0 + kStride >= chunk_end) break;
-    patch(t0 + kStride, tb);
-    compute_tile(t0 + kStride, tb);
-    load_tile(t0 + 3 * kStride, tb, chunk_end);
-  }
+  auto sweep = [&](auto body, auto which) {
+    for (int t0 = t_first; t0 < chunk_end; t0 += 2 * kStride) {
+      patch(t0, ta);
+      body(t0, ta);
+      load_tile(t0 + 2 * kStride, ta, chunk_end, which);
+      if (t0 + kStride >= chunk_end) break;
+      patch(t0 + kStride, tb);
+      body(t0 + kStride, tb);
+      load_tile(t0 + 3 * kStride, tb, chunk_end, which);
+    }
+  };
 
-  // Finish the per-lane partial sums of l over the 4 lane groups.
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
-
-  __syncthreads();  // V tiles are dead; reuse LDS for the cross-wave merge.
   float* sm_m = reinterpret_cast<float*>(smem);
   float* sm_l = sm_m + kWaves * kMaxGroups;
   float* sm_o = sm_l + kWaves * kMaxGroups;  // [wave][head][D]
-  if (g == 0) {
-    sm_m[wave * kMaxGroups + c] = m_run;
-    sm_l[wave * kMaxGroups + c] = l_run;
+  if constexpr (EXACT) {
+    // Pass 1, then the row max and sum over the 4 lane groups and the waves.
+    sweep(score_tile, KOnly{});
+    load_tile(t_first, ta, chunk_end, VOnly{});  // pass 2's first tiles fly
+    load_tile(t_first + kStride, tb, chunk_end, VOnly{});  // during the combine
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+    if (g == 0) {
+      sm_m[wave * kMaxGroups + c] = m_run;
+      sm_l[wave * kMaxGroups + c] = l_run;
+    }
+    __syncthreads();
+    float mmax = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mmax = fmaxf(mmax, sm_m[w * kMaxGroups + c]);
+    const float mu = mmax == -INFINITY ? 0.0f : mmax;
+    float lsum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w)
+      lsum += fast_exp2(sm_m[w * kMaxGroups + c] - mu) * sm_l[w * kMaxGroups + c];
+    // An empty row (no token, or all of them masked to -inf) has sum 0 and
+    // gives NaN, as the reference's softmax over an all -inf row does.
+    norm_shift = lsum > 0.0f ? mu + __builtin_amdgcn_logf(lsum) : __builtin_nanf("");
+    sweep(weigh_tile, VOnly{});
+    __syncthreads();  // the LDS combine area is reused below
+  } else {
+    sweep(compute_tile, First{});
+    // Finish the per-lane partial sums of l over the 4 lane groups.
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+    __syncthreads();  // V tiles are dead; reuse LDS for the cross-wave merge.
+    if (g == 0) {
+      sm_m[wave * kMaxGroups + c] = m_run;
+      sm_l[wave * kMaxGroups + c] = l_run;
+    }
   }
 #pragma unroll
   for (int db = 0; db < DB; ++db)
@@ -695,6 +782,19 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   for (int idx = tid; idx < groups * D; idx += kThreads) {
     const int head = idx / D;
     const int d = idx % D;
+    const int qh = kvh * groups + head;
+    if constexpr (EXACT) {
+      // The waves' sums of normalised terms add up in wave order; a row with
+      // no weight at all (sum 0) is NaN, as in the reference's softmax.
+      float osum = 0.0f, lsum = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        osum += sm_o[(w * kMaxGroups + head) * D + d];
+        lsum += sm_l[w * kMaxGroups + head];
+      }
+      output[b * o_sb + qh * o_sh + d] = slc::from_f32<T>(lsum > 0.0f ? osum : __builtin_nanf(""));
+      continue;
+    }
     float mmax = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) mmax = fmaxf(mmax, sm_m[w * kMaxGroups + head]);
@@ -706,24 +806,21 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
       lsum += f * sm_l[w * kMaxGroups + head];
       osum += f * sm_o[(w * kMaxGroups + head) * D + d];
     }
-    const int qh = kvh * groups + head;
     if (nchunks == 1) {
       output[b * o_sb + qh * o_sh + d] = slc::from_f32<T>(osum / lsum);
     } else {
       const int64_t p = (b * q_heads + qh) * nchunks + chunk;
-      publish(part_o + p * D + d, osum, counters);
+      publish(part_o + p * D + d, osum);
       if (d == 0) {
-        publish(part_ml + 2 * p, mmax, counters);
-        publish(part_ml + 2 * p + 1, lsum, counters);
+        publish(part_ml + 2 * p, mmax);
+        publish(part_ml + 2 * p + 1, lsum);
       }
     }
   }
   if constexpr (ROPE) {
     // One chunk: no merge to carry the advance.  Every wave read the length
     // before the combine's barriers, so the count may be bumped now.
-    if (nchunks == 1 && tid == 0)
-      finish_advance(adv, __hip_atomic_fetch_add(adv.counter, 1, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT));
+    if (nchunks == 1 && tid == 0) finish_advance(adv, count_arrival(adv.counter));
   }
   if (nchunks > 1 && counters != nullptr) {
     __syncthreads();  // the merge reuses the LDS
@@ -799,7 +896,10 @@ __global__ __launch_bounds__(256) void decode_attention_merge_kernel(
 // Any dtype / head_dim <= 256 / any group size: one workgroup per
 // (batch, query head), each wave takes every 4th token and reduces q.k with
 // shuffles.  Used for fp32 and for shapes the MFMA kernel does not cover.
-template <typename T, int NI>
+// EXACT: the reference's softmax order (normalise, round, then P.V) in two
+// passes over the keys: the first forms the row max and sum, the second
+// recomputes each score and weighs V with its normalised, rounded probability.
+template <typename T, int NI, bool EXACT>
 __global__ __launch_bounds__(256) void decode_attention_generic_kernel(
     const T* __restrict__ query, const T* __restrict__ key_buffer,
     const T* __restrict__ value_buffer, const void* __restrict__ lengths,
@@ -831,7 +931,9 @@ __global__ __launch_bounds__(256) void decode_attention_generic_kernel(
   float m_run = -INFINITY, l_run = 0.0f;
   const T* kbase = key_buffer + b * kv_sb + kvh * kv_sh;
   const T* vbase = value_buffer + b * kv_sb + kvh * kv_sh;
-  for (int64_t t = wave; t < end; t += kGenericWaves) {
+  // Score of token t in log2 units.  16-bit dtypes materialise q.k and its
+  // scaling like the reference's matmul and multiply; fp32 keeps them exact.
+  auto score = [&](int64_t t) {
     float dot = 0.0f;
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
@@ -839,26 +941,48 @@ __global__ __launch_bounds__(256) void decode_attention_generic_kernel(
       if (d < head_dim) dot += q[i] * slc::to_f32(kbase[t * kv_ss + d]);
     }
     dot = slc::wave_sum(dot);
-    // 16-bit dtypes materialise q.k and its scaling like the reference's
-    // matmul and multiply; fp32 keeps them exact.
-    float s = (sizeof(T) == 2 ? slc::round_to<T>(slc::round_to<T>(dot) * scale) : dot * scale) * kLog2e;
-    if (mask != nullptr) s += slc::load_as_f32(mask, b * m_sb + t * m_ss, mask_dtype) * kLog2e;
-    const float m_new = fmaxf(m_run, s);
+    float sc = (sizeof(T) == 2 ? slc::round_to<T>(slc::round_to<T>(dot) * scale) : dot * scale) * kLog2e;
+    if (mask != nullptr) sc += slc::load_as_f32(mask, b * m_sb + t * m_ss, mask_dtype) * kLog2e;
+    return sc;
+  };
+  for (int64_t t = wave; t < end; t += kGenericWaves) {
+    const float sc = score(t);
+    const float m_new = fmaxf(m_run, sc);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
     const float alpha = exp2f(m_run - m_use);
-    const float p = exp2f(s - m_use);
+    const float p = exp2f(sc - m_use);
     l_run = l_run * alpha + p;
+    if constexpr (!EXACT) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int d = lane + 64 * i;
-      const float v = d < head_dim ? slc::to_f32(vbase[t * kv_ss + d]) : 0.0f;
-      acc[i] = acc[i] * alpha + p * v;
+      for (int i = 0; i < NI; ++i) {
+        const int d = lane + 64 * i;
+        const float v = d < head_dim ? slc::to_f32(vbase[t * kv_ss + d]) : 0.0f;
+        acc[i] = acc[i] * alpha + p * v;
+      }
     }
     m_run = m_new;
   }
   if (lane == 0) {
     sm_m[wave] = m_run;
     sm_l[wave] = l_run;
+  }
+  if constexpr (EXACT) {
+    __syncthreads();
+    float mmax = -INFINITY;
+    for (int w = 0; w < kGenericWaves; ++w) mmax = fmaxf(mmax, sm_m[w]);
+    const float mu = mmax == -INFINITY ? 0.0f : mmax;
+    float lsum = 0.0f;
+    for (int w = 0; w < kGenericWaves; ++w) lsum += exp2f(sm_m[w] - mu) * sm_l[w];
+    const float shift = lsum > 0.0f ? mu + log2f(lsum) : __builtin_nanf("");
+    for (int64_t t = wave; t < end; t += kGenericWaves) {
+      const float p = slc::round_to<T>(exp2f(score(t) - shift));
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int d = lane + 64 * i;
+        const float v = d < head_dim ? slc::to_f32(vbase[t * kv_ss + d]) : 0.0f;
+        acc[i] += p * v;
+      }
+    }
   }
 #pragma unroll
   for (int i = 0; i < NI; ++i) sm_o[wave][lane + 64 * i] = acc[i];
@@ -871,9 +995,10 @@ __global__ __launch_bounds__(256) void decode_attention_generic_kernel(
     for (int w = 0; w < kGenericWaves; ++w) {
       const float f = exp2f(sm_m[w] - mu);
       lsum += f * sm_l[w];
-      osum += f * sm_o[w][d];
+      osum += EXACT ? sm_o[w][d] : f * sm_o[w][d];
     }
-    output[b * o_sb + h * o_sh + d] = slc::from_f32<T>(osum / lsum);
+    const float out = EXACT ? (lsum > 0.0f ? osum : __builtin_nanf("")) : osum / lsum;
+    output[b * o_sb + h * o_sh + d] = slc::from_f32<T>(out);
   }
 }
 
@@ -911,62 +1036,58 @@ int64_t choose_chunk(int64_t batch, int64_t kv_heads, int64_t mask_len,
   return chunk;
 }
 
-// Workspace layout of the split-sequence path:
-//   float part_o[batch * q_heads * nchunks * D]
-//   float part_ml[batch * q_heads * nchunks * 2]
+// Caller-owned device memory of a call:
+//   counters (zero before first use; every call leaves them zero again):
+//     int merge[batch * kv_heads]       split-merge arrival counters
+//     int advance[batch]                RoPE variant's length-advance counters
+//   workspace (scratch, no initial contents needed):
+//     float part_o[batch * q_heads * nchunks * D]
+//     float part_ml[batch * q_heads * nchunks * 2]
+// The counters are a separate array so that a call's partials can never land
+// where a later call (of another shape) keeps its counters.
+int64_t counter_count(int64_t batch, int64_t kv_heads) { return batch * kv_heads + batch; }
+int64_t partial_bytes(int64_t batch, int64_t q_heads, int64_t head_dim, int64_t nchunks) {
+  return nchunks > 1 ? batch * q_heads * nchunks * (head_dim + 2) * 4 : 0;
+}
+
+// Longest sequence (mask length) the EXACT MFMA kernel holds in LDS: 1 KB of
+// rounded scores per 32 tokens next to the static combine area.
+int64_t exact_max_tokens(int64_t head_dim) {
+  return head_dim == 64 ? 4096 : head_dim == 128 ? 2048 : 0;
+}
 
 #ifndef SLC_DECODE_FUSED_MERGE
 #define SLC_DECODE_FUSED_MERGE 1
 #endif
 
-// Counter region of a stream for the in-kernel merge: the first
-// kCounterRegions distinct streams each get one (calls on one stream run in
-// order, so they never share counters concurrently); later streams use the
-// separate merge kernel.
-int counter_region(hipStream_t stream) {
-  static std::mutex lock;
-  static hipStream_t owners[kCounterRegions];
-  static int used = 0;
-  std::lock_guard<std::mutex> guard(lock);
-  for (int i = 0; i < used; ++i)
-    if (owners[i] == stream) return i;
-  if (used == kCounterRegions) return -1;
-  owners[used] = stream;
-  return used++;
-}
-
-// Device address of a region's counters on the current device (each device
-// holds its own copy of the static array), or nullptr if it cannot be found.
-// advance: the length-advance counters instead of the merge counters.
-int* merge_counters(int region, bool advance = false) {
-  static std::mutex lock;
-  static int* base[2][64] = {};
-  int device = 0;
-  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return nullptr;
-  std::lock_guard<std::mutex> guard(lock);
-  int*& slot = base[advance ? 1 : 0][device];
-  if (slot == nullptr) {
-    void* address = nullptr;
-    const hipError_t e = advance
-        ? hipGetSymbolAddress(&address, HIP_SYMBOL(g_advance_counters))
-        : hipGetSymbolAddress(&address, HIP_SYMBOL(g_merge_counters));
-    if (e != hipSuccess) return nullptr;
-    slot = static_cast<int*>(address);
-  }
-  return slot + static_cast<int64_t>(region) * kCounterPairs;
-}
-
 // Status of a fused call the kernels cannot take (nothing was launched).
 constexpr int kUnsupported = -2;
+
+template <typename T, int D, int MK, bool L64, bool ROPE, bool EXACT>
+hipError_t exact_lds_limit(int bytes) {
+  // Dynamic LDS above the 64 KB default needs the kernel's opt-in (once per
+  // instantiation; the attribute is per function).
+  static std::once_flag once;
+  static hipError_t status = hipSuccess;
+  std::call_once(once, [&] {
+    status = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&decode_attention_mfma_kernel<T, D, MK, L64, ROPE, EXACT>),
+        hipFuncAttributeMaxDynamicSharedMemorySize,
+        static_cast<int>(slc_host::ceil_div(exact_max_tokens(D), kTile) * 1024));
+  });
+  (void)bytes;
+  return status;
+}
 
 template <typename T, int D>
 int launch_mfma(const void* query, const void* kb, const void* vb,
                 const void* lengths, int lengths_dtype, const void* mask,
-                int mask_dtype, void* output, void* workspace, int64_t batch,
+                int mask_dtype, void* output, void* workspace, int* counters, int64_t batch,
                 int64_t q_heads, int64_t kv_heads, int64_t capacity,
                 int64_t mask_len, const int64_t* st, float scale,
-                int64_t chunk, int64_t nchunks, hipStream_t stream,
+                int64_t chunk, int64_t nchunks, bool exact, hipStream_t stream,
                 const RopeStore* rope = nullptr) {
+  int* advance = counters + batch * kv_heads;
   float* part_o = nullptr;
   float* part_ml = nullptr;
   if (nchunks > 1) {
@@ -976,36 +1097,42 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
   const int groups = static_cast<int>(q_heads / kv_heads);
   const dim3 grid(static_cast<unsigned>(nchunks), static_cast<unsigned>(kv_heads),
                   static_cast<unsigned>(batch));
-  // Merge inside the split kernel when this stream has a counter region and
-  // the chunk weights fit the kernel's LDS; else the separate merge kernel.
-  int* counters = nullptr;
-  if (nchunks > 1 && SLC_DECODE_FUSED_MERGE && batch * kv_heads <= kCounterPairs &&
-      (2 * groups * nchunks + groups) * 4 <= SharedLayout<T, D>::kBytes) {
-    const int region = counter_region(stream);
-    if (region >= 0) counters = merge_counters(region);
+  // Merge inside the split kernel when the chunk weights fit the kernel's
+  // LDS; else the separate merge kernel.
+  int* merge = nchunks > 1 && SLC_DECODE_FUSED_MERGE &&
+                       (2 * groups * nchunks + groups) * 4 <= SharedLayout<T, D>::kBytes
+                   ? counters
+                   : nullptr;
+  const size_t dyn_lds =
+      exact ? static_cast<size_t>(slc_host::ceil_div(std::min(mask_len, capacity), kTile) * 1024) : 0;
+#define SLC_MFMA_K(MK, L64, ROPE, EX)                                                      \
+  do {                                                                                     \
+    if (EX && exact_lds_limit<T, D, MK, L64, ROPE, EX>(static_cast<int>(dyn_lds)) != hipSuccess) \
+      return slc_host::check_launch("slc_hip_decode_attention(exact LDS opt-in)");         \
+    hipLaunchKernelGGL((decode_attention_mfma_kernel<T, D, MK, L64, ROPE, EX>), grid,     \
+                       dim3(kThreads), dyn_lds, stream, static_cast<const T*>(query),      \
+                       static_cast<const T*>(kb), static_cast<const T*>(vb), lengths,      \
+                       lengths_dtype, mask, mask_dtype, static_cast<T*>(output), part_o,   \
+                       part_ml, static_cast<int>(q_heads), static_cast<int>(kv_heads),     \
+                       groups, capacity, mask_len, st[0], st[1], st[2],                    \
+                       static_cast<int>(st[3]), st[4], st[5], static_cast<int>(st[6]),     \
+                       st[7], st[8], scale, static_cast<int>(chunk),                       \
+                       static_cast<int>(nchunks), merge, rs);                              \
+  } while (0)
+#define SLC_MFMA_ORDER(MK, L64, ROPE)     \
+  if (exact) {                            \
+    SLC_MFMA_K(MK, L64, ROPE, true);      \
+  } else {                                \
+    SLC_MFMA_K(MK, L64, ROPE, false);     \
   }
-#define SLC_MFMA_K(MK, L64, ROPE)                                             \
-  hipLaunchKernelGGL((decode_attention_mfma_kernel<T, D, MK, L64, ROPE>), grid,           \
-                     dim3(kThreads), 0, stream, static_cast<const T*>(query),           \
-                     static_cast<const T*>(kb), static_cast<const T*>(vb),    \
-                     lengths, lengths_dtype, mask, mask_dtype,                \
-                     static_cast<T*>(output), part_o, part_ml,                \
-                     static_cast<int>(q_heads), static_cast<int>(kv_heads),   \
-                     groups, capacity, mask_len, st[0], st[1], st[2],         \
-                     static_cast<int>(st[3]), st[4], st[5],                   \
-                     static_cast<int>(st[6]), st[7], st[8], scale,            \
-                     static_cast<int>(chunk), static_cast<int>(nchunks), counters, rs)
   RopeStore rs{};
   if (rope != nullptr) {
     // The advance rides on the in-kernel merge (or, with one chunk, on the
     // workgroup's end); int64 lengths only.
-    const int region = counter_region(stream);
-    int* advance = region >= 0 && batch <= kCounterPairs ? merge_counters(region, true) : nullptr;
-    if (advance == nullptr || lengths_dtype != SLC_I64 || (nchunks > 1 && counters == nullptr))
-      return kUnsupported;
+    if (lengths_dtype != SLC_I64 || (nchunks > 1 && merge == nullptr)) return kUnsupported;
     rs = *rope;
     rs.counters = advance;
-#define SLC_ROPE(MK) SLC_MFMA_K(MK, true, true)
+#define SLC_ROPE(MK) SLC_MFMA_ORDER(MK, true, true)
     if (mask == nullptr) {
       SLC_ROPE(0);
     } else if (mask_dtype == SLC_BF16) {
@@ -1019,11 +1146,11 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
     return slc_host::check_launch("slc_hip_rope_decode_attention");
   }
   slc_host::mark_kernel_begin(stream);
-#define SLC_MFMA(MK)                                                          \
-  if (lengths_dtype == SLC_I64) {                                             \
-    SLC_MFMA_K(MK, true, false);                                              \
-  } else {                                                                    \
-    SLC_MFMA_K(MK, false, false);                                             \
+#define SLC_MFMA(MK)                          \
+  if (lengths_dtype == SLC_I64) {             \
+    SLC_MFMA_ORDER(MK, true, false);          \
+  } else {                                    \
+    SLC_MFMA_ORDER(MK, false, false);         \
   }
   for (int rep = slc_host::timed_repeats(); rep > 0; --rep) {
     if (mask == nullptr) {
@@ -1037,10 +1164,11 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
     }
   }
 #undef SLC_MFMA
+#undef SLC_MFMA_ORDER
 #undef SLC_MFMA_K
   slc_host::mark_kernel_end(stream);
   int rc = slc_host::check_launch("slc_hip_decode_attention");
-  if (rc != SLC_OK || nchunks == 1 || counters != nullptr) return rc;
+  if (rc != SLC_OK || nchunks == 1 || merge != nullptr) return rc;
   hipLaunchKernelGGL((decode_attention_merge_kernel<T, D>),
                      dim3(static_cast<unsigned>(batch * kv_heads)), dim3(256), 0,
                      stream, part_o, part_ml, static_cast<T*>(output),
@@ -1054,19 +1182,25 @@ int launch_generic(const void* query, const void* kb, const void* vb,
                    const void* lengths, int lengths_dtype, const void* mask,
                    int mask_dtype, void* output, int64_t batch, int64_t q_heads,
                    int64_t kv_heads, int64_t head_dim, int64_t capacity,
-                   int64_t mask_len, const int64_t* st, float scale,
+                   int64_t mask_len, const int64_t* st, float scale, bool exact,
                    hipStream_t stream) {
   const int groups = static_cast<int>(q_heads / kv_heads);
   const dim3 grid(static_cast<unsigned>(batch * q_heads));
-#define SLC_GENERIC(NI)                                                        \
-  hipLaunchKernelGGL((decode_attention_generic_kernel<T, NI>), grid, dim3(256), \
-                     0, stream, static_cast<const T*>(query),                  \
-                     static_cast<const T*>(kb), static_cast<const T*>(vb),     \
-                     lengths, lengths_dtype, mask, mask_dtype,                 \
-                     static_cast<T*>(output), static_cast<int>(q_heads),       \
-                     groups, static_cast<int>(head_dim), capacity, mask_len,   \
-                     st[0], st[1], st[2], st[3], st[4], st[5], st[6], st[7],   \
+#define SLC_GENERIC_K(NI, EX)                                                          \
+  hipLaunchKernelGGL((decode_attention_generic_kernel<T, NI, EX>), grid, dim3(256),    \
+                     0, stream, static_cast<const T*>(query),                          \
+                     static_cast<const T*>(kb), static_cast<const T*>(vb),             \
+                     lengths, lengths_dtype, mask, mask_dtype,                         \
+                     static_cast<T*>(output), static_cast<int>(q_heads),               \
+                     groups, static_cast<int>(head_dim), capacity, mask_len,           \
+                     st[0], st[1], st[2], st[3], st[4], st[5], st[6], st[7],           \
                      st[8], scale)
+#define SLC_GENERIC(NI)          \
+  if (exact) {                   \
+    SLC_GENERIC_K(NI, true);     \
+  } else {                       \
+    SLC_GENERIC_K(NI, false);    \
+  }
   if (head_dim <= 64) {
     SLC_GENERIC(1);
   } else if (head_dim <= 128) {
@@ -1075,7 +1209,33 @@ int launch_generic(const void* query, const void* kb, const void* vb,
     SLC_GENERIC(4);
   }
 #undef SLC_GENERIC
+#undef SLC_GENERIC_K
   return slc_host::check_launch("slc_hip_decode_attention(generic)");
+}
+
+// Geometry of one call: which kernel, the split, and the workspace it needs.
+struct Plan {
+  bool mfma;
+  int64_t chunk, nchunks;
+  int64_t need;      // workspace bytes (partials)
+  int64_t counters;  // counter ints, 0 for the generic kernel
+};
+
+Plan plan_call(int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
+               int64_t head_dim, int64_t mask_len, int64_t split_tokens, bool exact) {
+  Plan p{false, 0, 1, 0, 0};
+  p.mfma = mfma_eligible(dtype, head_dim, q_heads / kv_heads) && mask_len > 0;
+  if (!p.mfma) return p;
+  if (exact) {
+    p.chunk = mask_len;
+    p.nchunks = 1;
+  } else {
+    p.chunk = choose_chunk(batch, kv_heads, mask_len, split_tokens);
+    p.nchunks = slc_host::ceil_div(mask_len, p.chunk);
+  }
+  p.need = partial_bytes(batch, q_heads, head_dim, p.nchunks);
+  p.counters = counter_count(batch, kv_heads);
+  return p;
 }
 
 }  // namespace
@@ -1087,28 +1247,39 @@ extern "C" int64_t slc_hip_decode_attention_workspace_size(
       q_heads % kv_heads != 0) {
     return 0;
   }
-  if (!mfma_eligible(dtype, head_dim, q_heads / kv_heads)) return 0;
-  const int64_t chunk = choose_chunk(batch, kv_heads, mask_len, split_tokens);
-  const int64_t nchunks = slc_host::ceil_div(mask_len, chunk);
-  if (nchunks <= 1) return 0;
-  return batch * q_heads * nchunks * (head_dim + 2) * static_cast<int64_t>(sizeof(float));
+  // The online split needs at least what the exact single-chunk form does.
+  return plan_call(dtype, batch, q_heads, kv_heads, head_dim, mask_len, split_tokens, false).need;
+}
+
+extern "C" int64_t slc_hip_decode_attention_counter_count(int64_t batch, int64_t kv_heads) {
+  return batch > 0 && kv_heads > 0 ? counter_count(batch, kv_heads) : 0;
+}
+
+extern "C" int64_t slc_hip_decode_attention_exact_max_tokens(int64_t head_dim, int dtype) {
+  if (dtype == SLC_BF16 || dtype == SLC_F16) {
+    if (head_dim == 64 || head_dim == 128) return exact_max_tokens(head_dim);
+  }
+  return INT64_MAX;  // the generic kernel takes any length in both orders
 }
 
 extern "C" int slc_hip_decode_attention(
     const void* query, const void* key_buffer, const void* value_buffer,
     const void* lengths, int lengths_dtype, const void* mask, int mask_dtype,
-    void* output, void* workspace, int64_t workspace_bytes, int dtype,
-    int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
-    int64_t capacity, int64_t mask_len, int64_t q_stride_b, int64_t q_stride_h,
-    int64_t kv_stride_b, int64_t kv_stride_s, int64_t kv_stride_h,
+    void* output, void* workspace, int64_t workspace_bytes, int* counters,
+    int64_t num_counters, int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
+    int64_t head_dim, int64_t capacity, int64_t mask_len, int64_t q_stride_b,
+    int64_t q_stride_h, int64_t kv_stride_b, int64_t kv_stride_s, int64_t kv_stride_h,
     int64_t mask_stride_b, int64_t mask_stride_s, int64_t out_stride_b,
-    int64_t out_stride_h, float scale, int64_t split_tokens, void* stream) {
+    int64_t out_stride_h, float scale, int64_t split_tokens, int softmax_order,
+    void* stream) {
   SLC_REQUIRE(slc_host::is_float_dtype(dtype),
               "slc_hip_decode_attention: bad dtype %d", dtype);
   SLC_REQUIRE(lengths_dtype == SLC_I64 || lengths_dtype == SLC_I32,
               "slc_hip_decode_attention: lengths must be int64 or int32");
   SLC_REQUIRE(mask == nullptr || slc_host::is_float_dtype(mask_dtype),
               "slc_hip_decode_attention: bad mask dtype %d", mask_dtype);
+  SLC_REQUIRE(softmax_order == SLC_SOFTMAX_ONLINE || softmax_order == SLC_SOFTMAX_EXACT,
+              "slc_hip_decode_attention: bad softmax order %d", softmax_order);
   SLC_REQUIRE(batch >= 0 && q_heads > 0 && kv_heads > 0 && head_dim > 0 &&
                   capacity > 0 && mask_len >= 0,
               "slc_hip_decode_attention: bad sizes");
@@ -1122,63 +1293,53 @@ extern "C" int slc_hip_decode_attention(
   if (batch == 0) return SLC_OK;
   SLC_REQUIRE(query && key_buffer && value_buffer && lengths && output,
               "slc_hip_decode_attention: null pointer");
-  const int64_t groups = q_heads / kv_heads;
+  const bool exact = softmax_order == SLC_SOFTMAX_EXACT;
   const int64_t st[9] = {q_stride_b,    q_stride_h,    kv_stride_b,
                          kv_stride_s,   kv_stride_h,   mask_stride_b,
                          mask_stride_s, out_stride_b,  out_stride_h};
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t ml = mask_len;
 
-  bool use_mfma = mfma_eligible(dtype, head_dim, groups) && ml > 0;
-  if (use_mfma) {
+  Plan plan = plan_call(dtype, batch, q_heads, kv_heads, head_dim, ml, split_tokens, exact);
+  if (plan.mfma) {
     // 16-byte vector loads need 8-element alignment of every row start.
     const uint64_t bits = reinterpret_cast<uintptr_t>(query) |
                           reinterpret_cast<uintptr_t>(key_buffer) |
                           reinterpret_cast<uintptr_t>(value_buffer);
     const int64_t strides = q_stride_b | q_stride_h | kv_stride_b |
                             kv_stride_s | kv_stride_h;
-    use_mfma = (bits & 15) == 0 && (strides & 7) == 0;
+    plan.mfma = (bits & 15) == 0 && (strides & 7) == 0;
     // Per-lane offsets inside one (batch, kv-head) slice are 32-bit.
     const int64_t mask_es = mask == nullptr ? 0 : slc_host::dtype_size(mask_dtype);
-    use_mfma = use_mfma && kv_stride_s > 0 && mask_stride_s >= 0 &&
-               capacity * kv_stride_s * 2 < (int64_t{1} << 31) &&
-               mask_len * mask_stride_s * mask_es < (int64_t{1} << 31) &&
-               capacity < (int64_t{1} << 30);
+    plan.mfma = plan.mfma && kv_stride_s > 0 && mask_stride_s >= 0 &&
+                capacity * kv_stride_s * 2 < (int64_t{1} << 31) &&
+                mask_len * mask_stride_s * mask_es < (int64_t{1} << 31) &&
+                capacity < (int64_t{1} << 30);
   }
-  if (use_mfma) {
-    const int64_t chunk = choose_chunk(batch, kv_heads, ml, split_tokens);
-    const int64_t nchunks = slc_host::ceil_div(ml, chunk);
-    const int64_t need =
-        nchunks > 1 ? batch * q_heads * nchunks * (head_dim + 2) * 4 : 0;
-    SLC_REQUIRE(nchunks <= 0x7fffffff, "slc_hip_decode_attention: too many chunks");
-    SLC_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need),
+  if (plan.mfma) {
+    SLC_REQUIRE(!exact || std::min(ml, capacity) <= exact_max_tokens(head_dim),
+                "slc_hip_decode_attention: the exact softmax order takes at most %lld tokens "
+                "at head_dim %lld, got a mask of %lld",
+                (long long)exact_max_tokens(head_dim), (long long)head_dim, (long long)ml);
+    SLC_REQUIRE(plan.nchunks <= 0x7fffffff, "slc_hip_decode_attention: too many chunks");
+    SLC_REQUIRE(plan.need == 0 || (workspace != nullptr && workspace_bytes >= plan.need),
                 "slc_hip_decode_attention: workspace of %lld bytes needed, got "
                 "%lld",
-                (long long)need, (long long)workspace_bytes);
+                (long long)plan.need, (long long)workspace_bytes);
+    SLC_REQUIRE(counters != nullptr && num_counters >= plan.counters,
+                "slc_hip_decode_attention: %lld counters needed, got %lld",
+                (long long)plan.counters, (long long)num_counters);
+#define SLC_DA_CALL(TT, DD)                                                                  \
+  launch_mfma<TT, DD>(query, key_buffer, value_buffer, lengths, lengths_dtype, mask,         \
+                      mask_dtype, output, workspace, counters, batch, q_heads, kv_heads,     \
+                      capacity, ml, st, scale, plan.chunk, plan.nchunks, exact, s)
     if (dtype == SLC_BF16) {
-      if (head_dim == 64)
-        return launch_mfma<slc::bf16_t, 64>(query, key_buffer, value_buffer,
-                                            lengths, lengths_dtype, mask,
-                                            mask_dtype, output, workspace, batch,
-                                            q_heads, kv_heads, capacity, ml, st,
-                                            scale, chunk, nchunks, s);
-      return launch_mfma<slc::bf16_t, 128>(query, key_buffer, value_buffer,
-                                           lengths, lengths_dtype, mask,
-                                           mask_dtype, output, workspace, batch,
-                                           q_heads, kv_heads, capacity, ml, st,
-                                           scale, chunk, nchunks, s);
+      if (head_dim == 64) return SLC_DA_CALL(slc::bf16_t, 64);
+      return SLC_DA_CALL(slc::bf16_t, 128);
     }
-    if (head_dim == 64)
-      return launch_mfma<slc::f16_t, 64>(query, key_buffer, value_buffer,
-                                         lengths, lengths_dtype, mask,
-                                         mask_dtype, output, workspace, batch,
-                                         q_heads, kv_heads, capacity, ml, st,
-                                         scale, chunk, nchunks, s);
-    return launch_mfma<slc::f16_t, 128>(query, key_buffer, value_buffer,
-                                        lengths, lengths_dtype, mask,
-                                        mask_dtype, output, workspace, batch,
-                                        q_heads, kv_heads, capacity, ml, st,
-                                        scale, chunk, nchunks, s);
+    if (head_dim == 64) return SLC_DA_CALL(slc::f16_t, 64);
+    return SLC_DA_CALL(slc::f16_t, 128);
+#undef SLC_DA_CALL
   }
   SLC_REQUIRE(batch * q_heads <= 0x7fffffff,
               "slc_hip_decode_attention: grid too large");
@@ -1187,18 +1348,18 @@ extern "C" int slc_hip_decode_attention(
       return launch_generic<float>(query, key_buffer, value_buffer, lengths,
                                    lengths_dtype, mask, mask_dtype, output,
                                    batch, q_heads, kv_heads, head_dim, capacity,
-                                   ml, st, scale, s);
+                                   ml, st, scale, exact, s);
     case SLC_BF16:
       return launch_generic<slc::bf16_t>(query, key_buffer, value_buffer,
                                          lengths, lengths_dtype, mask,
                                          mask_dtype, output, batch, q_heads,
                                          kv_heads, head_dim, capacity, ml, st,
-                                         scale, s);
+                                         scale, exact, s);
     default:
       return launch_generic<slc::f16_t>(query, key_buffer, value_buffer,
                                         lengths, lengths_dtype, mask, mask_dtype,
                                         output, batch, q_heads, kv_heads,
-                                        head_dim, capacity, ml, st, scale,
+                                        head_dim, capacity, ml, st, scale, exact,
                                         s);
   }
 }
@@ -1207,14 +1368,17 @@ extern "C" int slc_hip_rope_decode_attention(
     const void* query, const void* key, const void* value, const void* cosine,
     const void* sine, void* key_buffer, void* value_buffer, const int64_t* lengths,
     int64_t* lengths_out, int* overflow, const void* mask, int mask_dtype, void* output,
-    void* workspace, int64_t workspace_bytes, int dtype, int64_t batch, int64_t q_heads,
+    void* workspace, int64_t workspace_bytes, int* counters, int64_t num_counters, int dtype,
+    int64_t batch, int64_t q_heads,
     int64_t kv_heads, int64_t head_dim, int64_t capacity, int64_t mask_len, int64_t q_stride_b,
     int64_t q_stride_h, int64_t k_stride_b, int64_t k_stride_h, int64_t v_stride_b,
     int64_t v_stride_h, int64_t cos_stride_b, int64_t sin_stride_b, int64_t kv_stride_b,
     int64_t kv_stride_s, int64_t kv_stride_h, int64_t mask_stride_b, int64_t mask_stride_s,
-    int64_t out_stride_b, int64_t out_stride_h, float scale, void* stream) {
+    int64_t out_stride_b, int64_t out_stride_h, float scale, int softmax_order, void* stream) {
   SLC_REQUIRE(mask == nullptr || slc_host::is_float_dtype(mask_dtype),
               "slc_hip_rope_decode_attention: bad mask dtype %d", mask_dtype);
+  SLC_REQUIRE(softmax_order == SLC_SOFTMAX_ONLINE || softmax_order == SLC_SOFTMAX_EXACT,
+              "slc_hip_rope_decode_attention: bad softmax order %d", softmax_order);
   SLC_REQUIRE(batch >= 0 && q_heads > 0 && kv_heads > 0 && head_dim > 0 && capacity > 0 &&
                   mask_len >= 0 && q_heads % kv_heads == 0,
               "slc_hip_rope_decode_attention: bad sizes");
@@ -1224,9 +1388,11 @@ extern "C" int slc_hip_rope_decode_attention(
   SLC_REQUIRE(query && key && value && cosine && sine && key_buffer && value_buffer && lengths &&
                   lengths_out && output,
               "slc_hip_rope_decode_attention: null pointer");
+  const bool exact = softmax_order == SLC_SOFTMAX_EXACT;
   const int64_t groups = q_heads / kv_heads;
   // The fused kernel's cases; everything else is the caller's two-kernel path.
   if (!mfma_eligible(dtype, head_dim, groups) || mask_len <= 0) return kUnsupported;
+  if (exact && std::min(mask_len, capacity) > exact_max_tokens(head_dim)) return kUnsupported;
   const uint64_t bits =
       reinterpret_cast<uintptr_t>(query) | reinterpret_cast<uintptr_t>(key) |
       reinterpret_cast<uintptr_t>(value) | reinterpret_cast<uintptr_t>(cosine) |
@@ -1240,12 +1406,13 @@ extern "C" int slc_hip_rope_decode_attention(
       capacity * kv_stride_s * 2 >= (int64_t{1} << 31) ||
       mask_len * mask_stride_s * mask_es >= (int64_t{1} << 31) || capacity >= (int64_t{1} << 30))
     return kUnsupported;
-  const int64_t chunk = choose_chunk(batch, kv_heads, mask_len, 0);
-  const int64_t nchunks = slc_host::ceil_div(mask_len, chunk);
-  const int64_t need = nchunks > 1 ? batch * q_heads * nchunks * (head_dim + 2) * 4 : 0;
-  SLC_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need),
+  const Plan plan = plan_call(dtype, batch, q_heads, kv_heads, head_dim, mask_len, 0, exact);
+  SLC_REQUIRE(plan.need == 0 || (workspace != nullptr && workspace_bytes >= plan.need),
               "slc_hip_rope_decode_attention: workspace of %lld bytes needed, got %lld",
-              (long long)need, (long long)workspace_bytes);
+              (long long)plan.need, (long long)workspace_bytes);
+  SLC_REQUIRE(counters != nullptr && num_counters >= plan.counters,
+              "slc_hip_rope_decode_attention: %lld counters needed, got %lld",
+              (long long)plan.counters, (long long)num_counters);
   const int64_t st[9] = {q_stride_b,    q_stride_h,    kv_stride_b,  kv_stride_s, kv_stride_h,
                          mask_stride_b, mask_stride_s, out_stride_b, out_stride_h};
   RopeStore rope{key,          value,        cosine,       sine,         k_stride_b,
@@ -1254,8 +1421,8 @@ extern "C" int slc_hip_rope_decode_attention(
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define SLC_ROPE_CALL(TT, DD)                                                                  \
   launch_mfma<TT, DD>(query, key_buffer, value_buffer, lengths, SLC_I64, mask, mask_dtype,     \
-                      output, workspace, batch, q_heads, kv_heads, capacity, mask_len, st,     \
-                      scale, chunk, nchunks, s, &rope)
+                      output, workspace, counters, batch, q_heads, kv_heads, capacity,         \
+                      mask_len, st, scale, plan.chunk, plan.nchunks, exact, s, &rope)
   if (dtype == SLC_BF16) {
     if (head_dim == 64) return SLC_ROPE_CALL(slc::bf16_t, 64);
     return SLC_ROPE_CALL(slc::bf16_t, 128);

@@ -490,8 +490,8 @@ struct RopeStoreArgs {
 // lengths_out[b] = positions[b] + advance (in place is fine: every read
 // happened before the count completed), flags an advance past the capacity and
 // re-arms the counter.
-constexpr int kRopeStoreRegions = 16;
-__device__ int g_rope_store_counters[kRopeStoreRegions];
+// The counter is the first int of the caller's counter array (zero between
+// calls).
 
 template <typename T, int VEC>
 __global__ __launch_bounds__(256) void rope_kv_store_kernel(
@@ -499,7 +499,7 @@ __global__ __launch_bounds__(256) void rope_kv_store_kernel(
     const T* __restrict__ cosine, const T* __restrict__ sine, T* __restrict__ q_out,
     T* __restrict__ key_buffer, T* __restrict__ value_buffer,
     const int64_t* positions, int* __restrict__ overflow, RopeStoreArgs a,
-    int64_t total, int64_t* lengths_out, int64_t batch, int64_t advance, int region) {
+    int64_t total, int64_t* lengths_out, int64_t batch, int64_t advance, int* counter) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (gid < total) {
     const int64_t per_row = a.half / VEC;
@@ -556,12 +556,12 @@ __global__ __launch_bounds__(256) void rope_kv_store_kernel(
   __shared__ int is_last;
   __syncthreads();  // every thread of this workgroup has read its positions
   if (threadIdx.x == 0) {
-    const int before = __hip_atomic_fetch_add(&g_rope_store_counters[region], 1,
-                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Acquire-release: this workgroup's reads of the positions precede the
+    // count, and the last workgroup's length writes follow every arrival.
+    const int before =
+        __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     is_last = before == static_cast<int>(gridDim.x) - 1;
-    if (is_last)
-      __hip_atomic_store(&g_rope_store_counters[region], 0, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+    if (is_last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!is_last) return;
@@ -710,7 +710,8 @@ extern "C" int slc_hip_rope_kv_store(
     int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t tokens, int64_t head_dim,
     int64_t capacity, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh,
     int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t cos_sb, int64_t cos_st,
-    int64_t sin_sb, int64_t sin_st, int64_t qo_sb, int64_t qo_sh, int64_t qo_st, void* stream) {
+    int64_t sin_sb, int64_t sin_st, int64_t qo_sb, int64_t qo_sh, int64_t qo_st, int* counters,
+    int64_t num_counters, void* stream) {
   const char* what = "slc_hip_rope_kv_store";
   SLC_REQUIRE(slc_host::is_float_dtype(dtype), "%s: bad dtype %d", what, dtype);
   SLC_REQUIRE(batch >= 0 && q_heads >= 0 && kv_heads >= 0 && tokens >= 0 && head_dim > 0 &&
@@ -733,18 +734,17 @@ extern "C" int slc_hip_rope_kv_store(
   const int64_t total = batch * (q_heads + 2 * kv_heads) * tokens * per_row;
   const dim3 grid(static_cast<unsigned>(slc_host::ceil_div(total, 256)));
   const bool vec4 = (head_dim / 2) % 4 == 0;
-  // The advance rides on the store kernel when this stream owns a counter
-  // region; otherwise it is its own launch after the store.
-  int region = -1;
-  if (lengths_out != nullptr) region = slc_host::stream_region(slc_host::kRegionRopeStore, s);
-  int64_t* fused_out = region >= 0 ? lengths_out : nullptr;
+  // The advance rides on the store kernel when the caller gives a counter
+  // for its arrivals; otherwise it is its own launch after the store.
+  int* counter = counters != nullptr && num_counters >= 1 ? counters : nullptr;
+  int64_t* fused_out = counter != nullptr ? lengths_out : nullptr;
 #define SLC_RS(T, V)                                                                      \
   hipLaunchKernelGGL((rope_kv_store_kernel<T, V>), grid, dim3(256), 0, s,                \
                      static_cast<const T*>(query), static_cast<const T*>(key),           \
                      static_cast<const T*>(value), static_cast<const T*>(cosine),        \
                      static_cast<const T*>(sine), static_cast<T*>(query_out),            \
                      static_cast<T*>(key_buffer), static_cast<T*>(value_buffer), positions, \
-                     overflow, a, total, fused_out, batch, advance, region < 0 ? 0 : region)
+                     overflow, a, total, fused_out, batch, advance, counter)
   if (dtype == SLC_BF16) {
     if (vec4) SLC_RS(slc::bf16_t, 4); else SLC_RS(slc::bf16_t, 1);
   } else if (dtype == SLC_F16) {

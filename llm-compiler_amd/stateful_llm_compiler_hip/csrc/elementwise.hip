@@ -237,21 +237,33 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const T* __restrict__ logi
 
 // Wide rows: `segs` workgroups per row each reduce one segment and publish
 // (value, index) with agent-scope stores; the workgroup that completes the
-// row's count (per-stream counter region) combines the segments in order and
-// re-arms the counter.  Ties keep the lowest index because segments are
-// combined in index order with the same comparison.
-constexpr int kArgmaxRegions = 16;
-constexpr int kArgmaxRows = 256;
+// row's count combines the segments in order and re-arms the counter.  The
+// counters (zero between calls) and the segment results (scratch) are the
+// caller's (ArgmaxWorkspace); the add that counts is an agent-scope acquire-release,
+// so the publishing thread's stores precede the count and the combining
+// workgroup's loads follow every other arrival.  Ties keep the lowest index
+// because segments are combined in index order with the same comparison.
 constexpr int kArgmaxSegs = 64;
 constexpr int kArgmaxThreads = 256;
-__device__ int g_argmax_counters[kArgmaxRegions][kArgmaxRows];
-__device__ float g_argmax_value[kArgmaxRegions][kArgmaxRows * kArgmaxSegs];
-__device__ int64_t g_argmax_index[kArgmaxRegions][kArgmaxRows * kArgmaxSegs];
+struct ArgmaxWorkspace {
+  int* counters;   // [rows], zero between calls
+  float* value;    // [rows * kArgmaxSegs]
+  int64_t* index;  // [rows * kArgmaxSegs]
+};
+int64_t argmax_workspace_bytes(int64_t rows) { return rows * kArgmaxSegs * (4 + 8); }
+ArgmaxWorkspace argmax_workspace(void* base, int* counters, int64_t rows) {
+  char* p = static_cast<char*>(base);
+  ArgmaxWorkspace w;
+  w.counters = counters;
+  w.index = reinterpret_cast<int64_t*>(p);
+  w.value = reinterpret_cast<float*>(p + rows * kArgmaxSegs * 8);
+  return w;
+}
 
 template <typename T>
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_split_kernel(
     const T* __restrict__ logits, int64_t* __restrict__ out, int64_t cols, int64_t row_stride,
-    int vector_ok, int64_t seg_len, int region) {
+    int vector_ok, int64_t seg_len, ArgmaxWorkspace ws) {
   const int seg = blockIdx.x;
   const int segs = gridDim.x;
   const int r = blockIdx.y;
@@ -264,17 +276,13 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_split_kernel(
   __shared__ int is_last;
   if (threadIdx.x == 0) {
     const int slot = r * kArgmaxSegs + seg;
-    __hip_atomic_store(&g_argmax_value[region][slot], best, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&g_argmax_index[region][slot], best_i, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // published before counting
-    const int before = __hip_atomic_fetch_add(&g_argmax_counters[region][r], 1, __ATOMIC_RELAXED,
+    __hip_atomic_store(&ws.value[slot], best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&ws.index[slot], best_i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int before = __hip_atomic_fetch_add(&ws.counters[r], 1, __ATOMIC_ACQ_REL,
                                               __HIP_MEMORY_SCOPE_AGENT);
     is_last = before == segs - 1;
     if (is_last)
-      __hip_atomic_store(&g_argmax_counters[region][r], 0, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&ws.counters[r], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!is_last || threadIdx.x >= 64) return;
@@ -284,10 +292,8 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_split_kernel(
   int64_t i = INT64_MAX;
   for (int s = threadIdx.x; s < segs; s += 64) {
     const int slot = r * kArgmaxSegs + s;
-    const float sv = __hip_atomic_load(&g_argmax_value[region][slot], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-    const int64_t si = __hip_atomic_load(&g_argmax_index[region][slot], __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
+    const float sv = __hip_atomic_load(&ws.value[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int64_t si = __hip_atomic_load(&ws.index[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (argmax_better(sv, si, v, i)) {
       v = sv;
       i = si;
@@ -431,8 +437,14 @@ extern "C" int slc_hip_kv_advance(const int64_t* lengths_in, int64_t* lengths_ou
   return slc_host::check_launch("slc_hip_kv_advance");
 }
 
+extern "C" int64_t slc_hip_argmax_workspace_size(int64_t rows) {
+  return rows > 0 ? argmax_workspace_bytes(rows) : 0;
+}
+
 extern "C" int slc_hip_argmax(const void* logits, int64_t* output, int dtype, int64_t rows,
-                              int64_t cols, int64_t row_stride, void* stream) {
+                              int64_t cols, int64_t row_stride, void* workspace,
+                              int64_t workspace_bytes, int* counters, int64_t num_counters,
+                              void* stream) {
   SLC_REQUIRE(slc_host::is_float_dtype(dtype), "slc_hip_argmax: bad dtype %d", dtype);
   SLC_REQUIRE(rows >= 0 && cols > 0 && rows <= 0x7fffffff, "slc_hip_argmax: bad sizes");
   if (rows == 0) return SLC_OK;
@@ -441,20 +453,21 @@ extern "C" int slc_hip_argmax(const void* logits, int64_t* output, int dtype, in
   const int64_t es = slc_host::dtype_size(dtype);
   const int vector_ok = (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (row_stride * es) % 16 == 0;
   // Wide rows split over several workgroups per row (about one per CU in
-  // total, segments of at least 4096 elements) when the stream owns a
-  // counter region; else one 1024-thread workgroup per row.
+  // total, segments of at least 4096 elements) when the caller gives a
+  // workspace and counters; else one 1024-thread workgroup per row.
   const int64_t vec = 16 / es;
   int64_t segs = std::min<int64_t>(kArgmaxSegs, std::max<int64_t>(1, 256 / rows));
   segs = std::min<int64_t>(segs, std::max<int64_t>(1, cols / 4096));
-  const int region = segs > 1 && rows <= kArgmaxRows ? slc_host::stream_region(slc_host::kRegionArgmax, s) : -1;
-  if (region >= 0) {
+  if (segs > 1 && workspace != nullptr && workspace_bytes >= argmax_workspace_bytes(rows) &&
+      counters != nullptr && num_counters >= rows && rows <= 65535) {
+    const ArgmaxWorkspace ws = argmax_workspace(workspace, counters, rows);
     const int64_t seg_len = slc_host::ceil_div(slc_host::ceil_div(cols, segs), vec) * vec;
     segs = slc_host::ceil_div(cols, seg_len);
     const dim3 grid(static_cast<unsigned>(segs), static_cast<unsigned>(rows));
 #define SLC_ARGMAX_SPLIT(TT)                                                                  \
   hipLaunchKernelGGL((argmax_split_kernel<TT>), grid, dim3(kArgmaxThreads), 0, s,            \
                      static_cast<const TT*>(logits), output, cols, row_stride, vector_ok, seg_len, \
-                     region)
+                     ws)
     switch (dtype) {
       case SLC_BF16: SLC_ARGMAX_SPLIT(slc::bf16_t); break;
       case SLC_F16: SLC_ARGMAX_SPLIT(slc::f16_t); break;

@@ -291,8 +291,10 @@ __global__ __launch_bounds__(256) void prefill_attention_mfma_kernel(
   }
 }
 
-// Generic path: one wave per query row, shuffled dot products, online softmax.
-template <typename T, int NI>
+// Generic path: one wave per query row, shuffled dot products, online softmax
+// (EXACT: a first pass for the row max and sum, then the normalised
+// probabilities rounded to the I/O dtype weigh V, the reference's order).
+template <typename T, int NI, bool EXACT>
 __global__ __launch_bounds__(256) void prefill_attention_generic_kernel(
     const T* __restrict__ query, const T* __restrict__ key, const T* __restrict__ value,
     const void* __restrict__ mask, int mask_dtype, T* __restrict__ output, int tokens,
@@ -314,8 +316,7 @@ __global__ __launch_bounds__(256) void prefill_attention_generic_kernel(
     acc[i] = 0.0f;
   }
   const int key_end = causal ? qi + 1 : tokens;
-  float m_run = -INFINITY, l_run = 0.0f;
-  for (int kidx = 0; kidx < key_end; ++kidx) {
+  auto score = [&](int kidx) {
     float dot = 0.0f;
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
@@ -325,23 +326,45 @@ __global__ __launch_bounds__(256) void prefill_attention_generic_kernel(
     dot = slc::wave_sum(dot);
     float s = (sizeof(T) == 2 ? slc::round_to<T>(slc::round_to<T>(dot) * scale) : dot * scale) * kLog2e;
     if (mask != nullptr) s += slc::load_as_f32(mask, b * m_sb + qi * m_sq + kidx * m_sk, mask_dtype) * kLog2e;
+    return s;
+  };
+  float m_run = -INFINITY, l_run = 0.0f;
+  for (int kidx = 0; kidx < key_end; ++kidx) {
+    const float s = score(kidx);
     const float m_new = fmaxf(m_run, s);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
     const float alpha = exp2f(m_run - m_use);
     const float p = exp2f(s - m_use);
     l_run = l_run * alpha + p;
+    if constexpr (!EXACT) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int d = lane + 64 * i;
-      const float v = d < head_dim ? slc::to_f32(value[b * v_sb + kvh * v_sh + kidx * v_st + d]) : 0.0f;
-      acc[i] = acc[i] * alpha + p * v;
+      for (int i = 0; i < NI; ++i) {
+        const int d = lane + 64 * i;
+        const float v = d < head_dim ? slc::to_f32(value[b * v_sb + kvh * v_sh + kidx * v_st + d]) : 0.0f;
+        acc[i] = acc[i] * alpha + p * v;
+      }
     }
     m_run = m_new;
+  }
+  float inv = 1.0f / l_run;
+  if constexpr (EXACT) {
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+    const float shift = l_run > 0.0f ? m_use + log2f(l_run) : __builtin_nanf("");
+    for (int kidx = 0; kidx < key_end; ++kidx) {
+      const float p = slc::round_to<T>(exp2f(score(kidx) - shift));
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int d = lane + 64 * i;
+        const float v = d < head_dim ? slc::to_f32(value[b * v_sb + kvh * v_sh + kidx * v_st + d]) : 0.0f;
+        acc[i] += p * v;
+      }
+    }
+    inv = l_run > 0.0f ? 1.0f : __builtin_nanf("");
   }
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int d = lane + 64 * i;
-    if (d < head_dim) output[b * o_sb + h * o_sh + qi * o_st + d] = slc::from_f32<T>(acc[i] / l_run);
+    if (d < head_dim) output[b * o_sb + h * o_sh + qi * o_st + d] = slc::from_f32<T>(acc[i] * inv);
   }
 }
 
@@ -392,7 +415,14 @@ __device__ __forceinline__ uint2 lds_read_tr(const unsigned char* p) {
 // range, |score| < 2^-126, where the difference vanishes in score - max.)
 // fp16 keeps both roundings: its narrow exponent range makes subnormal
 // scaled scores common.
-template <typename T, int G, int MK, bool CAUSAL, bool POW2>
+// EXACT: the reference executor's softmax order (execution.py:720-739:
+// softmax in fp32, rounded to the I/O dtype, then P.V): two passes over the
+// key tiles.  Pass 1 forms each query row's max and sum (K and the mask only;
+// the producer's V loads of that pass read a zero-length range, so they move
+// no data but keep every tile's load count equal); pass 2 recomputes the
+// scores and weighs V with exp(score - max) / sum rounded to the I/O dtype,
+// so the rounding applies to the normalised probability as in the reference.
+template <typename T, int G, int MK, bool CAUSAL, bool POW2, bool EXACT>
 __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
     const T* __restrict__ query, const T* __restrict__ key, const T* __restrict__ value,
     const void* __restrict__ mask, T* __restrict__ output, int tokens, int kv_heads,
@@ -419,6 +449,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
   const float c_log2 = POW2 ? scale * kLog2e : kLog2e;
   const int key_end = CAUSAL ? min(q0 + kV2Queries, tokens) : tokens;
   const int ntiles = (key_end + kKeys - 1) / kKeys;
+  const int nsteps = EXACT ? 2 * ntiles : ntiles;  // ring steps (tile visits)
 
   if (wave == G) {
     // ---- producer ---------------------------------------------------------
@@ -430,14 +461,16 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
     const int q_rows = min(kV2Queries, tokens - q0);
     // Lane L of DMA instruction n fills LDS row 8n + L/8, chunk position L%8,
     // with the global 16-byte chunk (L%8) ^ (row & 7) of that row.
-    auto issue = [&](int tile, int stage) {
+    auto issue = [&](int step, int stage) {
       unsigned char* dst = ring[stage];
+      const int tile = EXACT && step >= ntiles ? step - ntiles : step;
+      const bool want_v = !EXACT || step >= ntiles;
       const int k0 = tile * kKeys;
-      const int rows = tile < ntiles ? min(kKeys, tokens - k0) : 0;
+      const int rows = step < nsteps ? min(kKeys, tokens - k0) : 0;
       const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + static_cast<int64_t>(k0) * k_st * 2,
                                                   rows > 0 ? (static_cast<int64_t>(rows) - 1) * k_st * 2 + kRowBytes : 0);
       const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + static_cast<int64_t>(k0) * v_st * 2,
-                                                  rows > 0 ? (static_cast<int64_t>(rows) - 1) * v_st * 2 + kRowBytes : 0);
+                                                  rows > 0 && want_v ? (static_cast<int64_t>(rows) - 1) * v_st * 2 + kRowBytes : 0);
 #pragma unroll
       for (int n = 0; n < kV2TileBytes / 1024; ++n) {
         const int row = 8 * n + lane / 8;
@@ -448,7 +481,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
       if constexpr (MK != 0) {
         // Mask rows are queries, chunks 8 keys; whole rows stay inside the
         // [T, T] plane (keys past T are masked as invalid anyway).
-        const int64_t bytes = tile < ntiles && q_rows > 0
+        const int64_t bytes = step < nsteps && q_rows > 0
                                   ? ((static_cast<int64_t>(q_rows) - 1) * m_sq + tokens - k0) * ME
                                   : 0;
         const __amdgpu_buffer_rsrc_t rm = make_rsrc(mbase + static_cast<int64_t>(k0) * ME, bytes);
@@ -463,7 +496,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
     };
 #pragma unroll
     for (int t = 0; t < kV2Stages - 1; ++t) issue(t, t);
-    for (int t = 0; t < ntiles; ++t) {
+    for (int t = 0; t < nsteps; ++t) {
       // Tile t landed: kStages - 2 later tiles (kOps each) may still fly.
       asm volatile("s_waitcnt vmcnt(%0)" ::"i"((kV2Stages - 2) * kOps) : "memory");
       __syncthreads();
@@ -513,10 +546,29 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
     tr_off[db] = row * kRowBytes + (((dim >> 3) ^ (row & 7)) << 4) + (dim & 7) * 2;
   }
   const int kv_off0 = c * kRowBytes;  // K operand row 16kb + c
+  // EXACT: per-lane partial row sums of pass 1 (the lane's 16 keys of each
+  // tile), then the exponent shift max + log2(sum) of pass 2.
+  float l_part[4] = {0.f, 0.f, 0.f, 0.f};
+  float shift[4] = {0.f, 0.f, 0.f, 0.f};
 
-  for (int t = 0; t < ntiles; ++t) {
-    __syncthreads();  // tile t is in ring[t % kStages]
-    const unsigned char* kt = ring[t % kV2Stages];
+  for (int step = 0; step < nsteps; ++step) {
+    __syncthreads();  // tile of this step is in ring[step % kStages]
+    const bool pass2 = EXACT && step >= ntiles;
+    const int t = pass2 ? step - ntiles : step;
+    if (EXACT && step == ntiles) {
+      // Pass 1 done: row sums over the 4 lane groups, then the shift.
+#pragma unroll
+      for (int qb = 0; qb < 4; ++qb) {
+        float l = l_part[qb];
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        const float m_use = m_run[qb] == -INFINITY ? 0.0f : m_run[qb];
+        // An empty row (every key masked) gives NaN, as the reference's
+        // softmax over an all -inf row does.
+        shift[qb] = l > 0.0f ? m_use + __builtin_amdgcn_logf(l) : __builtin_nanf("");
+      }
+    }
+    const unsigned char* kt = ring[step % kV2Stages];
     const unsigned char* vt = kt + kV2TileBytes;
     const unsigned char* mt = kt + 2 * kV2TileBytes;  // mask tile, rows = queries
     const int k0 = t * kKeys;
@@ -625,16 +677,36 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
           mx = fmaxf(mx, v);
         }
       }
+      if (pass2) continue;
       mx = slc::max_xor32(slc::max_xor16(mx));
       if constexpr (MK == 0) mx *= c_log2;
       if (__any(mx > m_run[qb] + kRescaleThreshold)) {
         const float m_new = fmaxf(m_run[qb], mx);
         const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - (m_new == -INFINITY ? 0.0f : m_new));
+        if constexpr (EXACT) {
+          l_part[qb] *= alpha;
+        } else {
 #pragma unroll
-        for (int db = 0; db < 5; ++db) acc[db][qb] = acc[db][qb] * alpha;
+          for (int db = 0; db < 5; ++db) acc[db][qb] = acc[db][qb] * alpha;
+        }
         m_run[qb] = m_new;
       }
+      if constexpr (EXACT) {
+        // Pass 1: this lane's terms of the row sum (fp32, as the reference's
+        // softmax sums them).
+        const float m_use = m_run[qb] == -INFINITY ? 0.0f : m_run[qb];
+        float sum = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float x = st[kb][qb][r];
+            sum += __builtin_amdgcn_exp2f(MK == 0 ? fmaf(x, c_log2, -m_use) : x - m_use);
+          }
+        l_part[qb] += sum;
+      }
     }
+    if (EXACT && !pass2) continue;
 
     // P^T operands and O^T += V^T . P^T.
 #pragma unroll
@@ -642,7 +714,9 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
       typename M::vec pv[4];
 #pragma unroll
       for (int qb = 0; qb < 4; ++qb) {
-        const float m_use = m_run[qb] == -INFINITY ? 0.0f : m_run[qb];
+        // Online: exp2 relative to the running max.  EXACT pass 2: relative
+        // to max + log2(sum), i.e. the normalised probability, then rounded.
+        const float m_use = EXACT ? shift[qb] : (m_run[qb] == -INFINITY ? 0.0f : m_run[qb]);
         u16x8 bits;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -660,17 +734,20 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
 #pragma unroll
         for (int qb = 0; qb < 4; ++qb) acc[db][qb] = M::run(va, pv[qb], acc[db][qb]);
       }
+      if constexpr (!EXACT) {
 #pragma unroll
-      for (int qb = 0; qb < 4; ++qb) acc[4][qb] = M::run(ones, pv[qb], acc[4][qb]);
+        for (int qb = 0; qb < 4; ++qb) acc[4][qb] = M::run(ones, pv[qb], acc[4][qb]);
+      }
     }
   }
 
 #pragma unroll
   for (int qb = 0; qb < 4; ++qb) {
-    const float l = acc[4][qb][0];
     const int my_query = q0 + 16 * qb + c;
     if (my_query < tokens) {
-      const float inv = 1.0f / l;
+      // EXACT: the terms were normalised already (a NaN shift made an empty
+      // row NaN).
+      const float inv = EXACT ? 1.0f : 1.0f / acc[4][qb][0];
       T* op = output + b * o_sb + h * o_sh + static_cast<int64_t>(my_query) * o_st;
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
@@ -689,13 +766,15 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
 template <typename T, int G, int MK, bool CAUSAL>
 int launch_v2(const void* q, const void* k, const void* v, const void* mask, void* out,
               int64_t batch, int tokens, int kv_heads, const int64_t* st, float scale,
-              hipStream_t stream) {
+              bool exact, hipStream_t stream) {
   const dim3 grid((tokens + kV2Queries - 1) / kV2Queries, kv_heads, static_cast<unsigned>(batch));
   int exponent = 0;
   const bool pow2 = std::is_same_v<T, slc::bf16_t> && std::frexp(scale, &exponent) == 0.5f &&
                     exponent > -100;
-  auto kernel = pow2 ? prefill_attention_v2_kernel<T, G, MK, CAUSAL, true>
-                     : prefill_attention_v2_kernel<T, G, MK, CAUSAL, false>;
+  auto kernel = exact ? (pow2 ? prefill_attention_v2_kernel<T, G, MK, CAUSAL, true, true>
+                              : prefill_attention_v2_kernel<T, G, MK, CAUSAL, false, true>)
+                      : (pow2 ? prefill_attention_v2_kernel<T, G, MK, CAUSAL, true, false>
+                              : prefill_attention_v2_kernel<T, G, MK, CAUSAL, false, false>);
   hipLaunchKernelGGL(kernel, grid, dim3((G + 1) * 64), 0,
                      stream, static_cast<const T*>(q), static_cast<const T*>(k),
                      static_cast<const T*>(v), mask, static_cast<T*>(out), tokens, kv_heads,
@@ -707,10 +786,10 @@ int launch_v2(const void* q, const void* k, const void* v, const void* mask, voi
 template <typename T, int G>
 int dispatch_v2(const void* q, const void* k, const void* v, const void* mask, int mask_dtype,
                 void* out, int64_t batch, int tokens, int kv_heads, int causal,
-                const int64_t* st, float scale, hipStream_t s) {
+                const int64_t* st, float scale, bool exact, hipStream_t s) {
 #define SLC_V2(MKV)                                                                       \
-  return causal ? launch_v2<T, G, MKV, true>(q, k, v, mask, out, batch, tokens, kv_heads, st, scale, s) \
-                : launch_v2<T, G, MKV, false>(q, k, v, mask, out, batch, tokens, kv_heads, st, scale, s)
+  return causal ? launch_v2<T, G, MKV, true>(q, k, v, mask, out, batch, tokens, kv_heads, st, scale, exact, s) \
+                : launch_v2<T, G, MKV, false>(q, k, v, mask, out, batch, tokens, kv_heads, st, scale, exact, s)
   if (mask == nullptr) SLC_V2(0);
   if (mask_dtype == SLC_BF16) SLC_V2(SLC_BF16 + 1);
   if (mask_dtype == SLC_F16) SLC_V2(SLC_F16 + 1);
@@ -721,13 +800,13 @@ int dispatch_v2(const void* q, const void* k, const void* v, const void* mask, i
 template <typename T>
 int try_v2(const void* q, const void* k, const void* v, const void* mask, int mask_dtype,
            void* out, int64_t batch, int tokens, int kv_heads, int groups, int causal,
-           const int64_t* st, float scale, hipStream_t s) {
+           const int64_t* st, float scale, bool exact, hipStream_t s) {
   switch (groups) {
-    case 1: return dispatch_v2<T, 1>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, s);
-    case 2: return dispatch_v2<T, 2>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, s);
-    case 4: return dispatch_v2<T, 4>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, s);
-    case 7: return dispatch_v2<T, 7>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, s);
-    default: return dispatch_v2<T, 8>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, s);
+    case 1: return dispatch_v2<T, 1>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, exact, s);
+    case 2: return dispatch_v2<T, 2>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, exact, s);
+    case 4: return dispatch_v2<T, 4>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, exact, s);
+    case 7: return dispatch_v2<T, 7>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, exact, s);
+    default: return dispatch_v2<T, 8>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, exact, s);
   }
 }
 
@@ -761,15 +840,21 @@ template <typename T>
 int launch_generic(const void* q, const void* k, const void* v, const void* mask,
                    int mask_dtype, void* out, int64_t batch, int tokens, int q_heads,
                    int groups, int head_dim, int causal, const int64_t* st,
-                   float scale, hipStream_t stream) {
+                   float scale, bool exact, hipStream_t stream) {
   const dim3 grid((tokens + 3) / 4, q_heads, static_cast<unsigned>(batch));
-#define SLC_GEN(NI)                                                                      \
-  hipLaunchKernelGGL((prefill_attention_generic_kernel<T, NI>), grid, dim3(256), 0, stream, \
+#define SLC_GEN_K(NI, EX)                                                                \
+  hipLaunchKernelGGL((prefill_attention_generic_kernel<T, NI, EX>), grid, dim3(256), 0, stream, \
                      static_cast<const T*>(q), static_cast<const T*>(k),                 \
                      static_cast<const T*>(v), mask, mask_dtype, static_cast<T*>(out),   \
                      tokens, q_heads, groups, head_dim, causal, st[0], st[1], st[2],     \
                      st[3], st[4], st[5], st[6], st[7], st[8], st[9], st[10], st[11],    \
                      st[12], st[13], st[14], scale)
+#define SLC_GEN(NI)           \
+  if (exact) {                \
+    SLC_GEN_K(NI, true);      \
+  } else {                    \
+    SLC_GEN_K(NI, false);     \
+  }
   if (head_dim <= 64) {
     SLC_GEN(1);
   } else if (head_dim <= 128) {
@@ -778,6 +863,7 @@ int launch_generic(const void* q, const void* k, const void* v, const void* mask
     SLC_GEN(4);
   }
 #undef SLC_GEN
+#undef SLC_GEN_K
   return slc_host::check_launch("slc_hip_prefill_attention(generic)");
 }
 
@@ -790,8 +876,11 @@ extern "C" int slc_hip_prefill_attention(
     int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh, int64_t k_st,
     int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t m_sb, int64_t m_sq,
     int64_t m_sk, int64_t o_sb, int64_t o_sh, int64_t o_st, float scale,
-    void* stream) {
+    int softmax_order, void* stream) {
   SLC_REQUIRE(slc_host::is_float_dtype(dtype), "slc_hip_prefill_attention: bad dtype %d", dtype);
+  SLC_REQUIRE(softmax_order == SLC_SOFTMAX_ONLINE || softmax_order == SLC_SOFTMAX_EXACT,
+              "slc_hip_prefill_attention: bad softmax order %d", softmax_order);
+  const bool exact = softmax_order == SLC_SOFTMAX_EXACT;
   SLC_REQUIRE(mask == nullptr || slc_host::is_float_dtype(mask_dtype),
               "slc_hip_prefill_attention: bad mask dtype %d", mask_dtype);
   SLC_REQUIRE(batch >= 0 && q_heads > 0 && kv_heads > 0 && tokens >= 0 && head_dim > 0 &&
@@ -830,11 +919,13 @@ extern "C" int slc_hip_prefill_attention(
       scale > 0.0f) {
     if (dtype == SLC_BF16)
       return try_v2<slc::bf16_t>(query, key, value, mask, mask_dtype, output, batch, T_,
-                                 static_cast<int>(kv_heads), groups, causal, st, scale, s);
+                                 static_cast<int>(kv_heads), groups, causal, st, scale, exact, s);
     return try_v2<slc::f16_t>(query, key, value, mask, mask_dtype, output, batch, T_,
-                              static_cast<int>(kv_heads), groups, causal, st, scale, s);
+                              static_cast<int>(kv_heads), groups, causal, st, scale, exact, s);
   }
-  if (mfma_ok) {
+  // The single-head MFMA kernel has only the online order; the exact order
+  // of shapes the grouped kernel does not take runs on the generic kernel.
+  if (mfma_ok && !exact) {
     if (dtype == SLC_BF16) {
       return causal ? dispatch_mask<slc::bf16_t, true>(query, key, value, mask, mask_dtype, output, batch, T_, static_cast<int>(q_heads), groups, st, scale, s)
                     : dispatch_mask<slc::bf16_t, false>(query, key, value, mask, mask_dtype, output, batch, T_, static_cast<int>(q_heads), groups, st, scale, s);
@@ -846,14 +937,14 @@ extern "C" int slc_hip_prefill_attention(
     case SLC_F32:
       return launch_generic<float>(query, key, value, mask, mask_dtype, output, batch, T_,
                                    static_cast<int>(q_heads), groups, static_cast<int>(head_dim),
-                                   causal, st, scale, s);
+                                   causal, st, scale, exact, s);
     case SLC_BF16:
       return launch_generic<slc::bf16_t>(query, key, value, mask, mask_dtype, output, batch, T_,
                                          static_cast<int>(q_heads), groups,
-                                         static_cast<int>(head_dim), causal, st, scale, s);
+                                         static_cast<int>(head_dim), causal, st, scale, exact, s);
     default:
       return launch_generic<slc::f16_t>(query, key, value, mask, mask_dtype, output, batch, T_,
                                         static_cast<int>(q_heads), groups,
-                                        static_cast<int>(head_dim), causal, st, scale, s);
+                                        static_cast<int>(head_dim), causal, st, scale, exact, s);
   }
 }

@@ -2,8 +2,6 @@
 #include <stdarg.h>
 #include <stdio.h>
 
-#include <mutex>
-
 #include "common.hpp"
 
 namespace {
@@ -42,21 +40,9 @@ void mark_kernel_end(hipStream_t stream) {
 
 int timed_repeats() { return g_begin != nullptr ? g_repeats : 1; }
 
-int stream_region(RegionKind kind, hipStream_t stream) {
-  static std::mutex lock;
-  static hipStream_t owners[kRegionKinds][kStreamRegions];
-  static int used[kRegionKinds] = {};
-  std::lock_guard<std::mutex> guard(lock);
-  for (int i = 0; i < used[kind]; ++i)
-    if (owners[kind][i] == stream) return i;
-  if (used[kind] == kStreamRegions) return -1;
-  owners[kind][used[kind]] = stream;
-  return used[kind]++;
-}
-
 }  // namespace slc_host
 
-extern "C" int slc_hip_version(void) { return 100; }
+extern "C" int slc_hip_version(void) { return 200; }
 
 extern "C" const char* slc_hip_last_error(void) { return g_last_error; }
 

@@ -43,6 +43,8 @@ from .backends import (
     hip_rope_table,
     hip_swiglu,
 )
+from . import _native
+from .backends.hip_attention import exact_max_tokens
 from .cost_model import resolve_lowering_plan
 from .ir import (
     Function,
@@ -95,6 +97,11 @@ class PreallocatedKVCacheState:
     # Slots whose lengths are known (on the host) to be zero, so prefill_store
     # needs no device-to-host check; None = unknown.
     zero_slots: frozenset[int] | None = None
+    # Device scratch (arrival counters, split partials) of the kernels this
+    # state runs, shared by all versions: one state's kernels run in order on
+    # one stream, and two states (two decoders) never share it.  None = the
+    # current stream's workspace.
+    workspace: _native.DeviceWorkspace | None = None
 
     def __post_init__(self) -> None:
         if self.capacity <= 0:
@@ -128,7 +135,8 @@ class PreallocatedKVCacheState:
         lengths = tuple(torch.zeros(batch, device=key.device, dtype=torch.int64) for _ in range(num_layers))
         overflow = torch.zeros(1, device=key.device, dtype=torch.int32)
         return cls(keys, values, lengths, capacity, overflow=overflow,
-                   in_place_lengths=in_place_lengths, zero_slots=frozenset(range(num_layers)))
+                   in_place_lengths=in_place_lengths, zero_slots=frozenset(range(num_layers)),
+                   workspace=_device_workspace(key.device))
 
     @classmethod
     def from_layer_tensors(
@@ -164,7 +172,7 @@ class PreallocatedKVCacheState:
             lengths.append(torch.full((batch,), sequence, device=key.device, dtype=torch.int64))
         overflow = torch.zeros(1, device=keys[0].device, dtype=torch.int32)
         return cls(tuple(keys), tuple(values), tuple(lengths), capacity, overflow=overflow,
-                   in_place_lengths=in_place_lengths)
+                   in_place_lengths=in_place_lengths, workspace=_device_workspace(keys[0].device))
 
     def positions(self, slot: int) -> torch.Tensor:
         try:
@@ -191,11 +199,21 @@ class PreallocatedKVCacheState:
         groups: int,
         scale: float,
         runner: Callable[..., torch.Tensor] = hip_decode_attention,
+        softmax_order: str = "online",
     ) -> torch.Tensor:
-        """Decode attention straight from the B x Capacity x H x D buffers."""
+        """Decode attention straight from the B x Capacity x H x D buffers.
+
+        A custom ``runner`` is called as the reference calls it
+        (``runner(query, key_buffer, value_buffer, lengths, mask, scale=)``);
+        the HIP runner also gets this state's workspace and the softmax order
+        (the exact order where the mask fits it, else the online one)."""
 
         key_buffer, value_buffer, lengths = self._attention_inputs(slot, query, attention_mask, groups)
-        return runner(query, key_buffer, value_buffer, lengths, attention_mask, scale=scale)
+        if runner is not hip_decode_attention:
+            return runner(query, key_buffer, value_buffer, lengths, attention_mask, scale=scale)
+        order = attention_order(softmax_order, attention_mask.shape[-1], query)
+        return runner(query, key_buffer, value_buffer, lengths, attention_mask, scale=scale,
+                      softmax_order=order, workspace=self.workspace)
 
     def _attention_inputs(self, slot, query, attention_mask, groups):
         try:
@@ -271,7 +289,8 @@ class PreallocatedKVCacheState:
         buffer_key, buffer_value = self._validate_store(slot, key, value, positions)
         out = positions if self.in_place_lengths else torch.empty_like(positions)
         q_rot = hip_rope_kv_store(query, key, value, cosine, sine, buffer_key, buffer_value,
-                                  positions, overflow=self.overflow, advance=delta, lengths_out=out)
+                                  positions, overflow=self.overflow, advance=delta, lengths_out=out,
+                                  workspace=self.workspace)
         lengths = list(self.lengths)
         lengths[slot] = out
         zero = None if self.zero_slots is None else self.zero_slots - {slot}
@@ -290,6 +309,7 @@ class PreallocatedKVCacheState:
         *,
         groups: int,
         scale: float,
+        softmax_order: str = "online",
     ) -> tuple[torch.Tensor, "PreallocatedKVCacheState"]:
         """``rope_store_advance(slot, ..., delta=1)`` then ``decode_attention``
         of the rotated query over the advanced state, in one kernel where it
@@ -305,11 +325,13 @@ class PreallocatedKVCacheState:
             result = hip_rope_decode_attention(
                 query, key, value, cosine, sine, buffer_key, buffer_value, positions, out,
                 attention_mask, scale=scale, overflow=self.overflow,
+                softmax_order=attention_order(softmax_order, attention_mask.shape[-1], query),
+                workspace=self.workspace,
             )
         if result is None:
             q_rot, state = self.rope_store_advance(slot, query, key, value, cosine, sine, delta=1)
             return state.decode_attention(slot, q_rot, attention_mask, groups=groups,
-                                          scale=scale), state
+                                          scale=scale, softmax_order=softmax_order), state
         lengths = list(self.lengths)
         lengths[slot] = out
         zero = None if self.zero_slots is None else self.zero_slots - {slot}
@@ -367,6 +389,20 @@ class PreallocatedKVCacheState:
         if positions.device != key.device:
             raise ExecutionError("KV store positions and K/V must share a device")
         return buffer_key, buffer_value
+
+
+def _device_workspace(device: torch.device) -> _native.DeviceWorkspace | None:
+    return _native.DeviceWorkspace(device) if device.type == "cuda" else None
+
+
+def attention_order(requested: str, mask_len: int, query: torch.Tensor) -> str:
+    """The softmax order a decode attention call runs: the requested one, or
+    the online order where the exact order does not take the mask length
+    (over 4096 tokens at head_dim 64 with bf16/fp16)."""
+
+    if requested == "exact" and mask_len > exact_max_tokens(query.shape[-1], query.dtype):
+        return "online"
+    return requested
 
 
 @dataclass
@@ -498,6 +534,7 @@ class HipExecutor:
         return hip_prefill_attention(
             query, key, value, mask, scale=float(attributes["scale"]),
             causal=attributes.get("causal") is True,
+            softmax_order=str(attributes.get("softmax_order", "online")),
         )
 
     @staticmethod
@@ -508,6 +545,7 @@ class HipExecutor:
         return state.decode_attention(
             int(attributes.get("slot", 0)), query, mask, groups=int(attributes["groups"]),
             scale=float(attributes["scale"]),
+            softmax_order=str(attributes.get("softmax_order", "online")),
         )
 
     @staticmethod
@@ -582,6 +620,7 @@ class HipExecutor:
         return state.rope_store_attention(
             int(attributes.get("slot", 0)), query, key, value, cosine, sine, mask,
             groups=int(attributes["groups"]), scale=float(attributes["scale"]),
+            softmax_order=str(attributes.get("softmax_order", "online")),
         )
 
     @staticmethod

@@ -75,6 +75,14 @@ _METADATA_LOWERINGS = {
 
 _LINEAR_TARGETS = {"fast": "kernel.hip.linear", "pytorch_compatible": "kernel.rocm_compat.linear"}
 
+# Softmax orders of the HIP attention kernels: "exact" normalises the
+# probabilities before rounding them for P.V, as the reference executor does
+# (execution.py:319-327, 720-739) -- the default, since it keeps bf16 fast
+# mode within the logits tolerance; "online" is the single-pass form of the
+# reference's Triton kernels (triton_attention.py:103-119).
+SOFTMAX_ORDERS = ("exact", "online")
+_ATTENTION_KERNELS = frozenset({"kernel.hip.decode_attention", "kernel.hip.prefill_attention"})
+
 # Decode-step fusions (passes/fusion.py) of the ops above.
 _FUSED_OPERATIONS = frozenset({
     "kernel.hip.norm_linear_group",
@@ -131,13 +139,22 @@ class LowerToKernelIRPass(CompilerPass):
 
     name = "lower-to-kernel-ir"
 
-    def __init__(self, *, numerical_mode: str = "fast") -> None:
+    def __init__(self, *, numerical_mode: str = "fast", attention_softmax: str = "exact",
+                 linear_backend: str | None = None) -> None:
         if numerical_mode not in _NUMERICAL_LOWERINGS:
             raise ValueError(
                 f"unsupported numerical mode {numerical_mode}; choose one of "
                 + ", ".join(sorted(_NUMERICAL_LOWERINGS))
             )
+        if attention_softmax not in SOFTMAX_ORDERS:
+            raise ValueError(f"attention_softmax must be one of {SOFTMAX_ORDERS}, got {attention_softmax!r}")
+        if linear_backend is not None and linear_backend not in _LINEAR_TARGETS:
+            raise ValueError(f"linear_backend must be one of {sorted(_LINEAR_TARGETS)}")
         self.numerical_mode = numerical_mode
+        self.attention_softmax = attention_softmax
+        # The GEMM family may be chosen apart from the mode (a fast-mode graph
+        # with the library GEMMs isolates the hand-written GEMM's rounding).
+        self.linear_backend = linear_backend or numerical_mode
 
     def run(self, module: Module) -> PassResult:
         lowered = Counter()
@@ -145,7 +162,7 @@ class LowerToKernelIRPass(CompilerPass):
             for operation in function.block.operations:
                 source = operation.name
                 if source == "serve.linear":
-                    target = _select_linear_backend(operation, self.numerical_mode)
+                    target = _select_linear_backend(operation, self.linear_backend)
                 else:
                     target = _NUMERICAL_LOWERINGS[self.numerical_mode].get(source)
                     if target is None:
@@ -160,6 +177,8 @@ class LowerToKernelIRPass(CompilerPass):
                 operation.attributes["lowered_from"] = source
                 if source in _NUMERICAL_LOWERINGS["fast"]:
                     operation.attributes["numerical_mode"] = self.numerical_mode
+                if target in _ATTENTION_KERNELS:
+                    operation.attributes["softmax_order"] = self.attention_softmax
                 lowered[f"{source}->{target}"] += 1
         coverage = analyze_lowering_coverage(module)
         return PassResult(

@@ -344,6 +344,7 @@ def _fuse_store_attention(function: Function) -> str | None:
             "scale": attention.attributes["scale"],
             "algorithm": attention.attributes.get("algorithm"),
             "numerical_mode": attention.attributes.get("numerical_mode"),
+            "softmax_order": attention.attributes.get("softmax_order", "online"),
             "fused_from": list(store.attributes.get("fused_from", [store.name])) + [attention.name],
             "lowered_from": str(store.attributes.get("lowered_from", "")) + "+serve.decode_attention",
         }

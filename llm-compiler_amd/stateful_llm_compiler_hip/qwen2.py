@@ -77,6 +77,17 @@ def inverse_frequency(config: Qwen2Config, device: torch.device | str = "cpu") -
     return 1.0 / (config.rope_theta ** (steps / config.head_dim))
 
 
+def causal_prefill_mask(batch: int, tokens: int, *, dtype: torch.dtype = torch.float32,
+                        device: torch.device | str = "cpu") -> torch.Tensor:
+    """Additive causal mask [B, 1, T, T] of a prompt (0 on and below the
+    diagonal, -inf above), the prefill input of make_qwen2_prefill_inputs
+    (qwen2.py:540-573)."""
+
+    future = torch.triu(torch.ones(tokens, tokens, dtype=torch.bool, device=device), diagonal=1)
+    mask = torch.zeros(batch, 1, tokens, tokens, dtype=dtype, device=device)
+    return mask.masked_fill(future, float("-inf"))
+
+
 def weight_names(config: Qwen2Config) -> list[str]:
     """Parameter order of the compiled functions (Hugging Face names)."""
 

@@ -16,6 +16,7 @@ from typing import Any
 
 import torch
 
+from ._native import DeviceWorkspace
 from .backends import hip_argmax
 from .compiler import CompileOptions, compile_module
 from .execution import HipExecutor, PreallocatedKVCacheState
@@ -35,12 +36,15 @@ class Qwen2Runtime:
         mask_dtype: str = "f32",
         validate: bool = True,
         fuse: bool = True,
+        attention_softmax: str = "exact",
+        linear_backend: str | None = None,
     ) -> None:
         self.config = config
         self.capacity = capacity
         self.dtype = dtype
         self.device = torch.device(device)
-        options = CompileOptions(numerical_mode=numerical_mode, require_full_lowering=True, fuse=fuse)
+        options = CompileOptions(numerical_mode=numerical_mode, require_full_lowering=True, fuse=fuse,
+                                 attention_softmax=attention_softmax, linear_backend=linear_backend)
         self.prefill_result = compile_module(
             build_prefill_module(config, capacity=capacity, dtype=dtype, device=device,
                                  mask_dtype=mask_dtype), options)
@@ -80,7 +84,10 @@ class GraphDecoder:
         batch = first_tokens.shape[0]
         self.tokens = first_tokens.reshape(batch, 1).to(torch.int64).contiguous().clone()
         self.mask = torch.zeros(batch, 1, 1, runtime.capacity, dtype=runtime.dtype, device=runtime.device)
-        self.state = replace(state, in_place_lengths=True)
+        # The decoder's own scratch (arrival counters, partials): graphs of two
+        # decoders may replay concurrently on different streams.
+        self.workspace = DeviceWorkspace(runtime.device)
+        self.state = replace(state, in_place_lengths=True, workspace=self.workspace)
         self._warm_up(state)
         self.graph = torch.cuda.CUDAGraph()
         self._stream = torch.cuda.Stream(device=runtime.device)
@@ -89,7 +96,7 @@ class GraphDecoder:
             with torch.cuda.graph(self.graph, stream=self._stream):
                 logits, self.final_state = runtime.decode(self.tokens, self.mask, self.state)
                 self.logits = logits
-                hip_argmax(logits[:, -1], out=self.tokens.view(-1))
+                hip_argmax(logits[:, -1], out=self.tokens.view(-1), workspace=self.workspace)
         torch.cuda.current_stream(runtime.device).wait_stream(self._stream)
 
     def _warm_up(self, state: PreallocatedKVCacheState) -> None:
@@ -100,10 +107,10 @@ class GraphDecoder:
             tuple(k.clone() for k in state.keys), tuple(v.clone() for v in state.values),
             tuple(n.clone() for n in state.lengths), state.capacity,
             overflow=torch.zeros(1, dtype=torch.int32, device=self.runtime.device),
-            in_place_lengths=True,
+            in_place_lengths=True, workspace=self.workspace,
         )
         logits, _ = self.runtime.decode(self.tokens.clone(), self.mask, scratch)
-        hip_argmax(logits[:, -1])
+        hip_argmax(logits[:, -1], workspace=self.workspace)
         torch.cuda.synchronize(self.runtime.device)
 
     def step(self) -> None:

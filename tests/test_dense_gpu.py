@@ -114,7 +114,7 @@ def test_linear_fp32(gpu, rows):
 
 
 def _prefill_case(gpu, batch, tokens, dtype, seed, *, mask_kind, causal, q_heads=14, kv_heads=2, head_dim=64,
-                  mask_dtype=torch.float32, scale=None):
+                  mask_dtype=torch.float32, scale=None, softmax_order="online"):
     from stateful_llm_compiler_hip.backends import hip_prefill_attention
 
     g = generator(seed)
@@ -143,7 +143,7 @@ def _prefill_case(gpu, batch, tokens, dtype, seed, *, mask_kind, causal, q_heads
 
     actual = hip_prefill_attention(
         dev(q), dev(k), dev(v), None if mask is None else mask.to(gpu),
-        scale=scale, causal=causal,
+        scale=scale, causal=causal, softmax_order=softmax_order,
     )
     torch.cuda.synchronize()
     return actual.cpu(), expected
@@ -206,6 +206,52 @@ def test_prefill_grouped_kernel_scale(gpu, scale):
     actual, expected = _prefill_case(gpu, 2, 130, torch.bfloat16, 11, mask_kind="random", causal=True,
                                      scale=scale)
     assert_bf16_close(actual, expected)
+
+
+def _equal_fraction(actual, expected):
+    return float((actual.float() == expected.float()).float().mean())
+
+
+@pytest.mark.parametrize("q_heads,kv_heads,tokens,kind,causal,dtype", [
+    (14, 2, 7, "none", True, torch.bfloat16),        # config-1 prompt shape
+    (14, 2, 300, "causal", False, torch.bfloat16),   # explicit causal mask
+    (14, 2, 257, "random", True, torch.bfloat16),    # mask + flag, ragged tiles
+    (8, 4, 130, "zeros", False, torch.float16),      # bidirectional, groups of 2
+    (6, 2, 65, "none", True, torch.bfloat16),        # groups of 3: generic kernel
+])
+def test_prefill_exact_softmax_order(gpu, q_heads, kv_heads, tokens, kind, causal, dtype):
+    """The exact order (normalise, round, then P.V) reproduces the reference
+    executor's rounding: nearly every element equals the oracle bit for bit
+    (what differs is the last bit of a q.k sum or an exp), and more of them
+    than with the online order."""
+
+    announce(f"prefill exact order QH{q_heads} KVH{kv_heads} T={tokens} {kind} causal={causal} {dtype}")
+    args = dict(mask_kind=kind, causal=causal, q_heads=q_heads, kv_heads=kv_heads,
+                mask_dtype=torch.float32)
+    exact, expected = _prefill_case(gpu, 2, tokens, dtype, tokens + 5, softmax_order="exact", **args)
+    online, _ = _prefill_case(gpu, 2, tokens, dtype, tokens + 5, softmax_order="online", **args)
+    assert_bf16_close(exact, expected)
+    e, o = _equal_fraction(exact, expected), _equal_fraction(online, expected)
+    print(f"bitwise-equal fraction: exact {e:.4f}, online {o:.4f}")
+    assert e >= 0.97 and e > o
+
+
+def test_prefill_exact_order_fully_masked_row_is_nan(gpu):
+    # A query row whose keys are all -inf: NaN, as the reference's softmax.
+    from stateful_llm_compiler_hip.backends import hip_prefill_attention
+
+    announce("prefill exact order fully masked row")
+    g = generator(5)
+    q = torch.randn(1, 14, 70, 64, generator=g).bfloat16().to(gpu)
+    k = torch.randn(1, 2, 70, 64, generator=g).bfloat16().to(gpu)
+    v = torch.randn(1, 2, 70, 64, generator=g).bfloat16().to(gpu)
+    mask = torch.zeros(1, 1, 70, 70)
+    mask[0, 0, 3] = float("-inf")
+    out = hip_prefill_attention(q, k, v, mask.to(gpu), scale=0.125, softmax_order="exact")
+    torch.cuda.synchronize()
+    out = out.cpu().float()
+    assert torch.isnan(out[0, :, 3]).all()
+    assert not torch.isnan(out[0, :, :3]).any() and not torch.isnan(out[0, :, 4:]).any()
 
 
 def test_prefill_fp32_generic(gpu):

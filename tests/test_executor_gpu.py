@@ -74,15 +74,8 @@ def test_config1_fp32_fast_mode(gpu):
 
 
 def test_config1_bf16_fast_mode(gpu):
-    """bf16 fast mode: KV within 2e-2 absolute of the eager model.
-
-    Logits: the eager bf16 model is itself ~2.4e-2 away from the same model
-    evaluated in fp64 on these logits (|logit| up to ~2.6, where one bf16 ulp
-    is 1.6e-2), so a single-pass online softmax -- which cannot round the
-    normalised probabilities the way eager does -- lands at the same noise
-    floor.  The test bounds the logits at 3e-2 from eager and requires the
-    HIP prefill logits to be no further from fp64 than eager's are, plus one
-    bf16 ulp of the logit magnitude."""
+    """bf16 fast mode (exact softmax order, the default): logits and KV within
+    2e-2 absolute of the eager model on the CPU."""
 
     announce("executor config1 bf16 fast")
     errors = {}
@@ -92,24 +85,31 @@ def test_config1_bf16_fast_mode(gpu):
 
     _run_both(gpu, torch.bfloat16, "fast", check=record)
     print("bf16 fast-mode errors:", {k: round(v, 5) for k, v in errors.items()})
-    kv = {k: v for k, v in errors.items() if k.endswith(" K") or k.endswith(" V")}
-    logits = {k: v for k, v in errors.items() if k.endswith("logits")}
-    assert max(kv.values()) <= 2e-2, kv
-    assert max(logits.values()) <= 3e-2, logits
+    assert max(errors.values()) <= 2e-2, errors
 
-    # Distance to the fp64 evaluation of the same bf16 weights (prefill).
-    weights = init_weights(CONFIG1, seed=0, dtype=torch.bfloat16)
-    w64 = {k: (v.double() if k != "rotary_emb.inv_freq" else v) for k, v in weights.items()}
-    ids, mask, pos = _prompt()
-    exact, _ = EagerQwen2(CONFIG1, w64).prefill(ids, mask.double(), pos)
-    eager, _ = EagerQwen2(CONFIG1, weights).prefill(ids, mask, pos)
-    rt = Qwen2Runtime(CONFIG1, {k: v.to(gpu) for k, v in weights.items()}, capacity=CAPACITY, device=str(gpu))
-    hip, _ = rt.prefill(ids.to(gpu), mask.to(gpu), pos.to(gpu))
-    eager_err = float((eager.double() - exact).abs().max())
-    hip_err = float((hip.cpu().double() - exact).abs().max())
-    ulp = 2.0 ** (torch.floor(torch.log2(exact.abs().max())).item() - 7)
-    print(f"fp64 distance: eager {eager_err:.4f}, hip {hip_err:.4f}")
-    assert hip_err <= eager_err + ulp
+
+def test_config1_bf16_fast_mode_online_softmax_attribution(gpu):
+    """The online softmax order (the reference's Triton form: probabilities
+    rounded before normalisation) is what takes config-1 logits past 2e-2:
+    with it the logits differ from eager by more than with the exact order,
+    and the K/V (written before any attention runs) are unaffected."""
+
+    announce("executor config1 bf16 fast, online vs exact attention")
+    results = {}
+    for order in ("exact", "online"):
+        errors = {}
+
+        def record(actual, expected, what, errors=errors):
+            errors[what] = float((actual.float().cpu() - expected.float().cpu()).abs().max())
+
+        weights = {k: v.to(gpu) for k, v in init_weights(CONFIG1, seed=0, dtype=torch.bfloat16).items()}
+        rt = Qwen2Runtime(CONFIG1, weights, capacity=CAPACITY, device=str(gpu), attention_softmax=order)
+        ids, mask, pos = _prompt()
+        logits, _ = rt.prefill(ids.to(gpu), mask.to(gpu), pos.to(gpu))
+        eager, _ = EagerQwen2(CONFIG1, init_weights(CONFIG1, seed=0, dtype=torch.bfloat16)).prefill(ids, mask, pos)
+        results[order] = float((logits.float().cpu() - eager.float()).abs().max())
+    print("prefill logits error by softmax order:", results)
+    assert results["exact"] <= 2e-2 < results["online"] or results["exact"] < results["online"]
 
 
 def test_config1_bf16_pytorch_compatible_is_exact(gpu):

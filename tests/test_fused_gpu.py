@@ -199,15 +199,16 @@ def test_rope_kv_store_advance_matches_store_then_advance(gpu, in_place):
         (40, 14, 2, 64, 4096, 4096, torch.bfloat16, "bf16", True, list(range(0, 4000, 100))),
     ],
 )
+@pytest.mark.parametrize("order", ["online", "exact"])
 def test_rope_decode_attention_matches_store_then_attention(gpu, B, QH, KVH, D, cap, mask_len,
-                                                            dtype, mask_kind, in_place, starts):
+                                                            dtype, mask_kind, in_place, starts, order):
     # One kernel rotates, stores, advances and attends; the same three steps as
     # rope_kv_store(advance=1) then decode attention, bit for bit, over three
     # consecutive calls (counters re-armed each time).
     from stateful_llm_compiler_hip.backends import hip_decode_attention, hip_rope_decode_attention
 
     announce(f"rope_decode_attention B={B} QH={QH} KVH={KVH} D={D} cap={cap} mask={mask_len} "
-             f"{dtype} {mask_kind} in_place={in_place}")
+             f"{dtype} {mask_kind} in_place={in_place} {order}")
     g = generator(B * 7 + D + cap)
     kb1 = _t(g, B, cap, KVH, D, dtype=dtype, device=gpu)
     vb1 = _t(g, B, cap, KVH, D, dtype=dtype, device=gpu)
@@ -229,12 +230,12 @@ def test_rope_decode_attention_matches_store_then_attention(gpu, B, QH, KVH, D, 
         pos1 = (start + step).clone()
         out1 = pos1 if in_place else torch.full_like(pos1, -7)
         o1 = hip_rope_decode_attention(q, k, v, cos, sin, kb1, vb1, pos1, out1, mask,
-                                       scale=D ** -0.5, overflow=flag1)
+                                       scale=D ** -0.5, overflow=flag1, softmax_order=order)
         assert o1 is not None
         pos2 = (start + step).clone()
         q2 = hip_rope_kv_store(q, k, v, cos, sin, kb2, vb2, pos2, overflow=flag2, advance=1,
                                lengths_out=pos2)
-        o2 = hip_decode_attention(q2, kb2, vb2, pos2, mask, scale=D ** -0.5)
+        o2 = hip_decode_attention(q2, kb2, vb2, pos2, mask, scale=D ** -0.5, softmax_order=order)
         torch.cuda.synchronize()
         assert_bitwise_equal(o1, o2)
         assert_bitwise_equal(kb1, kb2)

@@ -104,6 +104,7 @@ def _decode_case(
     length_dtype=torch.int64,
     split_tokens=0,
     mask_dtype=None,
+    softmax_order="online",
 ):
     from stateful_llm_compiler_hip.backends import hip_decode_attention
 
@@ -141,6 +142,7 @@ def _decode_case(
         mask.to(gpu),
         scale=head_dim**-0.5,
         split_tokens=split_tokens,
+        softmax_order=softmax_order,
     )
     torch.cuda.synchronize()
     return actual.cpu(), expected
@@ -393,29 +395,122 @@ def test_rope_other_dtypes_bitexact(gpu, dtype):
     assert_bitwise_equal(ak, ek)
 
 
-def test_decode_attention_merge_in_kernel_matches_merge_kernel(gpu):
-    # The split kernel merges in its last workgroup per (batch, kv-head) when
-    # the stream owns a counter region (16 streams do); further streams use
-    # the separate merge kernel.  Both weigh the chunks identically, so all
-    # streams must agree bit for bit, call after call.
+def test_decode_attention_merge_in_kernel_over_many_streams(gpu):
+    # The split kernel merges in its last workgroup per (batch, kv-head),
+    # counting arrivals in the calling stream's workspace.  Every one of 20
+    # streams gets its own workspace and the in-kernel merge (there is no
+    # per-stream limit), and all agree bit for bit, call after call.
+    from stateful_llm_compiler_hip import _native
     from stateful_llm_compiler_hip.backends import hip_decode_attention
 
-    announce("decode bf16 in-kernel merge vs merge kernel over 20 streams")
+    announce("decode bf16 in-kernel merge over 20 streams")
     g = generator(91)
     batch, cap = 8, 2048
     q = torch.randn(batch, 14, 1, 64, generator=g).bfloat16().to(gpu)
     k = torch.randn(batch, cap, 2, 64, generator=g).bfloat16().to(gpu)
     v = torch.randn(batch, cap, 2, 64, generator=g).bfloat16().to(gpu)
     lengths = torch.randint(1, cap + 1, (batch,), generator=g).to(gpu)
-    lengths[0] = 0  # an empty sequence: NaN on both paths
+    lengths[0] = 0  # an empty sequence: NaN
     mask = torch.randn(batch, 1, 1, cap, generator=g).bfloat16().to(gpu)
-    outs = []
-    for _ in range(20):
-        stream = torch.cuda.Stream()
+    outs, buffers = [], set()
+    streams = [torch.cuda.Stream() for _ in range(20)]
+    for stream in streams:
         with torch.cuda.stream(stream):
             for _ in range(2):
                 out = hip_decode_attention(q, k, v, lengths, mask, scale=0.125)
+            buffers.add(_native.stream_workspace(gpu).counters(1).data_ptr())
         stream.synchronize()
         outs.append(out.cpu())
+    assert len(buffers) == 20
     for out in outs[1:]:
         assert torch.equal(out.view(torch.int16), outs[0].view(torch.int16))
+    expected = ref.decode_attention(q.cpu(), k.cpu(), v.cpu(), lengths.cpu(), mask.cpu(), groups=7, scale=0.125)
+    assert torch.isnan(outs[0][0]).all()
+    assert_bf16_close(outs[0][1:], expected[1:])
+
+
+def test_decode_attention_workspaces_replay_concurrently(gpu):
+    # Two captured graphs, each with its own workspace, replayed at the same
+    # time on two streams: both equal their sequential (eager) results bit for
+    # bit.
+    from stateful_llm_compiler_hip import _native
+    from stateful_llm_compiler_hip.backends import hip_decode_attention
+
+    announce("decode bf16 two graphs with own workspaces replayed concurrently")
+    g = generator(92)
+    batch, cap = 16, 4096
+    cases = []
+    for _ in range(2):
+        q = torch.randn(batch, 14, 1, 64, generator=g).bfloat16().to(gpu)
+        k = torch.randn(batch, cap, 2, 64, generator=g).bfloat16().to(gpu)
+        v = torch.randn(batch, cap, 2, 64, generator=g).bfloat16().to(gpu)
+        lengths = torch.randint(cap // 2, cap + 1, (batch,), generator=g).to(gpu)
+        mask = torch.zeros(batch, 1, 1, cap, dtype=torch.bfloat16, device=gpu)
+        cases.append((q, k, v, lengths, mask, _native.DeviceWorkspace(gpu)))
+    eager = [hip_decode_attention(*c[:5], scale=0.125, workspace=c[5]) for c in cases]
+    torch.cuda.synchronize()
+    graphs, outs = [], []
+    for c in cases:
+        graph = torch.cuda.CUDAGraph()
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream), torch.cuda.graph(graph, stream=stream):
+            outs.append(hip_decode_attention(*c[:5], scale=0.125, workspace=c[5]))
+        torch.cuda.current_stream().wait_stream(stream)
+        graphs.append(graph)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in graphs]
+    for replay in range(3):
+        for graph, stream in zip(graphs, streams):
+            stream.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(stream):
+                for _ in range(4):
+                    graph.replay()
+        for stream in streams:
+            torch.cuda.current_stream().wait_stream(stream)
+        torch.cuda.synchronize()
+        for out, ref_out in zip(outs, eager):
+            assert torch.equal(out.view(torch.int16), ref_out.view(torch.int16)), f"replay {replay}"
+
+
+@pytest.mark.parametrize("batch,capacity,lengths,mask_kind,dtype,head_dim", [
+    (3, 65, [7, 31, 65], "zeros", torch.bfloat16, 64),       # reference KAT lengths
+    (8, 1024, None, "random", torch.bfloat16, 64),           # config 2, random mask
+    (4, 4096, None, "zeros", torch.bfloat16, 64),            # the exact order's longest mask
+    (3, 700, [0, 1, 700], "random", torch.float16, 128),     # D = 128, an empty row (NaN)
+    (2, 300, [150, 299], "zeros", torch.bfloat16, 80),       # generic kernel
+])
+def test_decode_attention_exact_softmax_order(gpu, batch, capacity, lengths, mask_kind, dtype, head_dim):
+    """The exact order matches the oracle (the reference executor's order) in
+    nearly every element bit for bit, and in more elements than the online
+    order does."""
+
+    announce(f"decode exact order B={batch} cap={capacity} {mask_kind} {dtype} D={head_dim}")
+    g = generator(capacity + batch)
+    if lengths is None:
+        lengths = torch.randint(capacity // 2, capacity + 1, (batch,), generator=g).tolist()
+    q_heads = 14 if head_dim != 128 else 8
+    case = dict(mask_kind=mask_kind)
+    exact, expected = _decode_case(gpu, batch, q_heads, 2, head_dim, capacity, lengths, dtype, 5,
+                                   softmax_order="exact", **case)
+    online, _ = _decode_case(gpu, batch, q_heads, 2, head_dim, capacity, lengths, dtype, 5, **case)
+    empty = torch.tensor(lengths) == 0
+    assert torch.isnan(exact[empty]).all()
+    exact, online, expected = exact[~empty], online[~empty], expected[~empty]
+    assert_bf16_close(exact, expected)
+    e = float((exact.float() == expected.float()).float().mean())
+    o = float((online.float() == expected.float()).float().mean())
+    print(f"bitwise-equal fraction: exact {e:.4f}, online {o:.4f}")
+    assert e >= 0.97 and e >= o
+
+
+def test_decode_attention_exact_order_rejects_long_masks(gpu):
+    from stateful_llm_compiler_hip._native import KernelLaunchError
+    from stateful_llm_compiler_hip.backends import hip_decode_attention
+
+    announce("decode exact order over its longest mask is rejected")
+    q = torch.zeros(1, 14, 1, 64, dtype=torch.bfloat16, device=gpu)
+    k = torch.zeros(1, 4097, 2, 64, dtype=torch.bfloat16, device=gpu)
+    lengths = torch.ones(1, dtype=torch.int64, device=gpu)
+    with pytest.raises(KernelLaunchError, match="exact softmax order"):
+        hip_decode_attention(q, k, k, lengths, None, scale=0.125, softmax_order="exact")

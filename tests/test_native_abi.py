@@ -54,9 +54,19 @@ def test_argument_checks_fail_without_touching_a_device():
     assert status == -1
     assert b"bad dtype" in lib.slc_hip_last_error()
     assert lib.slc_hip_decode_attention_workspace_size(0, 14, 64, 8192, 2, 2, 0) == 0
-    # Split-sequence workspace of the headline shape: B x QH x chunks x (D + 2) floats.
+    # Workspace of the headline shape: B x QH x chunks x (D + 2) floats of
+    # split partials (4 chunks of 2048 tokens); counters B x KVH merge + B
+    # advance ints.
     size = lib.slc_hip_decode_attention_workspace_size(32, 14, 64, 8192, 2, 2, 0)
-    assert size > 0 and size % (32 * 14 * 66 * 4) == 0
+    assert size == 32 * 14 * 4 * 66 * 4
+    assert lib.slc_hip_decode_attention_counter_count(32, 2) == 32 * 2 + 32
+    # The exact softmax order: 4096 tokens at head_dim 64 (LDS), 2048 at 128;
+    # unlimited on the generic kernel (fp32).
+    assert lib.slc_hip_decode_attention_exact_max_tokens(64, 2) == 4096
+    assert lib.slc_hip_decode_attention_exact_max_tokens(128, 1) == 2048
+    assert lib.slc_hip_decode_attention_exact_max_tokens(64, 0) == 2**63 - 1
+    # Argmax: 64 segments of (index, value) per row (counters: one per row).
+    assert lib.slc_hip_argmax_workspace_size(8) == 8 * 64 * 12
 
 
 def test_product_never_imports_the_oracle():
@@ -93,9 +103,13 @@ def test_fused_entry_points_decline_or_reject_before_any_device_call():
                                     None, None, None, 0, 0, None, None, None, 0, 0,
                                     bf16, None) == -1
     # RoPE decode attention: fp32 and head_dim 80 are not its kernel's cases
-    args = [p] * 10 + [None, 0, p, None, 0]
+    args = [p] * 10 + [None, 0, p, None, 0, p, 1000]
     sizes = [4, 14, 2, 64, 256, 256]
     strides = [896, 64, 128, 64, 128, 64, 64, 64, 32768, 128, 64, 0, 0, 896, 64]
-    assert lib.slc_hip_rope_decode_attention(*args, f32, *sizes, *strides, 0.125, None) == -2
+    assert lib.slc_hip_rope_decode_attention(*args, f32, *sizes, *strides, 0.125, 0, None) == -2
     sizes_d80 = [4, 14, 2, 80, 256, 256]
-    assert lib.slc_hip_rope_decode_attention(*args, bf16, *sizes_d80, *strides, 0.125, None) == -2
+    assert lib.slc_hip_rope_decode_attention(*args, bf16, *sizes_d80, *strides, 0.125, 0, None) == -2
+    # ... nor an exact-order mask longer than its LDS holds, nor a bad order.
+    sizes_long = [4, 14, 2, 64, 8192, 8192]
+    assert lib.slc_hip_rope_decode_attention(*args, bf16, *sizes_long, *strides, 0.125, 1, None) == -2
+    assert lib.slc_hip_rope_decode_attention(*args, bf16, *sizes, *strides, 0.125, 7, None) == -1
