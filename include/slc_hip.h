@@ -69,6 +69,20 @@ enum slc_status { SLC_OK = 0, SLC_ERR_INVALID_ARGUMENT = -1, SLC_ERR_UNSUPPORTED
  */
 enum slc_softmax_order { SLC_SOFTMAX_ONLINE = 0, SLC_SOFTMAX_EXACT = 1 };
 
+/*
+ * Split-sequence choice of decode attention (the split_tokens argument):
+ *   0                  : fixed chunk per (batch, kv head), sized so the grid
+ *                        fills the GPU; the chunks past a sequence's length
+ *                        exit at once
+ *   > 0                : fixed chunk of that many tokens (rounded up to the
+ *                        workgroup's 128-token sweep)
+ *   SLC_SPLIT_BALANCED : length-balanced split: every workgroup streams one
+ *                        contiguous piece of one sequence, the pieces sized
+ *                        from the device-side lengths so that all are about
+ *                        equal (online order, batch <= 2048; else as 0)
+ */
+enum slc_split { SLC_SPLIT_BALANCED = -1 };
+
 /* Library version (major*10000 + minor*100 + patch). */
 SLC_API int slc_hip_version(void);
 
@@ -140,8 +154,8 @@ SLC_API int slc_hip_kv_store(void* key_buffer, void* value_buffer, const void* k
  *                  concurrently) its own.
  * Token s of batch b is attended iff s < min(lengths[b], mask_len, capacity).
  * kv head of query head h is h / (q_heads / kv_heads).
- * split_tokens selects the split-sequence chunk (0 = automatic; ignored by
- * the exact order, which runs one chunk per (batch, kv head)).
+ * split_tokens selects the split (slc_split above; ignored by the exact
+ * order, which runs one chunk per (batch, kv head)).
  * softmax_order: SLC_SOFTMAX_ONLINE or SLC_SOFTMAX_EXACT; the exact order
  * takes min(mask_len, capacity) up to
  * slc_hip_decode_attention_exact_max_tokens(head_dim, dtype) tokens.

@@ -31,6 +31,9 @@ SLC_I64 = 4
 # slc_softmax_order
 SOFTMAX_ORDERS = {"online": 0, "exact": 1}
 
+# slc_split: decode attention's length-balanced split-sequence variant
+SPLIT_BALANCED = -1
+
 _DTYPE_TAGS = {
     torch.float32: SLC_F32,
     torch.float16: SLC_F16,

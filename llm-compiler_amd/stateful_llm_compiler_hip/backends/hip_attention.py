@@ -14,6 +14,8 @@ import torch
 from .. import _native
 from .hip_ops import check_flag
 
+SPLIT_BALANCED = _native.SPLIT_BALANCED
+
 
 def _workspace(lib, device: torch.device, nbytes: int, batch: int, kv_heads: int,
                workspace: _native.DeviceWorkspace | None) -> tuple[torch.Tensor | None, torch.Tensor, int]:
@@ -53,6 +55,9 @@ def hip_decode_attention(
     dtype) or int32.  ``attention_mask`` is B x 1 x 1 x S additive, or None
     for an all-zero mask over the whole capacity.
 
+    ``split_tokens``: 0 picks a fixed chunk per (batch, kv head) sized to fill
+    the GPU, > 0 a fixed chunk of that many tokens, ``SPLIT_BALANCED`` (-1)
+    the length-balanced split (pieces sized from the device-side lengths).
     ``softmax_order``: "online" (the reference Triton kernel's single-pass
     form, the default) or "exact" (normalise, round, then P.V -- the
     reference executor's order; masks up to ``exact_max_tokens`` long).

@@ -32,193 +32,12 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "decode_tiles.hpp"
 #include "op_math.hpp"
 
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kTile = 32;   // tokens per wave iteration
-#ifndef SLC_DECODE_WAVES
-#define SLC_DECODE_WAVES 4
-#endif
-constexpr int kWaves = SLC_DECODE_WAVES;  // wavefronts per split-kernel workgroup
-constexpr int kThreads = kWaves * 64;
-constexpr int kGenericWaves = 4;          // wavefronts of the generic kernel
-constexpr int kMaxGroups = 16;
-constexpr int kMaxChunks = 256;  // split-sequence chunks per (batch, kv-head), merge LDS
-
-struct u16x8 {
-  uint16_t v[8];
-};
-
-template <typename T>
-struct Mfma;
-template <>
-struct Mfma<slc::bf16_t> {
-  using vec = bf16x8_t;
-  static __device__ __forceinline__ f32x4_t run(vec a, vec b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-};
-template <>
-struct Mfma<slc::f16_t> {
-  using vec = f16x8_t;
-  static __device__ __forceinline__ f32x4_t run(vec a, vec b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-};
-
-template <typename T>
-__device__ __forceinline__ typename Mfma<T>::vec as_vec(uint4 raw) {
-  return __builtin_bit_cast(typename Mfma<T>::vec, raw);
-}
-
-template <typename T>
-__device__ __forceinline__ uint16_t bits_of(float f) {
-  return slc::from_f32<T>(f).bits;
-}
-
-__device__ __forceinline__ float fast_exp2(float x) {
-  return __builtin_amdgcn_exp2f(x);
-}
-
-// LDS row stride (in 16-bit elements) of a staged V tile row.  The 4-element
-// pad makes the four token rows read by one transposed access land on disjoint
-// bank groups.
-template <int D>
-constexpr int v_row() {
-  return D + 4;
-}
-
-template <typename T, int D>
-struct SharedLayout {
-  static constexpr int kVTileElems = kTile * v_row<D>();
-  static constexpr int kVBytes = kWaves * kVTileElems * 2;
-  static constexpr int kCombineBytes =
-      kWaves * (2 * kMaxGroups + kMaxGroups * D) * 4;
-  static constexpr int kBytes = kVBytes > kCombineBytes ? kVBytes : kCombineBytes;
-};
-
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
-
-// Raw buffer resource over [base, base + bytes): loads at or past the end
-// return zero without touching memory (the hardware range check), which is how
-// rows past the chunk end are handled -- no clamps, no branches.
-// Callers pass wave-uniform values; readfirstlane states that to the compiler
-// so the resource stays in scalar registers (no per-lane waterfall loop).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
-  const uint64_t address = reinterpret_cast<uint64_t>(base);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(address));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(address >> 32));
-  void* uniform = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
-  return __builtin_amdgcn_make_buffer_rsrc(uniform, 0, __builtin_amdgcn_readfirstlane(bytes),
-                                           0x00020000);
-}
-__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int offset) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 0));
-}
-
-// ---- merge inside the split kernel ------------------------------------------
-// The caller's counter array holds one counter per (batch, kv-head) (and one
-// per batch for the RoPE variant's length advance); it is zero-filled once by
-// its owner and every kernel leaves it zero again.  Every
-// split workgroup publishes its partial with agent-scope stores, meets its
-// waves at a barrier, and one thread bumps the (batch, kv-head)'s counter
-// with an agent-scope acquire-release add: the release orders the whole
-// workgroup's stores (made visible to that thread by the barrier) before the
-// count, and the acquire of the workgroup that completes the count orders its
-// later loads of the partials after every other workgroup's release.  The
-// merge weighs the chunks exactly as the separate merge kernel does, so both
-// paths give bit-identical outputs.  Two calls that share counters must not
-// run concurrently (calls on one stream never do).
-__device__ __forceinline__ void publish(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float fetch_partial(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int count_arrival(int* counter) {
-  return __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void rearm(int* counter) {
-  __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-constexpr int kFusedMergeUnroll = 8;
-// Length advance folded into the attention kernel: every workgroup of a
-// batch bumps the batch's counter once all its waves have read the length
-// (the merge's barrier), and the one completing the count writes the new
-// length (flagging an advance past the capacity) and re-arms the counter.
-struct LenAdvance {
-  int* counter;      // nullptr: no advance
-  int total;         // workgroups per batch (kv heads x chunks)
-  int64_t* out;      // the batch's length
-  int64_t next;      // its new value
-  int* overflow;
-  int64_t capacity;
-};
-
-__device__ __forceinline__ void finish_advance(const LenAdvance& adv, int before) {
-  if (adv.counter == nullptr || before != adv.total - 1) return;
-  rearm(adv.counter);
-  *adv.out = adv.next;
-  if (adv.overflow != nullptr && (adv.next > adv.capacity || adv.next < 0)) *adv.overflow = 1;
-}
-
-// RoPE + KV store of the new token folded into the attention kernel
-// (slc_hip_rope_decode_attention).  key/value: the token's projections
-// [b, kv_head, D] (key before RoPE); cosine/sine: [b, D] rows of its position.
-struct RopeStore {
-  const void* key;
-  const void* value;
-  const void* cosine;
-  const void* sine;
-  int64_t k_sb, k_sh, v_sb, v_sh, c_sb, s_sb;
-  // The KV buffers again, for the new row's write (the kernel's buffer
-  // arguments are read-only views; the only row written is one this
-  // workgroup does not use from memory, see the tile patch).
-  void* key_out;
-  void* value_out;
-  int64_t* lengths_out;
-  int* overflow;
-  int* counters;  // per-batch advance counters (caller's counter array)
-};
-
-// Qwen2 half rotation of one lane's slices: slice kk pairs with kk + KK/2
-// (dims d and d + D/2), rounded exactly as the RoPE kernel rounds.
-template <typename T, int KK>
-__device__ __forceinline__ void rope_slices(uint4 (&x)[KK], const uint4 (&cs)[KK],
-                                            const uint4 (&sn)[KK]) {
-  constexpr int H = KK / 2;
-  auto f = [](uint16_t bits) {
-    T t;
-    t.bits = bits;
-    return slc::to_f32(t);
-  };
-#pragma unroll
-  for (int kk = 0; kk < H; ++kk) {
-    u16x8 a = __builtin_bit_cast(u16x8, x[kk]);
-    u16x8 z = __builtin_bit_cast(u16x8, x[kk + H]);
-    const u16x8 c1 = __builtin_bit_cast(u16x8, cs[kk]);
-    const u16x8 c2 = __builtin_bit_cast(u16x8, cs[kk + H]);
-    const u16x8 s1 = __builtin_bit_cast(u16x8, sn[kk]);
-    const u16x8 s2 = __builtin_bit_cast(u16x8, sn[kk + H]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float o1, o2;
-      slc::rope_pair<T>(f(a.v[i]), f(z.v[i]), f(c1.v[i]), f(c2.v[i]), f(s1.v[i]), f(s2.v[i]),
-                        o1, o2);
-      a.v[i] = bits_of<T>(o1);
-      z.v[i] = bits_of<T>(o2);
-    }
-    x[kk] = __builtin_bit_cast(uint4, a);
-    x[kk + H] = __builtin_bit_cast(uint4, z);
-  }
-}
+using namespace slc_decode;
 
 template <typename T, int D>
 __device__ __forceinline__ void merge_if_last(const float* part_o, const float* part_ml,
@@ -1216,16 +1035,28 @@ int launch_generic(const void* query, const void* kb, const void* vb,
 // Geometry of one call: which kernel, the split, and the workspace it needs.
 struct Plan {
   bool mfma;
+  bool stream;       // balanced split (decode_stream.hip)
   int64_t chunk, nchunks;
   int64_t need;      // workspace bytes (partials)
   int64_t counters;  // counter ints, 0 for the generic kernel
 };
 
+// split_tokens: 0 = fixed chunk sized for the grid, > 0 = fixed chunk of that
+// many tokens, SLC_SPLIT_BALANCED = the length-balanced split (decode_stream.hip;
+// online order, where it fits -- else the automatic fixed chunk).
 Plan plan_call(int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
-               int64_t head_dim, int64_t mask_len, int64_t split_tokens, bool exact) {
-  Plan p{false, 0, 1, 0, 0};
+               int64_t head_dim, int64_t mask_len, int64_t capacity, int64_t split_tokens,
+               bool exact, bool allow_stream = true) {
+  Plan p{false, false, 0, 1, 0, 0};
   p.mfma = mfma_eligible(dtype, head_dim, q_heads / kv_heads) && mask_len > 0;
   if (!p.mfma) return p;
+  if (allow_stream && !exact && split_tokens == SLC_SPLIT_BALANCED &&
+      stream_eligible(batch, kv_heads, q_heads / kv_heads, mask_len, capacity)) {
+    p.stream = true;
+    p.need = stream_workspace_bytes(q_heads, kv_heads, head_dim);
+    p.counters = counter_count(batch, kv_heads);
+    return p;
+  }
   if (exact) {
     p.chunk = mask_len;
     p.nchunks = 1;
@@ -1248,7 +1079,15 @@ extern "C" int64_t slc_hip_decode_attention_workspace_size(
     return 0;
   }
   // The online split needs at least what the exact single-chunk form does.
-  return plan_call(dtype, batch, q_heads, kv_heads, head_dim, mask_len, split_tokens, false).need;
+  // Enough for either split (the balanced one may decline at the call's
+  // capacity and take the fixed-chunk grid).
+  const int64_t fixed =
+      plan_call(dtype, batch, q_heads, kv_heads, head_dim, mask_len, mask_len, split_tokens,
+                false, false).need;
+  const int64_t balanced =
+      plan_call(dtype, batch, q_heads, kv_heads, head_dim, mask_len, mask_len, split_tokens,
+                false).need;
+  return std::max(fixed, balanced);
 }
 
 extern "C" int64_t slc_hip_decode_attention_counter_count(int64_t batch, int64_t kv_heads) {
@@ -1300,7 +1139,8 @@ extern "C" int slc_hip_decode_attention(
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t ml = mask_len;
 
-  Plan plan = plan_call(dtype, batch, q_heads, kv_heads, head_dim, ml, split_tokens, exact);
+  Plan plan =
+      plan_call(dtype, batch, q_heads, kv_heads, head_dim, ml, capacity, split_tokens, exact);
   if (plan.mfma) {
     // 16-byte vector loads need 8-element alignment of every row start.
     const uint64_t bits = reinterpret_cast<uintptr_t>(query) |
@@ -1329,6 +1169,14 @@ extern "C" int slc_hip_decode_attention(
     SLC_REQUIRE(counters != nullptr && num_counters >= plan.counters,
                 "slc_hip_decode_attention: %lld counters needed, got %lld",
                 (long long)plan.counters, (long long)num_counters);
+    if (plan.stream) {
+      StreamCall call{query,   key_buffer, value_buffer, lengths,  lengths_dtype, mask,
+                      mask_dtype, output,  workspace,    counters, dtype,         batch,
+                      q_heads, kv_heads,  head_dim,     capacity, ml,            {},
+                      scale,   s};
+      std::copy(st, st + 9, call.st);
+      return launch_stream(call);
+    }
 #define SLC_DA_CALL(TT, DD)                                                                  \
   launch_mfma<TT, DD>(query, key_buffer, value_buffer, lengths, lengths_dtype, mask,         \
                       mask_dtype, output, workspace, counters, batch, q_heads, kv_heads,     \
@@ -1406,7 +1254,8 @@ extern "C" int slc_hip_rope_decode_attention(
       capacity * kv_stride_s * 2 >= (int64_t{1} << 31) ||
       mask_len * mask_stride_s * mask_es >= (int64_t{1} << 31) || capacity >= (int64_t{1} << 30))
     return kUnsupported;
-  const Plan plan = plan_call(dtype, batch, q_heads, kv_heads, head_dim, mask_len, 0, exact);
+  const Plan plan =
+      plan_call(dtype, batch, q_heads, kv_heads, head_dim, mask_len, capacity, 0, exact);
   SLC_REQUIRE(plan.need == 0 || (workspace != nullptr && workspace_bytes >= plan.need),
               "slc_hip_rope_decode_attention: workspace of %lld bytes needed, got %lld",
               (long long)plan.need, (long long)workspace_bytes);

@@ -21,6 +21,9 @@ from helpers import (
 )
 from oracle import kernels as ref
 
+# slc_split: the length-balanced split-sequence variant of decode attention.
+SPLIT_BALANCED = -1
+
 pytestmark = pytest.mark.gpu
 
 
@@ -157,31 +160,39 @@ def test_decode_attention_reference_lengths_fp32(gpu):
     assert_fp32_close(actual, expected)
 
 
+@pytest.mark.parametrize("split", [0, SPLIT_BALANCED])
 @pytest.mark.parametrize("batch", [1, 8, 32, 64])
 @pytest.mark.parametrize("max_len", [64, 1024, 8192])
-def test_decode_attention_config2_bf16(gpu, batch, max_len):
-    announce(f"decode bf16 B={batch} L={max_len}")
+def test_decode_attention_config2_bf16(gpu, batch, max_len, split):
+    announce(f"decode bf16 B={batch} L={max_len} split_tokens={split}")
     g = generator(batch * 7 + max_len)
     lengths = torch.randint(max_len // 2, max_len + 1, (batch,), generator=g).tolist()
-    actual, expected = _decode_case(gpu, batch, 14, 2, 64, max_len, lengths, torch.bfloat16, batch + max_len)
+    actual, expected = _decode_case(gpu, batch, 14, 2, 64, max_len, lengths, torch.bfloat16, batch + max_len,
+                                    split_tokens=split)
     assert_bf16_close(actual, expected)
 
 
-def test_decode_attention_config2_bf16_long(gpu):
-    announce("decode bf16 B=8 L=32768")
-    g = generator(11)
-    lengths = torch.randint(16384, 32769, (8,), generator=g).tolist()
-    actual, expected = _decode_case(gpu, 8, 14, 2, 64, 32768, lengths, torch.bfloat16, 12)
+@pytest.mark.parametrize("split", [0, SPLIT_BALANCED])
+@pytest.mark.parametrize("batch", [1, 8, 32, 64])
+def test_decode_attention_config2_bf16_long(gpu, batch, split):
+    # Config 2's longest rows: L = 32768, lengths U[L/2, L] (B = 64 holds 1 GB
+    # of K/V on the host for the oracle).
+    announce(f"decode bf16 B={batch} L=32768 split_tokens={split}")
+    g = generator(11 + batch)
+    lengths = torch.randint(16384, 32769, (batch,), generator=g).tolist()
+    actual, expected = _decode_case(gpu, batch, 14, 2, 64, 32768, lengths, torch.bfloat16, 12 + batch,
+                                    split_tokens=split)
     assert_bf16_close(actual, expected)
 
 
+@pytest.mark.parametrize("split", [0, SPLIT_BALANCED])
 @pytest.mark.parametrize("layout", ["bshd", "bhsd"])
 @pytest.mark.parametrize("length_dtype", [torch.int64, torch.int32])
-def test_decode_attention_layouts_and_length_dtypes(gpu, layout, length_dtype):
-    announce(f"decode bf16 layout={layout} lengths={length_dtype}")
+def test_decode_attention_layouts_and_length_dtypes(gpu, layout, length_dtype, split):
+    announce(f"decode bf16 layout={layout} lengths={length_dtype} split_tokens={split}")
     actual, expected = _decode_case(
         gpu, 4, 14, 2, 64, 1024, [1, 333, 1000, 1024], torch.bfloat16, 21,
-        layout=layout, length_dtype=length_dtype,
+        layout=layout, length_dtype=length_dtype, split_tokens=split,
     )
     assert_bf16_close(actual, expected)
 
@@ -195,7 +206,7 @@ def test_decode_attention_forced_split(gpu, split):
     assert_bf16_close(actual, expected)
 
 
-@pytest.mark.parametrize("split", [0, 32, 64, 100, 5000])
+@pytest.mark.parametrize("split", [0, 32, 64, 100, 5000, SPLIT_BALANCED])
 @pytest.mark.parametrize("batch", [3, 65, 130])
 def test_decode_attention_balanced_split(gpu, batch, split):
     # The length-balanced split lays every (batch, kv-head) tile range end to
@@ -214,7 +225,44 @@ def test_decode_attention_balanced_split(gpu, batch, split):
     assert_bf16_close(actual, expected)
 
 
-@pytest.mark.parametrize("split", [0, 64])
+@pytest.mark.parametrize(
+    "batch,q_heads,kv_heads,cap,max_len",
+    [
+        (1024, 14, 2, 128, 100),   # more sequences than workgroups: the grid loops
+        (2049, 14, 2, 64, 64),     # past the balanced split's batch limit: fixed chunks
+        (5, 8, 1, 700, 700),       # one kv head: one head per wave
+        (6, 12, 4, 900, 900),      # 4 kv heads of 3 query heads: head pairs
+    ],
+)
+def test_decode_attention_balanced_shapes(gpu, batch, q_heads, kv_heads, cap, max_len):
+    announce(f"decode bf16 balanced B={batch} QH={q_heads} KVH={kv_heads} cap={cap}")
+    g = generator(batch + q_heads * 31 + cap)
+    lengths = torch.randint(1, max_len + 1, (batch,), generator=g).tolist()
+    actual, expected = _decode_case(
+        gpu, batch, q_heads, kv_heads, 64, cap, lengths, torch.bfloat16, batch + cap,
+        split_tokens=SPLIT_BALANCED, mask_kind="random",
+    )
+    assert_bf16_close(actual, expected)
+
+
+def test_decode_attention_balanced_is_deterministic(gpu):
+    # The pieces of a sequence merge in a fixed order: repeated calls on the
+    # same inputs are bitwise equal.
+    from stateful_llm_compiler_hip.backends import hip_decode_attention
+
+    announce("decode bf16 balanced determinism B=32 L=8192")
+    g = generator(5)
+    q = torch.randn(32, 14, 1, 64, generator=g).bfloat16().to(gpu)
+    k = torch.randn(32, 8192, 2, 64, generator=g).bfloat16().to(gpu)
+    v = torch.randn(32, 8192, 2, 64, generator=g).bfloat16().to(gpu)
+    lengths = torch.randint(4096, 8193, (32,), generator=g).to(gpu)
+    outs = [hip_decode_attention(q, k, v, lengths, None, scale=0.125, split_tokens=SPLIT_BALANCED)
+            for _ in range(3)]
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+@pytest.mark.parametrize("split", [0, 64, SPLIT_BALANCED])
 def test_decode_attention_empty_sequences(gpu, split):
     # A sequence with no attended token is a softmax over an empty row: NaN,
     # as in the reference; its neighbours are unaffected.
@@ -230,33 +278,37 @@ def test_decode_attention_empty_sequences(gpu, split):
     assert_bf16_close(actual[~empty], expected[~empty])
 
 
+@pytest.mark.parametrize("split", [0, SPLIT_BALANCED])
 @pytest.mark.parametrize("mask_dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("mask_len", [1000, 1001])
-def test_decode_attention_mask_dtype_and_length(gpu, mask_dtype, mask_len):
-    # A mask length that is a multiple of 4 takes the MFMA kernel (the mask is
-    # staged 4 tokens at a time); 1001 takes the generic kernel.
-    announce(f"decode bf16 mask {mask_dtype} mask_len={mask_len}")
+def test_decode_attention_mask_dtype_and_length(gpu, mask_dtype, mask_len, split):
+    # A mask length that is a multiple of 4 lets the balanced split read the
+    # mask 4 tokens per load; 1001 reads it per token.
+    announce(f"decode bf16 mask {mask_dtype} mask_len={mask_len} split_tokens={split}")
     actual, expected = _decode_case(
         gpu, 4, 14, 2, 64, 1024, [1001, 999, 3, 640], torch.bfloat16, 43,
-        mask_len=mask_len, mask_kind="random", mask_dtype=mask_dtype,
+        mask_len=mask_len, mask_kind="random", mask_dtype=mask_dtype, split_tokens=split,
     )
     assert_bf16_close(actual, expected)
 
 
-def test_decode_attention_random_mask_short_mask(gpu):
+@pytest.mark.parametrize("split", [0, SPLIT_BALANCED])
+def test_decode_attention_random_mask_short_mask(gpu, split):
     # Mask shorter than the capacity bounds the attended prefix (execution.py:301-327).
-    announce("decode bf16 mask_len < capacity, random mask")
+    announce(f"decode bf16 mask_len < capacity, random mask, split_tokens={split}")
     actual, expected = _decode_case(
         gpu, 5, 14, 2, 64, 512, [10, 300, 512, 200, 1], torch.bfloat16, 41,
-        mask_len=300, mask_kind="random",
+        mask_len=300, mask_kind="random", split_tokens=split,
     )
     assert_bf16_close(actual, expected)
 
 
+@pytest.mark.parametrize("split", [0, SPLIT_BALANCED])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_decode_attention_head_dim_128(gpu, dtype):
-    announce(f"decode {dtype} D=128 QH4 KVH2")
-    actual, expected = _decode_case(gpu, 8, 4, 2, 128, 1024, [1024, 513, 2, 700, 999, 64, 65, 1000], dtype, 51)
+def test_decode_attention_head_dim_128(gpu, dtype, split):
+    announce(f"decode {dtype} D=128 QH4 KVH2 split_tokens={split}")
+    actual, expected = _decode_case(gpu, 8, 4, 2, 128, 1024, [1024, 513, 2, 700, 999, 64, 65, 1000], dtype, 51,
+                                    split_tokens=split)
     assert_bf16_close(actual, expected)
 
 
