@@ -180,6 +180,30 @@ SLC_API int slc_hip_decode_attention(
     int64_t out_stride_h, float scale, int64_t split_tokens, int softmax_order,
     void* stream);
 
+/*
+ * slc_hip_decode_attention without allocation.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation).
+ * Same arguments and result as slc_hip_decode_attention minus the workspace
+ * and counters: the split partials (at most 8 MiB) and arrival counters (at
+ * most 131072) live in one device array of the library that each GPU holds
+ * until the process ends.  A call needing more returns
+ * SLC_ERR_INVALID_ARGUMENT before any device work.  The first call on a GPU
+ * launches one small kernel on `stream` to zero the counters; no call
+ * allocates.  All calls on one GPU share its array: calls that overlap in
+ * time on one GPU (other streams, other threads) race; calls on one stream
+ * do not.
+ */
+SLC_API int slc_hip_decode_attention_noalloc(
+    const void* query, const void* key_buffer, const void* value_buffer,
+    const void* lengths, int lengths_dtype, const void* mask, int mask_dtype,
+    void* output, int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
+    int64_t head_dim, int64_t capacity, int64_t mask_len, int64_t q_stride_b,
+    int64_t q_stride_h, int64_t kv_stride_b, int64_t kv_stride_s, int64_t kv_stride_h,
+    int64_t mask_stride_b, int64_t mask_stride_s, int64_t out_stride_b,
+    int64_t out_stride_h, float scale, int64_t split_tokens, int softmax_order,
+    void* stream);
+
 /* Longest mask the SLC_SOFTMAX_EXACT order takes (INT64_MAX: no limit). */
 SLC_API int64_t slc_hip_decode_attention_exact_max_tokens(int64_t head_dim, int dtype);
 

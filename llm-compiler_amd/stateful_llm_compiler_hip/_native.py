@@ -86,6 +86,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         + [_L] * 15
         + [_F, _L, _I, _P],
     ),
+    "slc_hip_decode_attention_noalloc": (
+        _I,
+        [_P, _P, _P, _P, _I, _P, _I, _P, _I] + [_L] * 15 + [_F, _L, _I, _P],
+    ),
     "slc_hip_decode_attention_exact_max_tokens": (_L, [_L, _I]),
     "slc_hip_decode_attention_counter_count": (_L, [_L, _L]),
     "slc_hip_rms_norm": (

@@ -1,6 +1,10 @@
 """gfx950 kernel wrappers (drop-ins for the reference's backends/triton_*)."""
 
-from .hip_attention import hip_decode_attention, hip_rope_decode_attention
+from .hip_attention import (
+    hip_decode_attention,
+    hip_decode_attention_noalloc,
+    hip_rope_decode_attention,
+)
 from .hip_fused import (
     hip_linear_residual,
     hip_norm_linear_group,
@@ -29,6 +33,7 @@ __all__ = [
     "hip_rope_table",
     "hip_swiglu",
     "hip_decode_attention",
+    "hip_decode_attention_noalloc",
     "hip_rope_decode_attention",
     "hip_linear_residual",
     "hip_norm_linear_group",

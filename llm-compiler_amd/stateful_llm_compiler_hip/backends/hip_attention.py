@@ -34,38 +34,10 @@ def exact_max_tokens(head_dim: int, dtype: torch.dtype) -> int:
         head_dim, _native.dtype_tag(dtype)))
 
 
-def hip_decode_attention(
-    query: torch.Tensor,
-    key_buffer: torch.Tensor,
-    value_buffer: torch.Tensor,
-    lengths: torch.Tensor,
-    attention_mask: torch.Tensor | None,
-    *,
-    scale: float,
-    split_tokens: int = 0,
-    softmax_order: str = "online",
-    workspace: _native.DeviceWorkspace | None = None,
-) -> torch.Tensor:
-    """B x H x 1 x D GQA decode attention over a B x Cap x KVH x D buffer.
+def _check_decode_operands(query, key_buffer, value_buffer, lengths, attention_mask):
+    """The reference wrapper's operand checks (triton_attention.py:152-180);
+    returns (batch, query_heads, head_dim, capacity, kv_heads)."""
 
-    ``key_buffer``/``value_buffer`` are indexed ``[b, s, h, :]``; the
-    reference's contiguous_bshd buffers are the normal case, and any view with
-    a contiguous head dim and equal K/V strides (for example a BHSD buffer
-    permuted to BSHD) is accepted.  ``lengths`` is int64 (the runtime's
-    dtype) or int32.  ``attention_mask`` is B x 1 x 1 x S additive, or None
-    for an all-zero mask over the whole capacity.
-
-    ``split_tokens``: 0 picks a fixed chunk per (batch, kv head) sized to fill
-    the GPU, > 0 a fixed chunk of that many tokens, ``SPLIT_BALANCED`` (-1)
-    the length-balanced split (pieces sized from the device-side lengths).
-    ``softmax_order``: "online" (the reference Triton kernel's single-pass
-    form, the default) or "exact" (normalise, round, then P.V -- the
-    reference executor's order; masks up to ``exact_max_tokens`` long).
-    ``workspace``: the caller's ``DeviceWorkspace`` (else the current
-    stream's); calls that may run concurrently need separate ones.
-    """
-
-    order = _native.softmax_order_tag(softmax_order)
     tensors = [query, key_buffer, value_buffer, lengths]
     if attention_mask is not None:
         tensors.append(attention_mask)
@@ -119,23 +91,62 @@ def hip_decode_attention(
     if head_dim > 256:
         raise ValueError("HIP decode attention: head_dim above 256")
 
+    return batch, query_heads, head_dim, capacity, kv_heads
+
+
+def _mask_args(attention_mask, capacity):
+    if attention_mask is None:
+        return None, 0, 0, 0, capacity
+    return (attention_mask.data_ptr(), _native.dtype_tag(attention_mask.dtype),
+            attention_mask.stride(0), attention_mask.stride(3), attention_mask.shape[-1])
+
+
+def hip_decode_attention(
+    query: torch.Tensor,
+    key_buffer: torch.Tensor,
+    value_buffer: torch.Tensor,
+    lengths: torch.Tensor,
+    attention_mask: torch.Tensor | None,
+    *,
+    scale: float,
+    split_tokens: int = 0,
+    softmax_order: str = "online",
+    workspace: _native.DeviceWorkspace | None = None,
+) -> torch.Tensor:
+    """B x H x 1 x D GQA decode attention over a B x Cap x KVH x D buffer.
+
+    ``key_buffer``/``value_buffer`` are indexed ``[b, s, h, :]``; the
+    reference's contiguous_bshd buffers are the normal case, and any view with
+    a contiguous head dim and equal K/V strides (for example a BHSD buffer
+    permuted to BSHD) is accepted.  ``lengths`` is int64 (the runtime's
+    dtype) or int32.  ``attention_mask`` is B x 1 x 1 x S additive, or None
+    for an all-zero mask over the whole capacity.
+
+    ``split_tokens``: 0 picks a fixed chunk per (batch, kv head) sized to fill
+    the GPU, > 0 a fixed chunk of that many tokens, ``SPLIT_BALANCED`` (-1)
+    the length-balanced split (pieces sized from the device-side lengths).
+    ``softmax_order``: "online" (the reference Triton kernel's single-pass
+    form, the default) or "exact" (normalise, round, then P.V -- the
+    reference executor's order; masks up to ``exact_max_tokens`` long).
+    ``workspace``: the caller's ``DeviceWorkspace`` (else the current
+    stream's); calls that may run concurrently need separate ones.
+    """
+
+    order = _native.softmax_order_tag(softmax_order)
+    batch, query_heads, head_dim, capacity, kv_heads = _check_decode_operands(
+        query, key_buffer, value_buffer, lengths, attention_mask)
+
     lib = _native.library()
     output = torch.empty_like(query)
     if batch == 0:
         return output
     dtype = _native.dtype_tag(query.dtype)
-    mask_len = capacity if attention_mask is None else attention_mask.shape[-1]
+    mask_ptr, mask_dtype, mask_sb, mask_ss, mask_len = _mask_args(attention_mask, capacity)
     nbytes = lib.slc_hip_decode_attention_workspace_size(
         batch, query_heads, head_dim, mask_len, kv_heads, dtype, split_tokens
     )
     stream = _native.current_stream(query.device)
     buffer, counters, count = _workspace(lib, query.device, nbytes, batch, kv_heads, workspace)
-    if attention_mask is None:
-        mask_ptr, mask_dtype, mask_sb, mask_ss = None, 0, 0, 0
-    else:
-        mask_ptr = attention_mask.data_ptr()
-        mask_dtype = _native.dtype_tag(attention_mask.dtype)
-        mask_sb, mask_ss = attention_mask.stride(0), attention_mask.stride(3)
     status = lib.slc_hip_decode_attention(
         query.data_ptr(),
         key_buffer.data_ptr(),
@@ -171,6 +182,45 @@ def hip_decode_attention(
         stream,
     )
     _native.check(status, "slc_hip_decode_attention")
+    return output
+
+
+def hip_decode_attention_noalloc(
+    query: torch.Tensor,
+    key_buffer: torch.Tensor,
+    value_buffer: torch.Tensor,
+    lengths: torch.Tensor,
+    attention_mask: torch.Tensor | None,
+    output: torch.Tensor,
+    *,
+    scale: float,
+    split_tokens: int = 0,
+    softmax_order: str = "online",
+) -> torch.Tensor:
+    """``hip_decode_attention`` into the caller's ``output`` through the entry
+    point that allocates nothing (``slc_hip_decode_attention_noalloc``): its
+    split partials and counters live in the library's own device array, so
+    the call makes no device allocation at all.  Calls that overlap in time on
+    one GPU share that array and race."""
+
+    order = _native.softmax_order_tag(softmax_order)
+    batch, query_heads, head_dim, capacity, kv_heads = _check_decode_operands(
+        query, key_buffer, value_buffer, lengths, attention_mask)
+    if not output.is_cuda or output.shape != query.shape or output.dtype != query.dtype:
+        raise ValueError("HIP decode attention: output must be a GPU tensor shaped like the query")
+    if output.stride(-1) != 1:
+        raise ValueError("HIP decode attention: output head dim must be contiguous")
+    lib = _native.library()
+    mask_ptr, mask_dtype, mask_sb, mask_ss, mask_len = _mask_args(attention_mask, capacity)
+    status = lib.slc_hip_decode_attention_noalloc(
+        query.data_ptr(), key_buffer.data_ptr(), value_buffer.data_ptr(), lengths.data_ptr(),
+        _native.dtype_tag(lengths.dtype), mask_ptr, mask_dtype, output.data_ptr(),
+        _native.dtype_tag(query.dtype), batch, query_heads, kv_heads, head_dim, capacity,
+        mask_len, query.stride(0), query.stride(1), key_buffer.stride(0), key_buffer.stride(1),
+        key_buffer.stride(2), mask_sb, mask_ss, output.stride(0), output.stride(1),
+        float(scale), int(split_tokens), order, _native.current_stream(query.device),
+    )
+    _native.check(status, "slc_hip_decode_attention_noalloc")
     return output
 
 

@@ -1212,6 +1212,97 @@ extern "C" int slc_hip_decode_attention(
   }
 }
 
+// ---- decode attention without allocation ------------------------------------
+// For callers that cannot allocate device memory (code under HIP graph
+// capture, tight serving loops, harnesses that forbid it): the split partials
+// and arrival counters live in one file-scope device array instead of a
+// caller workspace.  Each GPU holds its own copy until the process ends; the
+// host never passes the array's name to a kernel, only the address that
+// hipGetSymbolAddress returns for the current device.
+namespace {
+
+constexpr int64_t kNoAllocCounterInts = 131072;              // 512 KiB of counters
+constexpr int64_t kNoAllocPartialBytes = int64_t{8} << 20;   // 8 MiB of partials
+constexpr int64_t kNoAllocBytes = kNoAllocCounterInts * 4 + kNoAllocPartialBytes;
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+__global__ void zero_ints_kernel(int* p, int64_t n) {
+  for (int64_t i = blockIdx.x * int64_t{blockDim.x} + threadIdx.x; i < n;
+       i += int64_t{gridDim.x} * blockDim.x)
+    p[i] = 0;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of `scratch`, set up on the first call on that
+// device: its address, and the counters zeroed by a small kernel on the
+// caller's stream (a kernel, not a memset, so that a first call under graph
+// capture records nothing a replay mishandles).  Every later call leaves the
+// counters zero again.
+int noalloc_scratch(hipStream_t stream, unsigned char** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    slc_host::set_error("slc_hip_decode_attention_noalloc: no usable current device");
+    return SLC_ERR_INVALID_ARGUMENT;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (rc != hipSuccess || ptr == nullptr) {
+      slc_host::set_error("slc_hip_decode_attention_noalloc: hipGetSymbolAddress failed: %s",
+                          hipGetErrorString(rc));
+      return static_cast<int>(rc != hipSuccess ? rc : hipErrorInvalidSymbol);
+    }
+    hipLaunchKernelGGL(zero_ints_kernel, dim3(128), dim3(256), 0, stream,
+                       static_cast<int*>(ptr), kNoAllocCounterInts);
+    const int launch = slc_host::check_launch("slc_hip_decode_attention_noalloc(zero counters)");
+    if (launch != SLC_OK) return launch;
+    g_scratch_ptr[dev] = static_cast<unsigned char*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return SLC_OK;
+}
+
+}  // namespace
+
+extern "C" int slc_hip_decode_attention_noalloc(
+    const void* query, const void* key_buffer, const void* value_buffer,
+    const void* lengths, int lengths_dtype, const void* mask, int mask_dtype,
+    void* output, int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
+    int64_t head_dim, int64_t capacity, int64_t mask_len, int64_t q_stride_b,
+    int64_t q_stride_h, int64_t kv_stride_b, int64_t kv_stride_s, int64_t kv_stride_h,
+    int64_t mask_stride_b, int64_t mask_stride_s, int64_t out_stride_b,
+    int64_t out_stride_h, float scale, int64_t split_tokens, int softmax_order,
+    void* stream) {
+  // Sizes first: a call the array cannot hold fails before any device call.
+  SLC_REQUIRE(batch >= 0 && q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0 &&
+                  mask_len >= 0,
+              "slc_hip_decode_attention_noalloc: bad sizes");
+  const int64_t partials = slc_hip_decode_attention_workspace_size(
+      batch, q_heads, head_dim, mask_len, kv_heads, dtype, split_tokens);
+  const int64_t counters = slc_hip_decode_attention_counter_count(batch, kv_heads);
+  SLC_REQUIRE(partials <= kNoAllocPartialBytes && counters <= kNoAllocCounterInts,
+              "slc_hip_decode_attention_noalloc: the call needs %lld bytes of partials and "
+              "%lld counters; the no-alloc scratch holds at most %lld and %lld",
+              (long long)partials, (long long)counters, (long long)kNoAllocPartialBytes,
+              (long long)kNoAllocCounterInts);
+  if (batch == 0) return SLC_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  unsigned char* base = nullptr;
+  const int rc = noalloc_scratch(s, &base);
+  if (rc != SLC_OK) return rc;
+  return slc_hip_decode_attention(
+      query, key_buffer, value_buffer, lengths, lengths_dtype, mask, mask_dtype, output,
+      base + kNoAllocCounterInts * 4, kNoAllocPartialBytes, reinterpret_cast<int*>(base),
+      kNoAllocCounterInts, dtype, batch, q_heads, kv_heads, head_dim, capacity, mask_len,
+      q_stride_b, q_stride_h, kv_stride_b, kv_stride_s, kv_stride_h, mask_stride_b,
+      mask_stride_s, out_stride_b, out_stride_h, scale, split_tokens, softmax_order, stream);
+}
+
 extern "C" int slc_hip_rope_decode_attention(
     const void* query, const void* key, const void* value, const void* cosine,
     const void* sine, void* key_buffer, void* value_buffer, const int64_t* lengths,
