@@ -216,12 +216,19 @@ SLC_API int64_t slc_hip_decode_attention_exact_max_tokens(int64_t head_dim, int 
  * have stride out_stride_row.  norm_dtype is the dtype the normalized value
  * is materialised in before the weight multiply (the reference's
  * output_dtype or the input dtype).
+ * waves_per_row picks the kernel variant -- the gfx950 counterpart of the
+ * reference plan's num_warps: 1 = one wavefront per row, the row held in
+ * registers (one HBM read and write; same dtype throughout, 16-byte aligned
+ * rows of at most 512 vectors); 4 = a 256-thread workgroup per row (any
+ * dtypes; the second pass re-reads the row from L2); 0 = the first when it
+ * applies, else the second.  A variant that does not apply falls back to 4.
  */
 SLC_API int slc_hip_rms_norm(const void* input, const void* weight, void* output,
                      int in_dtype, int weight_dtype, int out_dtype,
                      int norm_dtype, int64_t rows, int64_t hidden,
                      int64_t in_stride_row, int64_t out_stride_row,
-                     float epsilon, int round_before_weight, void* stream);
+                     float epsilon, int round_before_weight, int waves_per_row,
+                     void* stream);
 
 /*
  * rope (dual output, Qwen2 half rotation):

@@ -94,7 +94,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "slc_hip_decode_attention_counter_count": (_L, [_L, _L]),
     "slc_hip_rms_norm": (
         _I,
-        [_P, _P, _P, _I, _I, _I, _I, _L, _L, _L, _L, _F, _I, _P],
+        [_P, _P, _P, _I, _I, _I, _I, _L, _L, _L, _L, _F, _I, _I, _P],
     ),
     "slc_hip_linear": (
         _I,

@@ -48,11 +48,15 @@ def hip_rms_norm(
 ) -> torch.Tensor:
     """RMSNorm of ``tensor`` over its last axis.
 
-    ``num_warps`` is accepted for signature compatibility with the reference's
-    profile plans; the gfx950 kernel always maps one wavefront per row.
+    ``num_warps`` keeps the reference's meaning of the launch width a profile
+    plan picked, in gfx950 terms: wavefronts per row, 1 (the row in one wave's
+    registers) or 4 (a 256-thread workgroup per row); None picks the first
+    where it applies.
     """
 
-    del num_warps
+    waves = 0 if num_warps is None else int(num_warps)
+    if waves not in (0, 1, 4):
+        raise ValueError(f"HIP RMSNorm: num_warps (waves per row) must be 1 or 4, got {num_warps}")
     if not tensor.is_cuda or not weight.is_cuda:
         raise ValueError("HIP RMSNorm: input and weight must be on the GPU")
     if tensor.ndim < 1:
@@ -100,6 +104,7 @@ def hip_rms_norm(
         hidden,
         float(epsilon),
         1 if round_before_weight else 0,
+        waves,
         _native.current_stream(tensor.device),
     )
     _native.check(status, "slc_hip_rms_norm")

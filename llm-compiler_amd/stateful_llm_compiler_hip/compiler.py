@@ -2,8 +2,9 @@
 
 Mirrors the reference's ``compile_exported_program`` / ``CompileOptions``
 (src/stateful_llm_compiler/compiler.py:25-79) for graphs that already are
-ServeIR: optional profile-guided RMSNorm plans, the KernelIR lowering in the
-chosen numerical mode, and ``require_full_lowering`` when strict.
+ServeIR: optional profile-guided plans of kernel variants (RMSNorm launch
+width, decode-attention split), the KernelIR lowering in the chosen numerical
+mode, and ``require_full_lowering`` when strict.
 """
 
 from __future__ import annotations
@@ -12,19 +13,20 @@ from dataclasses import dataclass, field
 from pathlib import Path
 from typing import Any
 
-from .cost_model import RMSNormCostModel
+from .cost_model import KernelProfile
 from .ir import Module
 from .lowering import LoweringCoverage, LowerToKernelIRPass, analyze_lowering_coverage, require_full_lowering
 from .pass_manager import PassManager, PassResult, operation_counts
-from .passes import FuseDecodeKernelsPass, SelectRMSNormLoweringPass
+from .passes import FuseDecodeKernelsPass, SelectDecodeSplitPass, SelectRMSNormLoweringPass
 
 
 @dataclass(frozen=True)
 class CompileOptions:
     numerical_mode: str = "fast"
     require_full_lowering: bool = True
+    # Schema-v1 profile (the reference's option name): its RMSNorm rows plan
+    # serve.rms_norm, its decode_attention rows (an extension) the split.
     rmsnorm_profile: str | Path | None = None
-    rmsnorm_fallback: str = "hip"
     # Fuse decode-step op chains into single kernels (fast mode only; the
     # fused kernels are bit-identical to the chains they replace).
     fuse: bool = True
@@ -57,8 +59,9 @@ def compile_module(module: Module, options: CompileOptions | None = None) -> Com
     options = options or CompileOptions()
     manager = PassManager()
     if options.rmsnorm_profile is not None:
-        manager.add(SelectRMSNormLoweringPass(RMSNormCostModel.load(options.rmsnorm_profile),
-                                              fallback=options.rmsnorm_fallback))
+        profile = KernelProfile.load(options.rmsnorm_profile)
+        manager.add(SelectRMSNormLoweringPass(profile))
+        manager.add(SelectDecodeSplitPass(profile))
     manager.add(LowerToKernelIRPass(numerical_mode=options.numerical_mode,
                                     attention_softmax=options.attention_softmax,
                                     linear_backend=options.linear_backend))

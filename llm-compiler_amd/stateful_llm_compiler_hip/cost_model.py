@@ -1,220 +1,245 @@
-"""Profile-guided lowering plans for ``serve.rms_norm``.
+"""Profile-guided choice of gfx950 kernel variants.
 
-Restates the reference's cost model (src/stateful_llm_compiler/cost_model.py:
-1-324): a schema-v1 profile of measured latencies per (rows, hidden, dtype)
-becomes row buckets split at the geometric midpoints of neighbouring
-measurements; each bucket picks its cheapest backend; at run time
-``resolve_lowering_plan`` maps the actual row count to a decision.  The gfx950
-backend adds the ``hip`` backend name; profiles measured on MI355X list it
-next to (or instead of) the reference's names.
+The reference plans ``serve.rms_norm`` from a schema-v1 profile of measured
+latencies (src/stateful_llm_compiler/cost_model.py:93-123 reads the format,
+benchmarks/bench_rmsnorm.py:183-208 writes it) and picks a *backend*
+(native / triton / inductor) per row bucket.  None of those backends exists
+here: every op runs a hand-written HIP kernel.  What does vary is which HIP
+kernel an op launches, so this module plans *variants*:
+
+* ``rms_norm``: ``wave`` (one wavefront per row, the row held in registers)
+  or ``block`` (a 256-thread workgroup per row); the run-time axis is the row
+  count.
+* ``decode_attention``: ``fixed`` (a fixed chunk per (batch, kv head), sized
+  to fill the GPU), ``balanced`` (the length-balanced split) or ``chunk<N>``
+  (a fixed chunk of N tokens); the run-time axis is batch x mask length.
+
+A profile keeps the schema-v1 layout -- ``schema_version``, ``target`` and a
+``results`` list of RMSNorm rows keyed ``rows`` / ``hidden_size`` / ``dtype``,
+so a reference profile loads unchanged -- and adds per-row ``hip_variants``
+(variant -> microseconds) plus a ``decode_attention`` list of the same form.
+A reference row without ``hip_variants`` contributes its ``hip_us`` (if any)
+as the automatic variant and nothing else.
+
+A plan is the op's measured samples, attached to the op as an attribute.  At
+run time every variant's latency is interpolated linearly in log(size)
+between the two samples around the actual size (outside the sampled range the
+end sample stands), and the call launches the variant with the lowest
+estimate.  Ties go to the variant listed first in ``VARIANTS``.
 """
 
 from __future__ import annotations
 
 import json
 import math
-from dataclasses import asdict, dataclass
+import re
+from dataclasses import dataclass, field
 from pathlib import Path
-from typing import Any, Iterable
+from typing import Any, Mapping
 
-BACKENDS = ("hip", "triton", "inductor", "native")
+SCHEMA_VERSION = 1
+
+# Variants each op can launch, in tie-break order; "auto" lets the kernel
+# library decide (a reference row's hip_us stands for it).
+VARIANTS: dict[str, tuple[str, ...]] = {
+    "rms_norm": ("auto", "wave", "block"),
+    "decode_attention": ("auto", "fixed", "balanced"),
+}
+_CHUNK = re.compile(r"chunk(\d+)$")
+
+_DTYPES = {"f16": "fp16", "float16": "fp16", "fp16": "fp16", "half": "fp16",
+           "bf16": "bf16", "bfloat16": "bf16", "f32": "fp32", "float32": "fp32",
+           "fp32": "fp32", "float": "fp32"}
 
 
 class ProfileError(ValueError):
-    pass
+    """A profile or plan that cannot be used."""
+
+
+def canonical_dtype(dtype: Any) -> str:
+    name = str(dtype).rsplit(".", 1)[-1].lower()
+    if name not in _DTYPES:
+        raise ProfileError(f"unsupported dtype {dtype!r}")
+    return _DTYPES[name]
+
+
+def _known_variant(op: str, variant: str) -> bool:
+    return variant in VARIANTS[op] or (op == "decode_attention" and _CHUNK.match(variant) is not None)
 
 
 @dataclass(frozen=True)
-class TargetProfile:
-    device_name: str = "unknown"
-    compute_capability: str = "unknown"
-    torch_version: str = "unknown"
-    triton_version: str = "unknown"
+class VariantChoice:
+    """What a call launches and why."""
 
-
-@dataclass(frozen=True)
-class RMSNormProfileEntry:
-    rows: int
-    hidden_size: int
-    dtype: str
-    native_us: float
-    triton_us: float | None = None
-    inductor_us: float | None = None
-    hip_us: float | None = None
-
-    def backend_costs(self) -> dict[str, float]:
-        costs = {"native": self.native_us}
-        for name, value in (("triton", self.triton_us), ("inductor", self.inductor_us),
-                            ("hip", self.hip_us)):
-            if value is not None:
-                costs[name] = value
-        return costs
-
-
-@dataclass(frozen=True)
-class LoweringVariant:
-    min_rows: int
-    max_rows: int | None
-    profile_rows: int
-    backend: str
-    estimated_us: float
-    num_warps: int | None = None
-
-    def contains(self, rows: int) -> bool:
-        return rows >= self.min_rows and (self.max_rows is None or rows <= self.max_rows)
-
-
-@dataclass(frozen=True)
-class LoweringDecision:
-    backend: str
-    source: str
-    profile_rows: int | None = None
+    variant: str
+    source: str                     # "profile" or "default"
+    size: int
     estimated_us: float | None = None
-    num_warps: int | None = None
 
 
-class RMSNormCostModel:
-    """Row-bucketed lowering plans built from discrete measurements."""
+@dataclass
+class VariantCurve:
+    """Measured latencies of one op's variants at a few sizes of its run-time
+    axis, for one static configuration.  Samples of equal size (for decode
+    attention: different batch / length splits of the same work) average."""
 
-    def __init__(self, target: TargetProfile, entries: Iterable[RMSNormProfileEntry], *,
-                 source: str = "memory") -> None:
-        self.target = target
-        self.entries = tuple(entries)
-        self.source = source
-        if not self.entries:
-            raise ProfileError("a profile needs at least one measurement")
-        _validate_entries(self.entries)
+    op: str
+    static: tuple[tuple[str, Any], ...]
+    axis: str
+    samples: dict[int, dict[str, list[float]]] = field(default_factory=dict)
+    _seen: set = field(default_factory=set)
 
-    @classmethod
-    def load(cls, path: str | Path) -> "RMSNormCostModel":
-        path = Path(path)
-        return cls.from_dict(json.loads(path.read_text(encoding="utf-8")), source=str(path))
+    def add(self, size: int, latencies: Mapping[str, float], *, key: Any = None) -> None:
+        if size <= 0:
+            raise ProfileError(f"{self.op}: sample size must be positive, got {size}")
+        key = size if key is None else key
+        if key in self._seen:
+            raise ProfileError(f"{self.op} {dict(self.static)}: two samples of {key}")
+        self._seen.add(key)
+        for variant, value in latencies.items():
+            if not _known_variant(self.op, variant):
+                raise ProfileError(f"{self.op}: unknown variant {variant!r}")
+            value = float(value)
+            if not math.isfinite(value) or value <= 0:
+                raise ProfileError(f"{self.op}: latency of {variant} must be finite and positive")
+            self.samples.setdefault(size, {}).setdefault(variant, []).append(value)
 
-    @classmethod
-    def from_dict(cls, payload: Any, *, source: str = "memory") -> "RMSNormCostModel":
-        if isinstance(payload, list):  # legacy: bare list of rows
-            target_data: dict[str, Any] = {}
-            rows = payload
-        elif isinstance(payload, dict):
-            if payload.get("schema_version") != 1:
-                raise ProfileError("unsupported profile schema_version")
-            target_data = payload.get("target", {})
-            rows = payload.get("results", [])
-        else:
-            raise ProfileError("a profile must be an object or a list")
-        target = TargetProfile(
-            device_name=str(target_data.get("device_name", "unknown")),
-            compute_capability=str(target_data.get("compute_capability", "unknown")),
-            torch_version=str(target_data.get("torch_version", "unknown")),
-            triton_version=str(target_data.get("triton_version", "unknown")),
-        )
-        return cls(target, [_parse_entry(row) for row in rows], source=source)
-
-    def variants(self, hidden_size: int, dtype: str, *,
-                 allowed_backends: Iterable[str] = BACKENDS) -> list[LoweringVariant]:
-        dtype = normalize_dtype(dtype)
-        allowed = set(allowed_backends)
-        candidates = sorted(
-            (e for e in self.entries if e.hidden_size == hidden_size and e.dtype == dtype),
-            key=lambda e: e.rows,
-        )
-        if not candidates:
-            return []
-        thresholds = [math.floor(math.sqrt(a.rows * b.rows)) for a, b in zip(candidates, candidates[1:])]
-        variants = []
-        minimum = 1
-        for index, entry in enumerate(candidates):
-            maximum = thresholds[index] if index < len(thresholds) else None
-            costs = {k: v for k, v in entry.backend_costs().items() if k in allowed}
-            if not costs:
-                raise ProfileError(f"M={entry.rows},N={hidden_size},{dtype} has no allowed backend")
-            backend = min(costs, key=costs.get)
-            variants.append(LoweringVariant(
-                min_rows=minimum, max_rows=maximum, profile_rows=entry.rows, backend=backend,
-                estimated_us=costs[backend],
-                num_warps=select_num_warps(entry.rows, hidden_size) if backend in ("triton", "hip") else None,
-            ))
-            minimum = maximum + 1 if maximum is not None else minimum
-        return variants
-
-    def plan_attribute(self, hidden_size: int, dtype: str, *, fallback: str = "hip",
-                       allowed_backends: Iterable[str] = BACKENDS) -> dict[str, Any]:
+    def to_plan(self, source: str, target: Mapping[str, Any]) -> dict[str, Any]:
         return {
-            "schema_version": 1,
-            "profile_source": self.source,
-            "target": asdict(self.target),
-            "hidden_size": hidden_size,
-            "dtype": normalize_dtype(dtype),
-            "fallback": fallback,
-            "variants": [asdict(v) for v in self.variants(hidden_size, dtype, allowed_backends=allowed_backends)],
+            "schema_version": SCHEMA_VERSION,
+            "op": self.op,
+            "axis": self.axis,
+            "static": dict(self.static),
+            "profile_source": source,
+            "target": dict(target),
+            "samples": [{"size": size,
+                         "latency_us": {v: sum(xs) / len(xs) for v, xs in self.samples[size].items()}}
+                        for size in sorted(self.samples)],
         }
 
 
-def select_variant(variants: Iterable[LoweringVariant] | Iterable[dict[str, Any]], rows: int) -> LoweringVariant | None:
-    for item in variants:
-        variant = item if isinstance(item, LoweringVariant) else LoweringVariant(**item)
-        if variant.contains(rows):
-            return variant
-    return None
+def _estimate(points: list[tuple[float, float]], x: float) -> float:
+    """Piecewise-linear value at x of points sorted by their first element;
+    flat beyond the ends."""
+
+    if x <= points[0][0]:
+        return points[0][1]
+    for (x0, y0), (x1, y1) in zip(points, points[1:]):
+        if x <= x1:
+            return y0 + (y1 - y0) * (x - x0) / (x1 - x0)
+    return points[-1][1]
 
 
-def resolve_lowering_plan(plan: dict[str, Any] | None, rows: int, *,
-                          default_backend: str = "hip") -> LoweringDecision:
-    """Map the run-time row count onto a compile-time plan (cost_model.py:220-245)."""
+def choose_variant(plan: Mapping[str, Any] | None, size: int, *,
+                   allowed: tuple[str, ...] | None = None) -> VariantChoice:
+    """The variant with the lowest interpolated latency at ``size``."""
 
-    if rows <= 0:
-        raise ProfileError("run-time rows must be positive")
+    if size <= 0:
+        raise ProfileError("run-time size must be positive")
     if not plan:
-        return LoweringDecision(default_backend, "default")
-    variant = select_variant(plan.get("variants", []), rows)
-    if variant is None:
-        return LoweringDecision(str(plan.get("fallback", default_backend)), "fallback")
-    return LoweringDecision(
-        backend=variant.backend, source="profile", profile_rows=variant.profile_rows,
-        estimated_us=variant.estimated_us, num_warps=variant.num_warps,
+        return VariantChoice("auto", "default", size)
+    op = plan.get("op")
+    if op not in VARIANTS:
+        raise ProfileError(f"plan for unknown op {op!r}")
+    curves: dict[str, list[tuple[float, float]]] = {}
+    for sample in plan.get("samples", []):
+        x = math.log(float(sample["size"]))
+        for variant, value in sample["latency_us"].items():
+            if allowed is None or variant in allowed:
+                curves.setdefault(variant, []).append((x, float(value)))
+    if not curves:
+        return VariantChoice("auto", "default", size)
+    x = math.log(float(size))
+    order = {name: i for i, name in enumerate(VARIANTS[op])}
+    best = min(
+        ((name, _estimate(sorted(points), x)) for name, points in curves.items()),
+        key=lambda item: (item[1], order.get(item[0], len(order)), item[0]),
     )
+    return VariantChoice(best[0], "profile", size, best[1])
 
 
-def select_num_warps(rows: int, hidden_size: int) -> int:
-    block = 1 << max(0, hidden_size - 1).bit_length()
-    if block < 2048:
-        return 4
-    if 4 <= rows <= 16:
-        return 4
-    return 8
+def waves_per_row(variant: str) -> int:
+    """rms_norm variant -> the waves_per_row argument of slc_hip_rms_norm."""
+
+    return {"auto": 0, "wave": 1, "block": 4}[variant]
 
 
-def normalize_dtype(dtype: str) -> str:
-    aliases = {"f16": "fp16", "float16": "fp16", "fp16": "fp16", "bf16": "bf16",
-               "bfloat16": "bf16", "f32": "fp32", "float32": "fp32", "fp32": "fp32"}
-    try:
-        return aliases[str(dtype).lower()]
-    except KeyError as error:
-        raise ProfileError(f"unsupported dtype {dtype}") from error
+def split_tokens(variant: str) -> int:
+    """decode_attention variant -> the split_tokens argument of
+    slc_hip_decode_attention (SLC_SPLIT_BALANCED is -1)."""
+
+    if variant in ("auto", "fixed"):
+        return 0
+    if variant == "balanced":
+        return -1
+    match = _CHUNK.match(variant)
+    if match is None:
+        raise ProfileError(f"not a decode attention variant: {variant!r}")
+    return int(match.group(1))
 
 
-def _parse_entry(row: dict[str, Any]) -> RMSNormProfileEntry:
-    try:
-        def opt(key: str) -> float | None:
-            return float(row[key]) if row.get(key) is not None else None
+class KernelProfile:
+    """A loaded schema-v1 profile: variant curves per (op, static key)."""
 
-        return RMSNormProfileEntry(
-            rows=int(row["rows"]), hidden_size=int(row["hidden_size"]),
-            dtype=normalize_dtype(str(row["dtype"])), native_us=float(row["native_eager_us"]),
-            triton_us=opt("triton_us"), inductor_us=opt("inductor_us"), hip_us=opt("hip_us"),
-        )
-    except (KeyError, TypeError, ValueError) as error:
-        raise ProfileError(f"illegal profile row: {row}") from error
+    def __init__(self, target: Mapping[str, Any], curves: list[VariantCurve], *,
+                 source: str = "memory") -> None:
+        self.target = dict(target)
+        self.source = source
+        self.curves = {(curve.op, curve.static): curve for curve in curves}
 
+    @classmethod
+    def load(cls, path: str | Path) -> "KernelProfile":
+        path = Path(path)
+        try:
+            payload = json.loads(path.read_text(encoding="utf-8"))
+        except (OSError, json.JSONDecodeError) as error:
+            raise ProfileError(f"cannot read profile {path}: {error}") from error
+        return cls.from_dict(payload, source=str(path))
 
-def _validate_entries(entries: tuple[RMSNormProfileEntry, ...]) -> None:
-    keys = set()
-    for entry in entries:
-        if entry.rows <= 0 or entry.hidden_size <= 0:
-            raise ProfileError("rows and hidden size must be positive")
-        if any(not math.isfinite(c) or c <= 0 for c in entry.backend_costs().values()):
-            raise ProfileError("backend latencies must be finite and positive")
-        key = (entry.rows, entry.hidden_size, entry.dtype)
-        if key in keys:
-            raise ProfileError(f"duplicate measurement {key}")
-        keys.add(key)
+    @classmethod
+    def from_dict(cls, payload: Any, *, source: str = "memory") -> "KernelProfile":
+        if isinstance(payload, list):  # early profiles: the results list alone
+            payload = {"schema_version": SCHEMA_VERSION, "results": payload}
+        if not isinstance(payload, dict) or payload.get("schema_version") != SCHEMA_VERSION:
+            raise ProfileError("a profile must be a schema_version 1 object")
+        curves: dict[tuple[str, tuple], VariantCurve] = {}
+
+        def curve(op, static, axis):
+            key = (op, static)
+            if key not in curves:
+                curves[key] = VariantCurve(op, static, axis)
+            return curves[key]
+
+        for row in payload.get("results", []) or []:
+            try:
+                static = (("hidden_size", int(row["hidden_size"])),
+                          ("dtype", canonical_dtype(row["dtype"])))
+                size = int(row["rows"])
+            except (KeyError, TypeError, ValueError) as error:
+                raise ProfileError(f"illegal rms_norm row {row!r}") from error
+            latencies = dict(row.get("hip_variants") or {})
+            if not latencies and row.get("hip_us") is not None:
+                latencies = {"auto": row["hip_us"]}
+            curve("rms_norm", static, "rows").add(size, latencies)
+        for row in payload.get("decode_attention", []) or []:
+            try:
+                static = (("q_heads", int(row["q_heads"])), ("kv_heads", int(row["kv_heads"])),
+                          ("head_dim", int(row["head_dim"])), ("dtype", canonical_dtype(row["dtype"])))
+                size = int(row["batch"]) * int(row["mask_len"])
+            except (KeyError, TypeError, ValueError) as error:
+                raise ProfileError(f"illegal decode_attention row {row!r}") from error
+            curve("decode_attention", static, "batch*mask_len").add(
+                size, row.get("hip_variants") or {}, key=(int(row["batch"]), int(row["mask_len"])))
+        return cls(payload.get("target") or {}, [c for c in curves.values() if c.samples],
+                   source=source)
+
+    def plan(self, op: str, **static: Any) -> dict[str, Any] | None:
+        """The plan attribute of ``op`` at a static configuration, or None
+        when the profile has no samples for it."""
+
+        if "dtype" in static:
+            static["dtype"] = canonical_dtype(static["dtype"])
+        keys = {"rms_norm": ("hidden_size", "dtype"),
+                "decode_attention": ("q_heads", "kv_heads", "head_dim", "dtype")}[op]
+        curve = self.curves.get((op, tuple((k, static[k]) for k in keys)))
+        return None if curve is None else curve.to_plan(self.source, self.target)

@@ -10,7 +10,9 @@
 // the sum of squares is a wave reduction, and the row is written back from the
 // registers, so HBM sees exactly one read and one write of every element.
 // Rows that do not fit the register plan, or mixed dtypes, use a one-block-
-// per-row kernel that re-reads the row (from L2) for the second pass.
+// per-row kernel that re-reads the row (from L2) for the second pass; a
+// profile-guided plan may also pick it for few rows, where four waves per row
+// shorten the latency of each row.
 #include "common.hpp"
 #include "op_math.hpp"
 
@@ -113,7 +115,8 @@ extern "C" int slc_hip_rms_norm(const void* input, const void* weight,
                                 int out_dtype, int norm_dtype, int64_t rows,
                                 int64_t hidden, int64_t in_stride_row,
                                 int64_t out_stride_row, float epsilon,
-                                int round_before_weight, void* stream) {
+                                int round_before_weight, int waves_per_row,
+                                void* stream) {
   SLC_REQUIRE(slc_host::is_float_dtype(in_dtype) &&
                   slc_host::is_float_dtype(weight_dtype) &&
                   slc_host::is_float_dtype(out_dtype) &&
@@ -135,7 +138,9 @@ extern "C" int slc_hip_rms_norm(const void* input, const void* weight,
                         reinterpret_cast<uintptr_t>(output);
   const bool aligned = (bits & 15) == 0 && hidden % vec == 0 &&
                        in_stride_row % vec == 0 && out_stride_row % vec == 0;
-  if (same && aligned && hidden / vec <= 512) {
+  SLC_REQUIRE(waves_per_row == 0 || waves_per_row == 1 || waves_per_row == 4,
+              "slc_hip_rms_norm: waves_per_row must be 0, 1 or 4, got %d", waves_per_row);
+  if (waves_per_row != 4 && same && aligned && hidden / vec <= 512) {
     const bool r = round_before_weight != 0;
     switch (in_dtype) {
       case SLC_BF16:

@@ -45,7 +45,7 @@ from .backends import (
 )
 from . import _native
 from .backends.hip_attention import exact_max_tokens
-from .cost_model import resolve_lowering_plan
+from .cost_model import choose_variant, split_tokens, waves_per_row
 from .ir import (
     Function,
     IRType,
@@ -200,20 +200,22 @@ class PreallocatedKVCacheState:
         scale: float,
         runner: Callable[..., torch.Tensor] = hip_decode_attention,
         softmax_order: str = "online",
+        split_tokens: int = 0,
     ) -> torch.Tensor:
         """Decode attention straight from the B x Capacity x H x D buffers.
 
         A custom ``runner`` is called as the reference calls it
         (``runner(query, key_buffer, value_buffer, lengths, mask, scale=)``);
-        the HIP runner also gets this state's workspace and the softmax order
-        (the exact order where the mask fits it, else the online one)."""
+        the HIP runner also gets this state's workspace, the softmax order
+        (the exact order where the mask fits it, else the online one) and the
+        split a profile plan chose."""
 
         key_buffer, value_buffer, lengths = self._attention_inputs(slot, query, attention_mask, groups)
         if runner is not hip_decode_attention:
             return runner(query, key_buffer, value_buffer, lengths, attention_mask, scale=scale)
         order = attention_order(softmax_order, attention_mask.shape[-1], query)
         return runner(query, key_buffer, value_buffer, lengths, attention_mask, scale=scale,
-                      softmax_order=order, workspace=self.workspace)
+                      softmax_order=order, workspace=self.workspace, split_tokens=split_tokens)
 
     def _attention_inputs(self, slot, query, attention_mask, groups):
         try:
@@ -494,15 +496,15 @@ class HipExecutor:
             raise ExecutionError("kernel.hip.rms_norm takes input and weight")
         tensor, weight = operands
         rows = tensor.numel() // tensor.shape[-1]
-        decision = resolve_lowering_plan(attributes.get("lowering_plan"), rows)
+        choice = choose_variant(attributes.get("lowering_plan"), max(rows, 1))
         self.lowering_trace.append({
-            "op": "rms_norm", "backend": "hip", "plan_backend": decision.backend,
-            "source": decision.source, "rows": rows, "profile_rows": decision.profile_rows,
-            "estimated_us": decision.estimated_us,
+            "op": "rms_norm", "backend": "hip", "variant": choice.variant,
+            "source": choice.source, "rows": rows, "estimated_us": choice.estimated_us,
         })
         return hip_rms_norm(
             tensor, weight, epsilon=float(attributes["epsilon"]),
             output_dtype=attributes.get("output_dtype"),
+            num_warps=waves_per_row(choice.variant) or None,
             round_before_weight=bool(attributes.get("round_before_weight", False)),
         )
 
@@ -537,15 +539,23 @@ class HipExecutor:
             softmax_order=str(attributes.get("softmax_order", "online")),
         )
 
-    @staticmethod
-    def _decode_attention(operands, attributes):
+    def _decode_attention(self, operands, attributes):
         if len(operands) != 3 or not isinstance(operands[0], PreallocatedKVCacheState):
             raise ExecutionError("kernel.hip.decode_attention takes state, query and mask")
         state, query, mask = operands
+        plan = attributes.get("split_plan")
+        split = 0
+        if plan is not None:
+            choice = choose_variant(plan, max(query.shape[0] * mask.shape[-1], 1))
+            split = split_tokens(choice.variant)
+            self.lowering_trace.append({
+                "op": "decode_attention", "backend": "hip", "variant": choice.variant,
+                "source": choice.source, "size": choice.size, "estimated_us": choice.estimated_us,
+            })
         return state.decode_attention(
             int(attributes.get("slot", 0)), query, mask, groups=int(attributes["groups"]),
             scale=float(attributes["scale"]),
-            softmax_order=str(attributes.get("softmax_order", "online")),
+            softmax_order=str(attributes.get("softmax_order", "online")), split_tokens=split,
         )
 
     @staticmethod

@@ -327,9 +327,12 @@ def _fuse_store_attention(function: Function) -> str | None:
             continue
         a_index = users[0][0]
         attention = ops[a_index]
+        # An attention with a profile-planned split keeps its own launch (the
+        # fused kernel runs the fixed-chunk split only).
         if (attention.name != "kernel.hip.decode_attention" or len(attention.operands) != 3
                 or attention.operands[0] is not state_out
-                or attention.attributes.get("slot", 0) != store.attributes.get("slot", 0)):
+                or attention.attributes.get("slot", 0) != store.attributes.get("slot", 0)
+                or "split_plan" in attention.attributes):
             continue
         state_in = store.operands[0]
         between = range(s_index + 1, a_index)

@@ -11,6 +11,8 @@ graph is a decode step with no Python per-op dispatch.  This is the
 
 from __future__ import annotations
 
+from pathlib import Path
+
 from dataclasses import replace
 from typing import Any
 
@@ -38,13 +40,15 @@ class Qwen2Runtime:
         fuse: bool = True,
         attention_softmax: str = "exact",
         linear_backend: str | None = None,
+        profile: str | Path | None = None,
     ) -> None:
         self.config = config
         self.capacity = capacity
         self.dtype = dtype
         self.device = torch.device(device)
         options = CompileOptions(numerical_mode=numerical_mode, require_full_lowering=True, fuse=fuse,
-                                 attention_softmax=attention_softmax, linear_backend=linear_backend)
+                                 attention_softmax=attention_softmax, linear_backend=linear_backend,
+                                 rmsnorm_profile=profile)
         self.prefill_result = compile_module(
             build_prefill_module(config, capacity=capacity, dtype=dtype, device=device,
                                  mask_dtype=mask_dtype), options)

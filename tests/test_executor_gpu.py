@@ -112,6 +112,47 @@ def test_config1_bf16_fast_mode_online_softmax_attribution(gpu):
     assert results["exact"] <= 2e-2 < results["online"] or results["exact"] < results["online"]
 
 
+def test_profile_plans_launch_the_planned_variants(gpu, tmp_path):
+    """A profile that makes the workgroup-per-row RMSNorm and the balanced
+    decode split the cheapest variants at every size: the executor launches
+    them (lowering trace) and the logits stay within the bf16 bar of the
+    unplanned run (online softmax order, which the balanced split serves)."""
+
+    import json
+
+    announce("executor config1 bf16 fast with a variant-forcing profile")
+    profile = {
+        "schema_version": 1,
+        "target": {"device_name": "test"},
+        "results": [{"rows": r, "hidden_size": 896, "dtype": "bf16",
+                     "hip_variants": {"wave": 10.0, "block": 1.0}} for r in (1, 4096)],
+        "decode_attention": [{"batch": b, "mask_len": 64, "q_heads": 14, "kv_heads": 2, "head_dim": 64,
+                              "dtype": "bf16", "hip_variants": {"fixed": 10.0, "balanced": 1.0}}
+                             for b in (1, 64)],
+    }
+    path = tmp_path / "force.json"
+    path.write_text(json.dumps(profile))
+    weights = {k: v.to(gpu) for k, v in init_weights(CONFIG1, seed=0, dtype=torch.bfloat16).items()}
+    ids, mask, pos = _prompt()
+    outputs = {}
+    for name, prof in (("plain", None), ("planned", path)):
+        rt = Qwen2Runtime(CONFIG1, weights, capacity=CAPACITY, device=str(gpu),
+                          attention_softmax="online", profile=prof)
+        logits, state = rt.prefill(ids.to(gpu), mask.to(gpu), pos.to(gpu))
+        token = logits[:, -1].argmax(-1, keepdim=True)
+        steps = [logits]
+        for step in range(2):
+            dmask = torch.zeros(BATCH, 1, 1, PAST + step + 1, dtype=torch.bfloat16, device=gpu)
+            logits, state = rt.decode(token, dmask, state)
+            steps.append(logits)
+        outputs[name] = steps
+        if prof is not None:
+            variants = {(t["op"], t["variant"]) for t in rt.executor.lowering_trace if "variant" in t}
+            assert ("rms_norm", "block") in variants and ("decode_attention", "balanced") in variants
+    for planned, plain in zip(outputs["planned"], outputs["plain"]):
+        assert_bf16_close(planned.cpu(), plain.cpu())
+
+
 def test_config1_bf16_pytorch_compatible_is_exact(gpu):
     announce("executor config1 bf16 pytorch_compatible vs eager GPU")
 

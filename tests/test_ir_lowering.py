@@ -10,10 +10,11 @@ import pytest
 
 from stateful_llm_compiler_hip.compiler import CompileOptions, compile_module
 from stateful_llm_compiler_hip.cost_model import (
+    KernelProfile,
     ProfileError,
-    RMSNormCostModel,
-    resolve_lowering_plan,
-    select_num_warps,
+    choose_variant,
+    split_tokens,
+    waves_per_row,
 )
 from stateful_llm_compiler_hip.ir import (
     Block,
@@ -180,50 +181,168 @@ def test_unsupported_numerical_mode():
 
 # ------------------------------------------------------------------ cost model
 
-PROFILE = {
+# A profile in the reference's format (benchmarks/bench_rmsnorm.py:183-208):
+# backends this build does not have, and hip_us.
+REFERENCE_PROFILE = {
     "schema_version": 1,
     "target": {"device_name": "AMD Instinct MI355X"},
     "results": [
-        {"rows": 1, "hidden_size": 896, "dtype": "bf16", "native_eager_us": 9.0, "hip_us": 3.0},
-        {"rows": 64, "hidden_size": 896, "dtype": "bf16", "native_eager_us": 4.0, "hip_us": 5.0},
+        {"rows": 1, "hidden_size": 896, "dtype": "bf16", "native_eager_us": 9.0,
+         "triton_us": 4.0, "inductor_us": 8.0, "hip_us": 3.0},
         {"rows": 4096, "hidden_size": 896, "dtype": "bf16", "native_eager_us": 30.0, "hip_us": 12.0},
     ],
 }
 
+VARIANT_PROFILE = {
+    "schema_version": 1,
+    "target": {"device_name": "AMD Instinct MI355X"},
+    "results": [
+        {"rows": 1, "hidden_size": 896, "dtype": "bf16", "hip_variants": {"wave": 3.0, "block": 2.0}},
+        {"rows": 64, "hidden_size": 896, "dtype": "bf16", "hip_variants": {"wave": 5.0, "block": 6.0}},
+        {"rows": 4096, "hidden_size": 896, "dtype": "bf16", "hip_variants": {"wave": 12.0, "block": 30.0}},
+    ],
+    "decode_attention": [
+        {"batch": 8, "mask_len": 1024, "q_heads": 14, "kv_heads": 2, "head_dim": 64, "dtype": "bf16",
+         "hip_variants": {"fixed": 10.0, "balanced": 13.0}},
+        {"batch": 64, "mask_len": 8192, "q_heads": 14, "kv_heads": 2, "head_dim": 64, "dtype": "bf16",
+         "hip_variants": {"fixed": 52.0, "balanced": 46.0, "chunk1024": 60.0}},
+    ],
+}
 
-def test_cost_model_buckets_split_at_geometric_midpoints():
-    model = RMSNormCostModel.from_dict(PROFILE)
-    variants = model.variants(896, "bf16")
-    assert [(v.min_rows, v.max_rows, v.backend) for v in variants] == [
-        (1, 8, "hip"), (9, 512, "native"), (513, None, "hip"),
-    ]
-    plan = model.plan_attribute(896, "bfloat16")
-    assert resolve_lowering_plan(plan, 8).profile_rows == 1
-    assert resolve_lowering_plan(plan, 9).backend == "native"
-    assert resolve_lowering_plan(plan, 100000).backend == "hip"
-    assert resolve_lowering_plan(None, 4).source == "default"
-    assert model.variants(1536, "bf16") == []
+
+def test_reference_profile_loads_and_plans_the_automatic_variant():
+    profile = KernelProfile.from_dict(REFERENCE_PROFILE)
+    plan = profile.plan("rms_norm", hidden_size=896, dtype="bfloat16")
+    assert [s["latency_us"] for s in plan["samples"]] == [{"auto": 3.0}, {"auto": 12.0}]
+    assert choose_variant(plan, 100).variant == "auto"
+    assert profile.plan("rms_norm", hidden_size=1536, dtype="bf16") is None
+    assert choose_variant(None, 4).source == "default"
 
 
-def test_cost_model_rejects_bad_profiles():
+def test_variant_latencies_interpolate_in_log_size():
+    plan = KernelProfile.from_dict(VARIANT_PROFILE).plan("rms_norm", hidden_size=896, dtype="bf16")
+    # rows 1: block 2 < wave 3.
+    assert choose_variant(plan, 1).variant == "block"
+    # rows 8 sits halfway (in log) between 1 and 64: wave 4.0 == block 4.0, a
+    # tie that goes to the variant listed first.
+    eight = choose_variant(plan, 8)
+    assert eight.variant == "wave" and eight.estimated_us == pytest.approx(4.0)
+    # rows 4: a third of the way: wave 3 + 2/3 < block 2 + 4/3?  No: 3.667 > 3.333.
+    four = choose_variant(plan, 4)
+    assert four.variant == "block" and four.estimated_us == pytest.approx(2.0 + 4.0 / 3.0)
+    # Past the last sample the end values stand: wave 12 < block 30.
+    assert choose_variant(plan, 10**6).variant == "wave"
+    assert waves_per_row("wave") == 1 and waves_per_row("block") == 4 and waves_per_row("auto") == 0
+
+    split = KernelProfile.from_dict(VARIANT_PROFILE).plan(
+        "decode_attention", q_heads=14, kv_heads=2, head_dim=64, dtype="bf16")
+    assert choose_variant(split, 8 * 1024).variant == "fixed"
+    assert choose_variant(split, 64 * 8192).variant == "balanced"
+    # chunk1024 was measured only at the large size: its flat estimate (60)
+    # never wins.
+    assert choose_variant(split, 100).variant == "fixed"
+    assert [split_tokens(v) for v in ("fixed", "balanced", "chunk1024", "auto")] == [0, -1, 1024, 0]
+
+
+def test_bad_profiles_are_rejected():
     with pytest.raises(ProfileError):
-        RMSNormCostModel.from_dict({"schema_version": 2, "results": []})
-    bad = copy.deepcopy(PROFILE)
-    bad["results"].append(dict(bad["results"][0]))
+        KernelProfile.from_dict({"schema_version": 2, "results": []})
+    dup = copy.deepcopy(VARIANT_PROFILE)
+    dup["results"].append(dict(dup["results"][0]))
     with pytest.raises(ProfileError):
-        RMSNormCostModel.from_dict(bad)
+        KernelProfile.from_dict(dup)
+    unknown = copy.deepcopy(VARIANT_PROFILE)
+    unknown["results"][0]["hip_variants"]["warp32"] = 1.0
     with pytest.raises(ProfileError):
-        resolve_lowering_plan({"variants": []}, 0)
-    assert select_num_warps(8, 896) == 4 and select_num_warps(64, 4096) == 8
+        KernelProfile.from_dict(unknown)
+    negative = copy.deepcopy(VARIANT_PROFILE)
+    negative["decode_attention"][0]["hip_variants"]["fixed"] = -1.0
+    with pytest.raises(ProfileError):
+        KernelProfile.from_dict(negative)
+    with pytest.raises(ProfileError):
+        choose_variant({"op": "rms_norm", "samples": []}, 0)
+    with pytest.raises(ProfileError):
+        split_tokens("wave")
 
 
-def test_profile_plan_pass_attaches_plans(tmp_path):
+def test_profile_plan_passes_attach_plans(tmp_path):
     import json
 
     path = tmp_path / "profile.json"
-    path.write_text(json.dumps(PROFILE))
+    path.write_text(json.dumps(VARIANT_PROFILE))
     result = compile_module(build_decode_module(SMALL, capacity=64),
                             CompileOptions(rmsnorm_profile=path))
-    norms = [op for op in result.module.functions[0].block.operations if op.name == "kernel.hip.rms_norm"]
-    assert norms and all(op.attributes["lowering_plan"]["variants"] for op in norms)
-    assert result.passes[0].statistics["planned_operations"] == len(norms)
+    ops = result.module.functions[0].block.operations
+    norms = [op for op in ops if op.name == "kernel.hip.rms_norm"]
+    attention = [op for op in ops if op.name == "kernel.hip.decode_attention"]
+    assert norms and all(op.attributes["lowering_plan"]["op"] == "rms_norm" for op in norms)
+    assert attention and all(op.attributes["split_plan"]["op"] == "decode_attention" for op in attention)
+    stats = {r.name: r.statistics for r in result.passes}
+    assert stats["select-rmsnorm-lowering"]["planned_operations"] == len(norms)
+    assert stats["select-decode-attention-split"]["planned_operations"] == len(attention)
+    # A planned attention keeps its own launch (the fused RoPE + attention
+    # kernel runs the fixed split only).
+    assert not any(op.name == "kernel.hip.rope_store_attention" for op in ops)
+
+
+def test_committed_mi355x_profile_plans_the_measured_winners():
+    """The profile measured on MI355X (profile_variants.py) loads, and its
+    plans pick what it measured fastest: one wave per RMSNorm row, and the
+    fixed-chunk split at the decode-attention bench shape."""
+
+    from pathlib import Path
+
+    import stateful_llm_compiler_hip
+
+    path = Path(stateful_llm_compiler_hip.__file__).parent / "profiles" / "mi355x.json"
+    profile = KernelProfile.load(path)
+    norm = profile.plan("rms_norm", hidden_size=896, dtype="bf16")
+    for rows in (1, 8, 4096, 32768):
+        assert choose_variant(norm, rows).variant == "wave"
+    split = profile.plan("decode_attention", q_heads=14, kv_heads=2, head_dim=64, dtype="bf16")
+    assert choose_variant(split, 32 * 8192).variant == "fixed"
+
+
+def test_plan_changes_the_variant_the_executor_launches(monkeypatch):
+    """The plan's choice reaches the HIP wrapper's launch argument (and from
+    there the C ABI's waves_per_row / split_tokens) and the lowering trace."""
+
+    import torch
+
+    from stateful_llm_compiler_hip import execution
+
+    profile = KernelProfile.from_dict(VARIANT_PROFILE)
+    seen = {}
+
+    def fake_rms_norm(tensor, weight, **kwargs):
+        seen["num_warps"] = kwargs.get("num_warps")
+        return tensor
+
+    monkeypatch.setattr(execution, "hip_rms_norm", fake_rms_norm)
+    executor = execution.HipExecutor()
+    plan = profile.plan("rms_norm", hidden_size=896, dtype="bf16")
+    attrs = {"epsilon": 1e-6, "round_before_weight": True, "lowering_plan": plan}
+    executor._rms_norm([torch.zeros(1, 896), torch.ones(896)], attrs)
+    assert seen["num_warps"] == 4                      # rows 1: the block variant
+    executor._rms_norm([torch.zeros(4096, 896), torch.ones(896)], attrs)
+    assert seen["num_warps"] == 1                      # rows 4096: one wave per row
+    executor._rms_norm([torch.zeros(4096, 896), torch.ones(896)],
+                       {"epsilon": 1e-6, "round_before_weight": True})
+    assert seen["num_warps"] is None                   # no plan: the library decides
+    assert [t["variant"] for t in executor.lowering_trace] == ["block", "wave", "auto"]
+
+    class RecordingState(execution.PreallocatedKVCacheState):
+        def decode_attention(self, slot, query, mask, **kwargs):
+            seen["split_tokens"] = kwargs["split_tokens"]
+            return query
+
+    state = object.__new__(RecordingState)
+    split = profile.plan("decode_attention", q_heads=14, kv_heads=2, head_dim=64, dtype="bf16")
+    attrs = {"groups": 7, "scale": 0.125, "split_plan": split}
+    executor._decode_attention([state, torch.zeros(64, 14, 1, 64), torch.zeros(64, 1, 1, 8192)], attrs)
+    assert seen["split_tokens"] == -1                  # the balanced split
+    executor._decode_attention([state, torch.zeros(8, 14, 1, 64), torch.zeros(8, 1, 1, 1024)], attrs)
+    assert seen["split_tokens"] == 0                   # the fixed-chunk split
+    assert executor.lowering_trace[-1]["variant"] == "fixed"
+
+

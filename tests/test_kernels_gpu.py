@@ -360,16 +360,20 @@ def test_decode_attention_positions_past_length_are_ignored(gpu):
 # ------------------------------------------------------------------ rms_norm
 
 
+@pytest.mark.parametrize("waves", [None, 1, 4])
 @pytest.mark.parametrize("rows", [1, 8, 64, 512, 32768])
-def test_rms_norm_bf16_round_before_weight(gpu, rows):
+def test_rms_norm_bf16_round_before_weight(gpu, rows, waves):
+    # Both launch widths a profile plan can pick (one wave per row, a
+    # 256-thread workgroup per row) and the automatic one.
     from stateful_llm_compiler_hip.backends import hip_rms_norm
 
-    announce(f"rms_norm bf16 rows={rows}")
+    announce(f"rms_norm bf16 rows={rows} waves_per_row={waves}")
     g = generator(rows)
     x = torch.randn(rows, 896, generator=g).bfloat16()
     w = (1.0 + 0.1 * torch.randn(896, generator=g)).bfloat16()
     expected = ref.rms_norm(x, w, epsilon=1e-6, round_before_weight=True)
-    actual = hip_rms_norm(x.to(gpu), w.to(gpu), epsilon=1e-6, round_before_weight=True)
+    actual = hip_rms_norm(x.to(gpu), w.to(gpu), epsilon=1e-6, round_before_weight=True,
+                          num_warps=waves)
     torch.cuda.synchronize()
     assert actual.dtype == expected.dtype
     assert_bf16_close(actual, expected)
