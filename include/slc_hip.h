@@ -16,6 +16,8 @@
  *   slc_hip_decode_attention   backends/triton_attention.py:134-210
  *                              (triton_decode_attention; semantics of
  *                              execution.py:281-327)
+ *   slc_hip_paged_decode_attention, slc_hip_paged_kv_store: the paged layout
+ *                              the reference plans next (docs/kv-bufferization.md:317-323)
  *   slc_hip_kv_store           backends/triton_kv.py:71-129 (triton_kv_store;
  *                              semantics of execution.py:743-781 native_kv_store)
  *   slc_hip_rms_norm           backends/triton_rmsnorm.py:205-443
@@ -203,6 +205,47 @@ SLC_API int slc_hip_decode_attention_noalloc(
     int64_t mask_stride_b, int64_t mask_stride_s, int64_t out_stride_b,
     int64_t out_stride_h, float scale, int64_t split_tokens, int softmax_order,
     void* stream);
+
+/*
+ * Paged KV (reference: the paged layout and block table that
+ * docs/kv-bufferization.md:317-323 names as the next step after the
+ * contiguous buffers; KVStateType.layout, ir.py:87).  Per layer, K and V rows
+ * live in page pools [num_pages, page_tokens, kv_heads, head_dim] with row
+ * stride kv_stride_s, head stride kv_stride_h and page stride page_stride
+ * (elements); block_table is int32 [batch, >= pages_per_seq] with batch
+ * stride table_stride_b, entry j of sequence b naming the pool page of its
+ * tokens [j * page_tokens, (j + 1) * page_tokens).  page_tokens is a power of
+ * two >= 16; capacity = pages_per_seq * page_tokens.
+ *
+ * slc_hip_paged_decode_attention: slc_hip_decode_attention over the paged
+ * layout, same arguments otherwise (bf16/fp16, head_dim 64 or 128, at most 16
+ * query heads per kv head; workspace and counters sized by
+ * slc_hip_decode_attention_workspace_size / _counter_count).  A call equals
+ * the contiguous call over the same tokens bit for bit.
+ */
+SLC_API int slc_hip_paged_decode_attention(
+    const void* query, const void* key_pool, const void* value_pool, const int* block_table,
+    int64_t table_stride_b, int64_t pages_per_seq, int64_t page_tokens, int64_t page_stride,
+    const void* lengths, int lengths_dtype, const void* mask, int mask_dtype, void* output,
+    void* workspace, int64_t workspace_bytes, int* counters, int64_t num_counters, int dtype,
+    int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t mask_len,
+    int64_t q_stride_b, int64_t q_stride_h, int64_t kv_stride_s, int64_t kv_stride_h,
+    int64_t mask_stride_b, int64_t mask_stride_s, int64_t out_stride_b, int64_t out_stride_h,
+    float scale, int64_t split_tokens, int softmax_order, void* stream);
+
+/*
+ * slc_hip_paged_kv_store: slc_hip_kv_store over the paged layout: row t of
+ * (b, h) goes to position positions[b] + t of sequence b (its page from the
+ * block table); positions outside [0, capacity) are dropped and set
+ * *overflow (if not NULL).  Rows, strides and pointers 16-byte aligned.
+ */
+SLC_API int slc_hip_paged_kv_store(
+    void* key_pool, void* value_pool, const int* block_table, int64_t table_stride_b,
+    int64_t pages_per_seq, int64_t page_tokens, int64_t page_stride, int64_t kv_stride_s,
+    int64_t kv_stride_h, const void* key, const void* value, const int64_t* positions,
+    int* overflow, int dtype, int64_t batch, int64_t heads, int64_t tokens, int64_t head_dim,
+    int64_t key_stride_b, int64_t key_stride_h, int64_t key_stride_t, int64_t value_stride_b,
+    int64_t value_stride_h, int64_t value_stride_t, void* stream);
 
 /* Longest mask the SLC_SOFTMAX_EXACT order takes (INT64_MAX: no limit). */
 SLC_API int64_t slc_hip_decode_attention_exact_max_tokens(int64_t head_dim, int dtype);

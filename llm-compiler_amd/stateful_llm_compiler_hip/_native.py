@@ -90,6 +90,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I,
         [_P, _P, _P, _P, _I, _P, _I, _P, _I] + [_L] * 15 + [_F, _L, _I, _P],
     ),
+    "slc_hip_paged_decode_attention": (
+        _I,
+        [_P, _P, _P, _P, _L, _L, _L, _L, _P, _I, _P, _I, _P, _P, _L, _P, _L, _I]
+        + [_L] * 13 + [_F, _L, _I, _P],
+    ),
+    "slc_hip_paged_kv_store": (
+        _I,
+        [_P, _P, _P, _L, _L, _L, _L, _L, _L, _P, _P, _P, _P, _I] + [_L] * 10 + [_P],
+    ),
     "slc_hip_decode_attention_exact_max_tokens": (_L, [_L, _I]),
     "slc_hip_decode_attention_counter_count": (_L, [_L, _L]),
     "slc_hip_rms_norm": (

@@ -194,6 +194,18 @@ __device__ __forceinline__ void rope_slices(uint4 (&x)[KK], const uint4 (&cs)[KK
   }
 }
 
+// Paged KV (decode_paged.hip): K/V rows live in page pools
+// [num_pages, page_tokens, kv_heads, head_dim]; token t of sequence b is row
+// t mod page_tokens of page table[b * table_sb + t / page_tokens].
+// page_tokens is a power of two >= 16 (a 16-row MFMA block never straddles
+// two pages); page_stride is one page's size in elements.
+struct Paging {
+  const int* table;
+  int64_t table_sb;
+  int page_shift;  // log2(page_tokens)
+  int64_t page_stride;
+};
+
 // ---- balanced split (decode_stream.hip) -------------------------------------
 constexpr int kStreamMaxBatch = 2048;  // lengths prefix held in LDS
 constexpr int kStreamMaxGrid = 1024;   // workgroups (partial slots) of one call

@@ -71,6 +71,51 @@ def kv_store(
                 value_buffer[b, position] = value[b, :, t]
 
 
+def gather_pages(pool: np.ndarray, block_table: np.ndarray) -> np.ndarray:
+    """The contiguous B x Cap x H x D buffer a paged layout stands for.
+
+    The paged layout is the one docs/kv-bufferization.md:317-323 plans next:
+    ``pool`` is [pages, page_tokens, H, D] and ``block_table[b, j]`` names the
+    pool page holding tokens [j * page_tokens, (j + 1) * page_tokens) of
+    sequence b, so the buffer row of (b, s) is ``pool[table[b, s // P],
+    s % P]``.  Decode attention over the pages is defined as
+    ``decode_attention`` over this gathered buffer.
+    """
+
+    page_tokens = pool.shape[1]
+    batch, pages = block_table.shape
+    out = np.empty((batch, pages * page_tokens) + pool.shape[2:], dtype=pool.dtype)
+    for b in range(batch):
+        for j in range(pages):
+            out[b, j * page_tokens:(j + 1) * page_tokens] = pool[int(block_table[b, j])]
+    return out
+
+
+def paged_kv_store(
+    key_pool: np.ndarray,
+    value_pool: np.ndarray,
+    block_table: np.ndarray,
+    key: np.ndarray,
+    value: np.ndarray,
+    positions: np.ndarray,
+) -> None:
+    """``kv_store`` into a paged layout, in place: row t of batch b goes to
+    position positions[b] + t of sequence b, i.e. row (p % P) of pool page
+    block_table[b, p // P]; positions outside the table's capacity are
+    dropped, as ``kv_store`` drops rows past the buffer."""
+
+    page_tokens = key_pool.shape[1]
+    batch, heads, tokens, _ = key.shape
+    capacity = block_table.shape[1] * page_tokens
+    for b in range(batch):
+        for t in range(tokens):
+            position = int(positions[b]) + t
+            if 0 <= position < capacity:
+                page = int(block_table[b, position // page_tokens])
+                key_pool[page, position % page_tokens] = key[b, :, t]
+                value_pool[page, position % page_tokens] = value[b, :, t]
+
+
 _DTYPES = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}
 
 

@@ -153,6 +153,58 @@ def test_kv_store_matches_index_copy_and_drops_overflow():
     assert np.array_equal(kb.reshape(B * cap, H, D), want.numpy())
 
 
+# ------------------------------------------------------------------ paged KV
+
+
+def _random_paging(g, batch, pages, extra=3):
+    """A block table naming distinct pages of a pool with spare pages, in a
+    random order."""
+
+    order = torch.randperm(batch * pages + extra, generator=g)[: batch * pages]
+    return order.view(batch, pages).numpy().astype(np.int32), batch * pages + extra
+
+
+def test_gather_pages_identity_table_is_a_reshape():
+    # A table that names pages in order makes the pool a reshaped contiguous
+    # buffer: gathering must give that buffer back.
+    g = generator(40)
+    B, pages, P, H, D = 3, 4, 16, 2, 8
+    buffer = torch.randn(B, pages * P, H, D, generator=g).numpy()
+    pool = buffer.reshape(B * pages, P, H, D)
+    table = np.arange(B * pages, dtype=np.int32).reshape(B, pages)
+    assert np.array_equal(ref.gather_pages(pool, table), buffer)
+
+
+def test_gather_pages_inverts_a_page_scatter():
+    g = generator(41)
+    B, pages, P, H, D = 2, 5, 16, 2, 4
+    buffer = torch.randn(B, pages * P, H, D, generator=g).numpy()
+    table, num_pages = _random_paging(g, B, pages)
+    pool = np.full((num_pages, P, H, D), np.nan, dtype=np.float32)
+    for b in range(B):
+        for j in range(pages):
+            pool[table[b, j]] = buffer[b, j * P:(j + 1) * P]
+    assert np.array_equal(ref.gather_pages(pool, table), buffer)
+
+
+def test_paged_kv_store_equals_contiguous_store_after_gather():
+    # Storing into pages then gathering must equal storing into the gathered
+    # buffer, including dropped rows past the table's capacity.
+    g = generator(42)
+    B, pages, P, H, T, D = 3, 3, 16, 2, 20, 4
+    table, num_pages = _random_paging(g, B, pages)
+    kp = torch.randn(num_pages, P, H, D, generator=g).numpy()
+    vp = torch.randn(num_pages, P, H, D, generator=g).numpy()
+    k = torch.randn(B, H, T, D, generator=g).numpy()
+    v = torch.randn(B, H, T, D, generator=g).numpy()
+    pos = np.array([0, 17, 40])  # the last runs 12 rows past capacity 48
+    kb, vb = ref.gather_pages(kp, table), ref.gather_pages(vp, table)
+    ref.kv_store(kb, vb, k, v, pos)
+    ref.paged_kv_store(kp, vp, table, k, v, pos)
+    assert np.array_equal(ref.gather_pages(kp, table), kb)
+    assert np.array_equal(ref.gather_pages(vp, table), vb)
+
+
 # -------------------------------------------------------------------- rms_norm
 
 
