@@ -36,6 +36,8 @@ from .backends import (
     hip_linear_residual,
     hip_norm_linear_group,
     hip_norm_linear_swiglu,
+    hip_paged_decode_attention,
+    hip_paged_kv_store,
     hip_prefill_attention,
     hip_rms_norm,
     hip_rope,
@@ -393,6 +395,196 @@ class PreallocatedKVCacheState:
         return buffer_key, buffer_value
 
 
+def _page_order(batch: int, pages_per_seq: int, device) -> torch.Tensor:
+    """Block table of a fully provisioned pool: page j of sequence b is pool
+    page j * batch + b, so every sequence's pages are scattered over the pool
+    (what a page allocator produces after sequences have grown in turn)."""
+
+    pages = torch.arange(pages_per_seq, dtype=torch.int32).view(1, -1) * batch
+    return (pages + torch.arange(batch, dtype=torch.int32).view(-1, 1)).to(device)
+
+
+@dataclass(frozen=True)
+class PagedKVCacheState(PreallocatedKVCacheState):
+    """The paged KV layout (``KVStateType.layout == "paged"``): the next step
+    the reference plans after its contiguous buffers
+    (docs/kv-bufferization.md:317-323).
+
+    ``keys``/``values`` hold one page pool per layer, [num_pages,
+    page_tokens, H, D]; ``block_table`` (int32 [B, capacity / page_tokens],
+    shared by every layer) names the pool page of each sequence's tokens
+    [j * page_tokens, (j + 1) * page_tokens).  Lengths, versions, the overflow
+    flag and the workspace behave as in the contiguous state, and every op
+    gives the contiguous state's result bit for bit.  RoPE + store runs as two
+    kernels here (the fused kernels address contiguous rows).
+    """
+
+    block_table: torch.Tensor | None = None
+    page_tokens: int = 0
+
+    def __post_init__(self) -> None:
+        if self.capacity <= 0:
+            raise ExecutionError("KV capacity must be positive")
+        p = self.page_tokens
+        if p < 16 or p & (p - 1) or self.capacity % p:
+            raise ExecutionError("page_tokens must be a power of two >= 16 dividing the capacity")
+        table = self.block_table
+        if table is None or table.ndim != 2 or table.dtype != torch.int32:
+            raise ExecutionError("a paged KV state needs an int32 [B, pages] block table")
+        if table.shape[1] != self.capacity // p:
+            raise ExecutionError("block table width must be capacity / page_tokens")
+        if not self.keys or len(self.keys) != len(self.values) or len(self.keys) != len(self.lengths):
+            raise ExecutionError("KV key/value/length slot counts must agree")
+        for key, value, lengths in zip(self.keys, self.values, self.lengths):
+            if key.shape != value.shape or key.ndim != 4 or key.shape[1] != p:
+                raise ExecutionError("KV pools must be equal-shaped pages x page_tokens x H x D tensors")
+            if lengths.shape != (table.shape[0],) or lengths.dtype != torch.int64:
+                raise ExecutionError("KV lengths must be an int64 [B] tensor")
+
+    @classmethod
+    def empty_from_key_template(
+        cls, key: torch.Tensor, *, num_layers: int, capacity: int, in_place_lengths: bool = False,
+        page_tokens: int = 64,
+    ) -> "PagedKVCacheState":
+        """Zeroed pools for every layer from a B x H x T x D key template,
+        with capacity / page_tokens pages per sequence."""
+
+        if key.ndim != 4 or num_layers <= 0 or capacity <= 0 or page_tokens <= 0 or capacity % page_tokens:
+            raise ExecutionError("paged KV init got an illegal template, layer count, capacity or page size")
+        batch, heads, _, head_dim = key.shape
+        pages = capacity // page_tokens
+        keys = tuple(torch.zeros(batch * pages, page_tokens, heads, head_dim, device=key.device,
+                                 dtype=key.dtype) for _ in range(num_layers))
+        values = tuple(torch.zeros_like(pool) for pool in keys)
+        lengths = tuple(torch.zeros(batch, device=key.device, dtype=torch.int64) for _ in range(num_layers))
+        return cls(keys, values, lengths, capacity,
+                   overflow=torch.zeros(1, device=key.device, dtype=torch.int32),
+                   in_place_lengths=in_place_lengths, zero_slots=frozenset(range(num_layers)),
+                   workspace=_device_workspace(key.device),
+                   block_table=_page_order(batch, pages, key.device), page_tokens=page_tokens)
+
+    @classmethod
+    def from_layer_tensors(cls, past_key_values, *, capacity: int, in_place_lengths: bool = False,
+                           page_tokens: int = 64) -> "PagedKVCacheState":
+        """Copy logical B x H x S x D caches into freshly paged slots (setup only)."""
+
+        if not past_key_values:
+            raise ExecutionError("a multi-layer KV cache needs at least one slot")
+        state = cls.empty_from_key_template(past_key_values[0][0], num_layers=len(past_key_values),
+                                            capacity=capacity, in_place_lengths=in_place_lengths,
+                                            page_tokens=page_tokens)
+        lengths = []
+        for slot, (key, value) in enumerate(past_key_values):
+            if key.shape != value.shape or key.shape != past_key_values[0][0].shape:
+                raise ExecutionError("all layer slots need one K/V shape")
+            if key.shape[2] > capacity:
+                raise ExecutionError(f"layer {slot}: initial length {key.shape[2]} exceeds capacity {capacity}")
+            zero = torch.zeros(key.shape[0], dtype=torch.int64, device=key.device)
+            hip_paged_kv_store(state.keys[slot], state.values[slot], state.block_table,
+                               key.to(state.keys[slot].dtype), value.to(state.keys[slot].dtype), zero)
+            lengths.append(torch.full_like(zero, key.shape[2]))
+        return replace(state, lengths=tuple(lengths), zero_slots=None)
+
+    @property
+    def batch(self) -> int:
+        return self.block_table.shape[0]
+
+    def gather(self, slot: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """The contiguous B x capacity x H x D buffers the pages stand for
+        (a copy; for eager composites and inspection)."""
+
+        try:
+            pools = self.keys[slot], self.values[slot]
+        except IndexError as error:
+            raise ExecutionError(f"KV buffer has no slot {slot}") from error
+        index = self.block_table.long()
+        return tuple(pool[index].reshape(self.batch, self.capacity, *pool.shape[2:]) for pool in pools)
+
+    def read(self, slot: int) -> tuple[torch.Tensor, torch.Tensor]:
+        key, value = self.gather(slot)
+        used = int(self.positions(slot).max().item())
+        return key[:, :used].transpose(1, 2), value[:, :used].transpose(1, 2)
+
+    def _check_attention(self, slot, query, attention_mask, groups):
+        try:
+            pool, lengths = self.keys[slot], self.lengths[slot]
+        except IndexError as error:
+            raise ExecutionError(f"KV buffer has no slot {slot}") from error
+        if query.ndim != 4 or query.shape[2] != 1:
+            raise ExecutionError("decode attention query must be B x H x 1 x D")
+        if attention_mask.ndim != 4 or attention_mask.shape[2] != 1:
+            raise ExecutionError("decode attention mask must be B x 1 x 1 x S")
+        if (query.shape[0] != self.batch or query.shape[0] != attention_mask.shape[0]
+                or query.shape[3] != pool.shape[3]):
+            raise ExecutionError("decode attention batch or head dim does not match the KV pages")
+        if groups <= 0 or query.shape[1] != pool.shape[2] * groups:
+            raise ExecutionError("decode attention GQA groups do not match")
+        if attention_mask.shape[-1] > self.capacity:
+            raise ExecutionError("decode attention mask is longer than the KV capacity")
+        return lengths
+
+    def _attention_inputs(self, slot, query, attention_mask, groups):
+        # Eager composites read the gathered contiguous buffers.
+        lengths = self._check_attention(slot, query, attention_mask, groups)
+        key, value = self.gather(slot)
+        return key, value, lengths
+
+    def decode_attention(self, slot, query, attention_mask, *, groups, scale,
+                         runner=hip_decode_attention, softmax_order="online", split_tokens=0):
+        """Decode attention straight from the pages through the block table;
+        a custom ``runner`` gets the gathered contiguous buffers."""
+
+        if runner is not hip_decode_attention:
+            key, value, lengths = self._attention_inputs(slot, query, attention_mask, groups)
+            return runner(query, key, value, lengths, attention_mask, scale=scale)
+        lengths = self._check_attention(slot, query, attention_mask, groups)
+        order = attention_order(softmax_order, attention_mask.shape[-1], query)
+        return hip_paged_decode_attention(
+            query, self.keys[slot], self.values[slot], self.block_table, lengths, attention_mask,
+            scale=scale, softmax_order=order, workspace=self.workspace, split_tokens=split_tokens)
+
+    def _validate_store(self, slot, key, value, positions):
+        try:
+            pool_key, pool_value = self.keys[slot], self.values[slot]
+        except IndexError as error:
+            raise ExecutionError(f"KV buffer has no slot {slot}") from error
+        if key.shape != value.shape or key.ndim != 4:
+            raise ExecutionError("KV store K/V must be equal B x H x T x D tensors")
+        batch, heads, _, head_dim = key.shape
+        if batch != self.batch or heads != pool_key.shape[2] or head_dim != pool_key.shape[3]:
+            raise ExecutionError("KV store batch, heads or head dim does not match")
+        if positions.shape != (batch,) or positions.dtype != torch.int64:
+            raise ExecutionError("KV store positions must be a 1-D batch int64 tensor")
+        if positions.device != key.device:
+            raise ExecutionError("KV store positions and K/V must share a device")
+        return pool_key, pool_value
+
+    def store(self, slot, key, value, positions, *, writer=hip_kv_store) -> "PagedKVCacheState":
+        pool_key, pool_value = self._validate_store(slot, key, value, positions)
+        if writer is not hip_kv_store:
+            raise ExecutionError("a paged KV state stores through its block table only")
+        hip_paged_kv_store(pool_key, pool_value, self.block_table, key, value, positions,
+                           overflow=self.overflow)
+        return self
+
+    def rope_store(self, slot, query, key, value, cosine, sine, positions):
+        q_rot, k_rot = hip_rope(query, key, cosine, sine)
+        return q_rot, self.store(slot, k_rot, value, positions)
+
+    def rope_store_advance(self, slot, query, key, value, cosine, sine, *, delta):
+        if delta <= 0:
+            raise ExecutionError("KV advance delta must be positive")
+        q_rot, state = self.rope_store(slot, query, key, value, cosine, sine, self.positions(slot))
+        return q_rot, state.advance(slot, delta=delta)
+
+    def rope_store_attention(self, slot, query, key, value, cosine, sine, attention_mask, *,
+                             groups, scale, softmax_order="online"):
+        self._check_attention(slot, query, attention_mask, groups)
+        q_rot, state = self.rope_store_advance(slot, query, key, value, cosine, sine, delta=1)
+        return state.decode_attention(slot, q_rot, attention_mask, groups=groups, scale=scale,
+                                      softmax_order=softmax_order), state
+
+
 def _device_workspace(device: torch.device) -> _native.DeviceWorkspace | None:
     return _native.DeviceWorkspace(device) if device.type == "cuda" else None
 
@@ -655,6 +847,11 @@ class HipExecutor:
     def _kv_init(operands, attributes):
         if len(operands) != 1 or not isinstance(operands[0], torch.Tensor):
             raise ExecutionError("runtime.kv.init takes one key template")
+        if attributes.get("layout", "contiguous_bshd") == "paged":
+            return PagedKVCacheState.empty_from_key_template(
+                operands[0], num_layers=int(attributes["num_layers"]),
+                capacity=int(attributes["capacity"]), page_tokens=int(attributes["page_tokens"]),
+            )
         return PreallocatedKVCacheState.empty_from_key_template(
             operands[0], num_layers=int(attributes["num_layers"]),
             capacity=int(attributes["capacity"]),
@@ -870,7 +1067,16 @@ def validate_runtime_value(value: Any, type_: IRType, symbols: dict[str, int], *
 def _validate_kv_state(value: Any, type_: KVStateType, context: str) -> None:
     if not isinstance(value, PreallocatedKVCacheState):
         raise ExecutionError(f"{context} must be a preallocated KV runtime state")
-    if type_.layout != "contiguous_bshd":
+    paged = isinstance(value, PagedKVCacheState)
+    if type_.layout == "paged":
+        if not paged:
+            raise ExecutionError(f"{context} must be a paged KV state")
+        if type_.page_tokens is not None and value.page_tokens != type_.page_tokens:
+            raise ExecutionError(f"{context} page_tokens must be {type_.page_tokens}, got {value.page_tokens}")
+    elif type_.layout == "contiguous_bshd":
+        if paged:
+            raise ExecutionError(f"{context} must be a contiguous_bshd KV state, got a paged one")
+    else:
         raise ExecutionError(f"{context}: layout {type_.layout} is not supported by the runtime")
     if type_.capacity is not None and value.capacity != type_.capacity:
         raise ExecutionError(f"{context} capacity must be {type_.capacity}, got {value.capacity}")

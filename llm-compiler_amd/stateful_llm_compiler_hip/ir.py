@@ -100,9 +100,14 @@ class KVStateType(IRType):
     layout: str = "blocked"
     resource: str = "kv"
     capacity: int | None = None
+    # Tokens per page of the "paged" layout (pools + block table); None for
+    # the contiguous layouts.
+    page_tokens: int | None = None
 
     def __str__(self) -> str:
         capacity = f", capacity={self.capacity}" if self.capacity is not None else ""
+        if self.page_tokens is not None:
+            capacity += f", page_tokens={self.page_tokens}"
         return (
             f"!serve.kv_state<{self.dtype}, layers={self.num_layers}, "
             f"heads={self.num_kv_heads}, head_dim={self.head_dim}, "
@@ -352,6 +357,24 @@ def _verify_kv(operation: Operation, errors: list[str]) -> None:
         _verify_decode_attention(operation, errors)
 
 
+# KV layouts the runtime executes: the reference's contiguous buffers and the
+# paged layout (page pools + block table) its bufferization plan names next
+# (docs/kv-bufferization.md:317-323).
+KV_LAYOUTS = ("contiguous_bshd", "paged")
+
+
+def _verify_paging(state: KVStateType, context: str, errors: list[str]) -> None:
+    if state.layout != "paged":
+        if state.page_tokens is not None:
+            errors.append(f"{context}: page_tokens only applies to the paged layout")
+        return
+    p = state.page_tokens
+    if not isinstance(p, int) or p < 16 or p & (p - 1):
+        errors.append(f"{context}: a paged state needs page_tokens, a power of two >= 16")
+    elif state.capacity is not None and state.capacity % p:
+        errors.append(f"{context}: the capacity must be a multiple of page_tokens")
+
+
 def _verify_kv_init(operation: Operation, errors: list[str]) -> None:
     if len(operation.operands) != 1 or len(operation.results) != 1:
         errors.append("serve.kv.init takes a key template and returns one state")
@@ -360,8 +383,13 @@ def _verify_kv_init(operation: Operation, errors: list[str]) -> None:
     if not isinstance(state, KVStateType):
         errors.append("serve.kv.init must return a KVStateType")
         return
-    if state.layout != "contiguous_bshd" or state.capacity is None:
-        errors.append("serve.kv.init must create a contiguous_bshd state with a capacity")
+    if state.layout not in KV_LAYOUTS or state.capacity is None:
+        errors.append("serve.kv.init must create a contiguous_bshd or paged state with a capacity")
+    _verify_paging(state, "serve.kv.init", errors)
+    if operation.attributes.get("layout", "contiguous_bshd") != state.layout:
+        errors.append("serve.kv.init layout does not match the state type")
+    if operation.attributes.get("page_tokens") != state.page_tokens:
+        errors.append("serve.kv.init page_tokens does not match the state type")
     _verify_kv_tensor(operation.operands[0].type, state, "serve.kv.init template", errors)
     if operation.attributes.get("num_layers") != state.num_layers:
         errors.append("serve.kv.init num_layers does not match the state type")
@@ -503,8 +531,9 @@ def _verify_decode_attention(operation: Operation, errors: list[str]) -> None:
     state, q, m = (o.type for o in operation.operands)
     if not isinstance(state, KVStateType):
         return
-    if state.layout != "contiguous_bshd":
-        errors.append(f"{name}: only the contiguous_bshd KV layout is supported")
+    if state.layout not in KV_LAYOUTS:
+        errors.append(f"{name}: only the contiguous_bshd and paged KV layouts are supported")
+    _verify_paging(state, name, errors)
     if not isinstance(q, TensorType) or len(q.shape) != 4:
         errors.append(f"{name}: query must be 4-D")
         return

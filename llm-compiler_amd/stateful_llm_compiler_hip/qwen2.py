@@ -291,10 +291,22 @@ def _kv_effects(resource: str = "kv", write: bool = False):
     return tuple(effects)
 
 
+def kv_state_type(dtype: str, config: "Qwen2Config", capacity: int,
+                  page_tokens: int | None = None) -> KVStateType:
+    """The model's KV state type: contiguous_bshd buffers, or the paged
+    layout (pools of ``page_tokens``-token pages + a block table) when
+    ``page_tokens`` is given."""
+
+    return KVStateType(dtype, config.num_layers, config.num_kv_heads, config.head_dim,
+                       layout="contiguous_bshd" if page_tokens is None else "paged",
+                       capacity=capacity, page_tokens=page_tokens)
+
+
 def build_decode_module(
     config: Qwen2Config,
     *,
     capacity: int,
+    page_tokens: int | None = None,
     dtype: torch.dtype = torch.bfloat16,
     device: str = "cuda:0",
     batch: int | str = "s_batch",
@@ -310,8 +322,7 @@ def build_decode_module(
     B, T = batch, 1
     input_ids = g.b.argument(g.tensor(B, T, dtype="i64"), "input_ids")
     mask = g.b.argument(g.tensor(B, 1, 1, "s_mask"), "attention_mask")
-    state_type = KVStateType(g.dt, c.num_layers, c.num_kv_heads, c.head_dim,
-                             layout="contiguous_bshd", capacity=capacity)
+    state_type = kv_state_type(g.dt, c, capacity, page_tokens)
     state = g.b.argument(state_type, "kv_state")
     g.add_weights()
 
@@ -341,6 +352,7 @@ def build_prefill_module(
     config: Qwen2Config,
     *,
     capacity: int,
+    page_tokens: int | None = None,
     dtype: torch.dtype = torch.bfloat16,
     device: str = "cuda:0",
     batch: int | str = "s_batch",
@@ -360,8 +372,7 @@ def build_prefill_module(
     mask = g.b.argument(g.tensor(B, 1, T, T, dtype=mask_dtype), "attention_mask")
     position_ids = g.b.argument(g.tensor(B, T, dtype="i64"), "position_ids")
     g.add_weights()
-    state_type = KVStateType(g.dt, c.num_layers, c.num_kv_heads, c.head_dim,
-                             layout="contiguous_bshd", capacity=capacity)
+    state_type = kv_state_type(g.dt, c, capacity, page_tokens)
 
     h = g.op("serve.embedding", [input_ids, g.weights["embed_tokens.weight"]],
              [g.tensor(B, T, c.hidden_size)])[0]
@@ -370,8 +381,9 @@ def build_prefill_module(
     for layer in range(c.num_layers):
         qr, kr, v4 = g.layer_head(h, layer, B, T, cos, sin)
         if state is None:
+            paging = {} if page_tokens is None else {"layout": "paged", "page_tokens": page_tokens}
             state = g.op("serve.kv.init", [kr], [state_type], num_layers=c.num_layers,
-                         capacity=capacity,
+                         capacity=capacity, **paging,
                          _effects=(Effect(EffectKind.ALLOCATE, "kv"), Effect(EffectKind.WRITE, "kv")))[0]
         state = g.op("serve.kv.prefill_store", [state, kr, v4], [state_type], slot=layer,
                      _effects=_kv_effects(write=True))[0]

@@ -41,7 +41,10 @@ class Qwen2Runtime:
         attention_softmax: str = "exact",
         linear_backend: str | None = None,
         profile: str | Path | None = None,
+        page_tokens: int | None = None,
     ) -> None:
+        """``page_tokens``: run on the paged KV layout (page pools + block
+        table, ``page_tokens`` tokens a page) instead of contiguous buffers."""
         self.config = config
         self.capacity = capacity
         self.dtype = dtype
@@ -51,9 +54,10 @@ class Qwen2Runtime:
                                  rmsnorm_profile=profile)
         self.prefill_result = compile_module(
             build_prefill_module(config, capacity=capacity, dtype=dtype, device=device,
-                                 mask_dtype=mask_dtype), options)
+                                 mask_dtype=mask_dtype, page_tokens=page_tokens), options)
         self.decode_result = compile_module(
-            build_decode_module(config, capacity=capacity, dtype=dtype, device=device), options)
+            build_decode_module(config, capacity=capacity, dtype=dtype, device=device,
+                                page_tokens=page_tokens), options)
         self.executor = HipExecutor(strict=True, validate=validate)
         self.weight_args = weight_arguments(config, weights)
 
@@ -107,11 +111,11 @@ class GraphDecoder:
         """Run one step on a scratch copy of the state so every kernel and
         allocation exists before capture."""
 
-        scratch = PreallocatedKVCacheState(
-            tuple(k.clone() for k in state.keys), tuple(v.clone() for v in state.values),
-            tuple(n.clone() for n in state.lengths), state.capacity,
+        scratch = replace(
+            state, keys=tuple(k.clone() for k in state.keys), values=tuple(v.clone() for v in state.values),
+            lengths=tuple(n.clone() for n in state.lengths),
             overflow=torch.zeros(1, dtype=torch.int32, device=self.runtime.device),
-            in_place_lengths=True, workspace=self.workspace,
+            in_place_lengths=True, workspace=self.workspace, zero_slots=None,
         )
         logits, _ = self.runtime.decode(self.tokens.clone(), self.mask, scratch)
         hip_argmax(logits[:, -1], workspace=self.workspace)

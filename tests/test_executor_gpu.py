@@ -214,3 +214,102 @@ def test_graph_decoder_replays_match_eager_steps(gpu):
         assert torch.equal(decoder.tokens.view(-1).cpu(), ref_tokens[step])
         assert torch.equal(decoder.logits.cpu(), ref_logits[step])
     assert state.lengths[0].tolist() == [PAST + STEPS] * BATCH
+
+
+def _paged_trajectory(gpu, page_tokens, *, fuse=True, mode="fast"):
+    weights = {k: v.to(gpu) for k, v in init_weights(CONFIG1, seed=0).items()}
+    rt = Qwen2Runtime(CONFIG1, weights, capacity=CAPACITY, device=str(gpu), fuse=fuse,
+                      numerical_mode=mode, page_tokens=page_tokens)
+    ids, mask, pos = _prompt()
+    logits, state = rt.prefill(ids.to(gpu), mask.to(gpu), pos.to(gpu))
+    out = [logits.cpu()]
+    token = logits[:, -1].argmax(-1, keepdim=True)
+    for step in range(STEPS):
+        dmask = torch.zeros(BATCH, 1, 1, PAST + step + 1, dtype=torch.bfloat16, device=gpu)
+        logits, state = rt.decode(token, dmask, state)
+        out.append(logits.cpu())
+        token = logits[:, -1].argmax(-1, keepdim=True)
+    kv = []
+    for slot in range(CONFIG1.num_layers):
+        k, v = state.read(slot)
+        kv += [k.cpu(), v.cpu()]
+    state.check_capacity()
+    return out, kv, state
+
+
+@pytest.mark.parametrize("fuse,mode", [(False, "fast"), (True, "fast"), (True, "pytorch_compatible")])
+def test_paged_layout_model_equals_contiguous(gpu, fuse, mode):
+    """Config 1 on the paged KV layout (16-token pages, block table scattered
+    over the pool) against the contiguous layout: the same logits and KV."""
+
+    from stateful_llm_compiler_hip.execution import PagedKVCacheState
+
+    announce(f"executor config1 paged vs contiguous fuse={fuse} mode={mode}")
+    paged_logits, paged_kv, state = _paged_trajectory(gpu, 16, fuse=fuse, mode=mode)
+    assert isinstance(state, PagedKVCacheState)
+    assert state.block_table.shape == (BATCH, CAPACITY // 16)
+    plain_logits, plain_kv, _ = _paged_trajectory(gpu, None, fuse=fuse, mode=mode)
+    for a, b in zip(paged_logits + paged_kv, plain_logits + plain_kv):
+        if fuse and mode == "fast":
+            # The contiguous layout runs RoPE, store and attention as one
+            # fused kernel, the paged layout as three: same bar as the model.
+            assert_bf16_close(a, b)
+        else:
+            assert torch.equal(a, b)
+
+
+def test_paged_layout_graph_decoder(gpu):
+    """HIP-graph replays over a paged state equal eager paged steps."""
+
+    from stateful_llm_compiler_hip.execution import PagedKVCacheState
+
+    announce("graph decoder over a paged state")
+    weights = {k: v.to(gpu) for k, v in init_weights(CONFIG1, seed=0).items()}
+    rt = Qwen2Runtime(CONFIG1, weights, capacity=CAPACITY, device=str(gpu), page_tokens=32)
+    ids, mask, pos = _prompt()
+    logits, state = rt.prefill(ids.to(gpu), mask.to(gpu), pos.to(gpu))
+    assert isinstance(state, PagedKVCacheState)
+    first = logits[:, -1].argmax(-1)
+    from dataclasses import replace
+    ref_state = replace(state, keys=tuple(k.clone() for k in state.keys),
+                        values=tuple(v.clone() for v in state.values),
+                        lengths=tuple(n.clone() for n in state.lengths),
+                        overflow=torch.zeros(1, dtype=torch.int32, device=gpu))
+    dmask = torch.zeros(BATCH, 1, 1, CAPACITY, dtype=torch.bfloat16, device=gpu)
+    token = first.view(-1, 1)
+    ref_logits = []
+    for _ in range(STEPS):
+        lg, ref_state = rt.decode(token, dmask, ref_state)
+        token = lg[:, -1].argmax(-1).view(-1, 1)
+        ref_logits.append(lg.cpu())
+    decoder = rt.graph_decoder(state, first)
+    for step in range(STEPS):
+        decoder.step()
+        torch.cuda.synchronize()
+        _ = (decoder.logits.float().sum()).item()
+        assert torch.equal(decoder.logits.cpu(), ref_logits[step])
+
+
+def test_paged_state_rejects_layout_mismatch(gpu):
+    from stateful_llm_compiler_hip.execution import PagedKVCacheState
+
+    announce("paged state type checks")
+    g = generator(3)
+    cache = tuple((torch.randn(BATCH, 2, 5, 64, generator=g).bfloat16().to(gpu),
+                   torch.randn(BATCH, 2, 5, 64, generator=g).bfloat16().to(gpu)) for _ in range(2))
+    paged = PagedKVCacheState.from_layer_tensors(cache, capacity=CAPACITY, page_tokens=16)
+    for slot, (k, v) in enumerate(cache):
+        rk, rv = paged.read(slot)
+        assert torch.equal(rk, k) and torch.equal(rv, v)
+    weights = {k: v.to(gpu) for k, v in init_weights(CONFIG1, seed=0).items()}
+    contiguous_rt = Qwen2Runtime(CONFIG1, weights, capacity=CAPACITY, device=str(gpu))
+    token = torch.zeros(BATCH, 1, dtype=torch.int64, device=gpu)
+    dmask = torch.zeros(BATCH, 1, 1, 6, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ExecutionError, match="contiguous_bshd"):
+        contiguous_rt.decode(token, dmask, paged)
+    paged_rt = Qwen2Runtime(CONFIG1, weights, capacity=CAPACITY, device=str(gpu), page_tokens=16)
+    plain = PreallocatedKVCacheState.from_layer_tensors(cache, capacity=CAPACITY)
+    with pytest.raises(ExecutionError, match="paged"):
+        paged_rt.decode(token, dmask, plain)
+    with pytest.raises(ExecutionError):
+        PagedKVCacheState.from_layer_tensors(cache, capacity=CAPACITY, page_tokens=24)

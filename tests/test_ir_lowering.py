@@ -106,6 +106,45 @@ def test_verifier_kv_store_and_slot_rules():
     assert "slot must be in" in text and "missing write" in text
 
 
+def test_paged_layout_verifies_and_lowers():
+    decode = build_decode_module(SMALL, capacity=256, page_tokens=64, device="cpu")
+    prefill = build_prefill_module(SMALL, capacity=256, page_tokens=64, device="cpu")
+    verify_module(decode)
+    verify_module(prefill)
+    state = decode.functions[0].block.arguments[2].type
+    assert state.layout == "paged" and state.page_tokens == 64
+    assert "layout=paged" in str(state) and "page_tokens=64" in str(state)
+    init = next(op for op in prefill.functions[0].block.operations if op.name == "serve.kv.init")
+    assert init.attributes["layout"] == "paged" and init.attributes["page_tokens"] == 64
+    for module in (decode, prefill):
+        result = compile_module(module, CompileOptions())
+        assert result.coverage.is_complete
+    lowered = next(op for op in prefill.functions[0].block.operations if op.name == "runtime.kv.init")
+    assert lowered.attributes["page_tokens"] == 64
+
+
+@pytest.mark.parametrize("layout,page_tokens,capacity,needle", [
+    ("paged", None, 64, "power of two"),
+    ("paged", 24, 96, "power of two"),
+    ("paged", 8, 64, "power of two"),
+    ("paged", 64, 96, "multiple of page_tokens"),
+    ("contiguous_bshd", 64, 64, "only applies to the paged layout"),
+    ("blocked", None, 64, "contiguous_bshd and paged"),
+])
+def test_verifier_rejects_bad_paging(layout, page_tokens, capacity, needle):
+    b = IRBuilder()
+    state = b.argument(KVStateType("bf16", 1, 2, 64, layout=layout, capacity=capacity,
+                                   page_tokens=page_tokens), "state")
+    q = b.argument(TensorType(dims("B", 14, 1, 64), "bf16"), "q")
+    m = b.argument(TensorType(dims("B", 1, 1, "S"), "bf16"), "mask")
+    op = b.emit("serve.decode_attention", [state, q, m], [q.type],
+                attributes={"slot": 0, "groups": 7, "scale": 0.125},
+                effects=(Effect(EffectKind.READ, "kv"),))
+    with pytest.raises(VerificationError) as error:
+        verify_module(Module([Function("f", b.block, op.results)]))
+    assert needle in str(error.value)
+
+
 def test_format_module_is_stable_text():
     text = format_module(_decode_attention_module())
     assert '"serve.decode_attention"' in text and "!serve.kv_state<bf16" in text
