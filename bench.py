@@ -200,6 +200,44 @@ def bench_decode_attention(steps: int, warmup: int, split_tokens: int) -> dict:
     }
 
 
+PAGE_TOKENS = 64
+
+
+def bench_paged_attention(contiguous: dict) -> dict:
+    """The headline decode attention over the paged KV layout: the same
+    tokens in 64-token pages scattered over the pool by a random block table.
+    Same timing as the contiguous leg (dominant kernel by HIP events, graph
+    step time); the ratio to the contiguous kernel is the paging overhead."""
+
+    from stateful_llm_compiler_hip.backends import hip_paged_decode_attention
+
+    device = torch.device("cuda:0")
+    q, k, v, lengths, mask = decode_inputs(device)
+    pages = LMAX // PAGE_TOKENS
+    g = torch.Generator(device="cpu").manual_seed(SEED + 1)
+    table = torch.randperm(BATCH * pages, generator=g).view(BATCH, pages).to(torch.int32).to(device)
+    index = table.view(-1).long()
+    key_pool = torch.empty(BATCH * pages, PAGE_TOKENS, KVH, D, dtype=k.dtype, device=device)
+    value_pool = torch.empty_like(key_pool)
+    key_pool[index] = k.view(BATCH * pages, PAGE_TOKENS, KVH, D)
+    value_pool[index] = v.view(BATCH * pages, PAGE_TOKENS, KVH, D)
+    del k, v
+
+    def step():
+        return hip_paged_decode_attention(q, key_pool, value_pool, table, lengths, mask, scale=D**-0.5)
+
+    step_us = _time_graph(step, reps=GRAPH_STEPS, outer=20)
+    kernel_us = dominant_kernel_us(step, 100)
+    return {
+        "workload": f"same B/L/lengths as the headline, {PAGE_TOKENS}-token pages, random int32 block table",
+        "kernel_us": round(kernel_us, 3),
+        "step_us_graph": round(step_us, 3),
+        "achieved_gbs": round(contiguous["bytes"] / (kernel_us * 1e-6) / 1e9, 2),
+        "kernel_vs_contiguous": round(kernel_us / contiguous["kernel_us"], 4),
+        "step_vs_contiguous": round(step_us / contiguous["step_us"], 4),
+    }
+
+
 MFMA_PEAK_TFLOPS = 2500.0  # dense bf16
 GRAPH_STEPS = 10  # decode-attention steps per graph replay
 
@@ -438,6 +476,7 @@ def main() -> None:
     parser.add_argument("--split-tokens", type=int, default=0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-model", action="store_true", help="skip the decode tok/s leg")
+    parser.add_argument("--no-paged", action="store_true", help="skip the paged-KV decode attention leg")
     parser.add_argument("--no-kernels", action="store_true", help="skip the other-op roofline table")
     parser.add_argument(
         "--model-only", action="store_true",
@@ -505,6 +544,8 @@ def main() -> None:
             "algorithmic_bytes": result["bytes"],
         },
     }
+    if not args.no_paged:
+        line["paged"] = bench_paged_attention(result)
     if not args.no_model:
         tok = bench_decode_tokens()
         line["decode_tok_s"] = round(tok["decode_tok_s"], 1)

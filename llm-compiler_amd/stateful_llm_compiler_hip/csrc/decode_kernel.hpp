@@ -201,6 +201,24 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   }
   const int chunk_start = chunk * chunk_tokens;
 
+  // PG: a window of 64 consecutive block-table entries of this sequence, one
+  // per lane, from page page_base on, read through a resource bounded at the
+  // table's width (entries past it read as 0 and are never used).  A tile
+  // picks its page from a register (readlane) instead of waiting on a table
+  // read before its K/V loads can issue; the first window is requested here,
+  // beside the length, and the window moves (one table read) when a tile
+  // leaves it.
+  int page_base = PG ? __builtin_amdgcn_readfirstlane(chunk_start >> pg.page_shift) : 0;
+  int page_win = 0;
+  const int* page_row = PG ? pg.table + b * pg.table_sb : nullptr;
+  auto load_window = [&]() {
+    const int pages = static_cast<int>(capacity >> pg.page_shift);
+    const __amdgpu_buffer_rsrc_t rt =
+        make_rsrc(page_row + page_base, page_base < pages ? (pages - page_base) * 4 : 0);
+    page_win = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(rt, lane * 4, 0, 0));
+  };
+  if constexpr (PG) load_window();
+
   // Q^T as the B operand: lane (head c, k-slice g) holds dims kk*32+8g..+7.
   // ROPE: the query arrives unrotated and is rotated here; every lane also
   // holds its slices of the new token's rotated key and its value (each
@@ -244,7 +262,6 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   const int64_t seq_off = PG ? kvh * kv_sh : b * kv_sb + kvh * kv_sh;
   const char* kbase = reinterpret_cast<const char*>(key_buffer + seq_off);
   const char* vbase = reinterpret_cast<const char*>(value_buffer + seq_off);
-  const int* page_row = PG ? pg.table + b * pg.table_sb : nullptr;
   constexpr int kMaskBytes = MK == SLC_F32 + 1 ? 4 : 2;
   const char* mbase = MK == 0 ? nullptr
                               : static_cast<const char*>(mask) + b * m_sb * kMaskBytes;
@@ -286,24 +303,58 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     constexpr int kWhich = decltype(which)::value;
     const int rows = bound - t0;
     if constexpr (PG) {
-      // Each 16-row block from its own page (its rows lie in one page), read
-      // through a resource bounded at the chunk end; a block wholly past it
-      // reads no table entry and touches no memory.
+      // Pages of 32 tokens or more hold a whole tile (tiles start at
+      // multiples of 32): one page, one resource per tile.  16-token pages:
+      // each 16-row block from its own page.  A resource is bounded at the
+      // chunk end; a block wholly past it reads no table entry and touches
+      // no memory.
+      auto page_of = [&](int tok) -> int64_t {
+        // Tile starts are wave-uniform: keep the slot and the window base in
+        // scalar registers so the move is a scalar branch.
+        int slot = __builtin_amdgcn_readfirstlane((tok >> pg.page_shift) - page_base);
+        if (static_cast<unsigned>(slot) >= 64u) {  // outside the window: move it
+          page_base = __builtin_amdgcn_readfirstlane(tok >> pg.page_shift);
+          load_window();
+          // Wait for the new window here (vmcnt(0)), on this rare path:
+          // otherwise the compiler cannot tell at the readlane whether the
+          // window is still in flight and drains every tile load before it,
+          // on every tile.
+          __builtin_amdgcn_s_waitcnt(0x0F70);
+          slot = 0;
+        }
+        return __builtin_amdgcn_readlane(page_win, slot);
+      };
+      auto row_offset = [&](int tok, int64_t page) -> int64_t {
+        return (page * pg.page_stride +
+                (tok & ((1 << pg.page_shift) - 1)) * static_cast<int64_t>(kv_ss)) * 2;
+      };
+      if (pg.page_shift >= 5) {
+        const int nbytes = rows <= 0 ? 0 : (rows < 32 ? rows : 32) * row_bytes;
+        const int64_t off = rows > 0 ? row_offset(t0, page_of(t0)) : 0;
+        const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + off, nbytes);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + off, nbytes);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int tok = t0 + 16 * j;
-        const int brows = rows - 16 * j;
-        const int nb = brows <= 0 ? 0 : (brows < 16 ? brows : 16) * row_bytes;
-        const int64_t page = brows > 0 ? page_row[tok >> pg.page_shift] : 0;
-        const int64_t off =
-            (page * pg.page_stride + (tok & ((1 << pg.page_shift) - 1)) * static_cast<int64_t>(kv_ss)) * 2;
-        const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + off, nb);
-        const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + off, nb);
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-          const int o = c * row_bytes + 16 * g + kk * 64;
-          if constexpr ((kWhich & 1) != 0) tile.k[j][kk] = buffer_load16(rk, o);
-          if constexpr ((kWhich & 2) != 0) tile.v[j][kk] = buffer_load16(rv, o);
+          for (int kk = 0; kk < KK; ++kk) {
+            if constexpr ((kWhich & 1) != 0) tile.k[j][kk] = buffer_load16(rk, koff[j] + kk * 64);
+            if constexpr ((kWhich & 2) != 0) tile.v[j][kk] = buffer_load16(rv, koff[j] + kk * 64);
+          }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int tok = t0 + 16 * j;
+          const int brows = rows - 16 * j;
+          const int nb = brows <= 0 ? 0 : (brows < 16 ? brows : 16) * row_bytes;
+          const int64_t off = brows > 0 ? row_offset(tok, page_of(tok)) : 0;
+          const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + off, nb);
+          const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + off, nb);
+#pragma unroll
+          for (int kk = 0; kk < KK; ++kk) {
+            const int o = c * row_bytes + 16 * g + kk * 64;
+            if constexpr ((kWhich & 1) != 0) tile.k[j][kk] = buffer_load16(rk, o);
+            if constexpr ((kWhich & 2) != 0) tile.v[j][kk] = buffer_load16(rv, o);
+          }
         }
       }
     } else {
@@ -406,6 +457,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     return;
   }
   const int chunk_end = min(chunk_start + chunk_tokens, end);
+
 
   using KV = std::integral_constant<int, 3>;
   using KOnly = std::integral_constant<int, 1>;
