@@ -148,8 +148,9 @@ constexpr float kRescaleThreshold = 8.0f;
 // sum; pass 2 streams V and weighs it with the normalised, rounded
 // probabilities.  K and V are each read once.
 // PG: K/V read through a block table (Paging; key_buffer/value_buffer are
-// the page pools); not combined with ROPE.
-template <typename T, int D, int MK, bool L64, bool ROPE, bool EXACT, bool PG = false>
+// the page pools); not combined with ROPE.  PG 1: pages of 32 tokens or more
+// (one page per 32-row tile); PG 2: 16-token pages (one per 16-row block).
+template <typename T, int D, int MK, bool L64, bool ROPE, bool EXACT, int PG = 0>
 __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     const T* __restrict__ query, const T* __restrict__ key_buffer,
     const T* __restrict__ value_buffer, const void* __restrict__ lengths,
@@ -205,9 +206,10 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   // per lane, from page page_base on, read through a resource bounded at the
   // table's width (entries past it read as 0 and are never used).  A tile
   // picks its page from a register (readlane) instead of waiting on a table
-  // read before its K/V loads can issue; the first window is requested here,
-  // beside the length, and the window moves (one table read) when a tile
-  // leaves it.
+  // read before its K/V loads can issue.  The first window is requested here,
+  // beside the length, and covers the first two tiles of every wave; the tile
+  // loop moves it (move_window, one table read) before it loads tiles that
+  // leave it, so the loads themselves never branch.
   int page_base = PG ? __builtin_amdgcn_readfirstlane(chunk_start >> pg.page_shift) : 0;
   int page_win = 0;
   const int* page_row = PG ? pg.table + b * pg.table_sb : nullptr;
@@ -217,7 +219,29 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
         make_rsrc(page_row + page_base, page_base < pages ? (pages - page_base) * 4 : 0);
     page_win = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(rt, lane * 4, 0, 0));
   };
-  if constexpr (PG) load_window();
+  if constexpr (PG != 0) load_window();
+  // Make the window hold the pages of tokens lo..hi (at most 64 pages apart).
+  auto move_window = [&](int lo, int hi) {
+    if constexpr (PG != 0) {
+      const int lo_page = lo >> pg.page_shift;
+      const int hi_page = hi >> pg.page_shift;
+      if (static_cast<unsigned>(lo_page - page_base) >= 64u || hi_page - page_base >= 64) {
+        page_base = __builtin_amdgcn_readfirstlane(lo_page);
+        load_window();
+        // Wait for the window here (vmcnt(0)), on this rare path: otherwise
+        // the compiler cannot tell at a readlane whether the window is still
+        // in flight and drains every tile load before it, on every tile.
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+      }
+    }
+  };
+  // The pool byte offset of token tok's row (its page from the window).
+  auto page_offset = [&](int tok) -> int64_t {
+    const int slot = __builtin_amdgcn_readfirstlane((tok >> pg.page_shift) - page_base);
+    const int64_t page = __builtin_amdgcn_readlane(page_win, slot);
+    return (page * pg.page_stride +
+            (tok & ((1 << pg.page_shift) - 1)) * static_cast<int64_t>(kv_ss)) * 2;
+  };
 
   // Q^T as the B operand: lane (head c, k-slice g) holds dims kk*32+8g..+7.
   // ROPE: the query arrives unrotated and is rotated here; every lane also
@@ -258,7 +282,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     }
   }
 
-  // PG: the pools' kv-head column; the page comes per 16-row block.
+  // PG: the pools' kv-head column; the page comes per tile (or 16-row block).
   const int64_t seq_off = PG ? kvh * kv_sh : b * kv_sb + kvh * kv_sh;
   const char* kbase = reinterpret_cast<const char*>(key_buffer + seq_off);
   const char* vbase = reinterpret_cast<const char*>(value_buffer + seq_off);
@@ -302,59 +326,37 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   auto load_tile = [&](int t0, Tile& tile, int bound, auto which) {
     constexpr int kWhich = decltype(which)::value;
     const int rows = bound - t0;
-    if constexpr (PG) {
+    if constexpr (PG == 1) {
       // Pages of 32 tokens or more hold a whole tile (tiles start at
-      // multiples of 32): one page, one resource per tile.  16-token pages:
-      // each 16-row block from its own page.  A resource is bounded at the
-      // chunk end; a block wholly past it reads no table entry and touches
-      // no memory.
-      auto page_of = [&](int tok) -> int64_t {
-        // Tile starts are wave-uniform: keep the slot and the window base in
-        // scalar registers so the move is a scalar branch.
-        int slot = __builtin_amdgcn_readfirstlane((tok >> pg.page_shift) - page_base);
-        if (static_cast<unsigned>(slot) >= 64u) {  // outside the window: move it
-          page_base = __builtin_amdgcn_readfirstlane(tok >> pg.page_shift);
-          load_window();
-          // Wait for the new window here (vmcnt(0)), on this rare path:
-          // otherwise the compiler cannot tell at the readlane whether the
-          // window is still in flight and drains every tile load before it,
-          // on every tile.
-          __builtin_amdgcn_s_waitcnt(0x0F70);
-          slot = 0;
+      // multiples of 32): one page, one resource per tile, bounded at the
+      // chunk end.
+      const int nbytes = rows <= 0 ? 0 : (rows < 32 ? rows : 32) * row_bytes;
+      const int64_t off = rows > 0 ? page_offset(t0) : 0;
+      const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + off, nbytes);
+      const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + off, nbytes);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+          if constexpr ((kWhich & 1) != 0) tile.k[j][kk] = buffer_load16(rk, koff[j] + kk * 64);
+          if constexpr ((kWhich & 2) != 0) tile.v[j][kk] = buffer_load16(rv, koff[j] + kk * 64);
         }
-        return __builtin_amdgcn_readlane(page_win, slot);
-      };
-      auto row_offset = [&](int tok, int64_t page) -> int64_t {
-        return (page * pg.page_stride +
-                (tok & ((1 << pg.page_shift) - 1)) * static_cast<int64_t>(kv_ss)) * 2;
-      };
-      if (pg.page_shift >= 5) {
-        const int nbytes = rows <= 0 ? 0 : (rows < 32 ? rows : 32) * row_bytes;
-        const int64_t off = rows > 0 ? row_offset(t0, page_of(t0)) : 0;
-        const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + off, nbytes);
-        const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + off, nbytes);
+    } else if constexpr (PG == 2) {
+      // 16-token pages: each 16-row block from its own page; a block wholly
+      // past the chunk end touches no memory.
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < 2; ++j) {
+        const int tok = t0 + 16 * j;
+        const int brows = rows - 16 * j;
+        const int nb = brows <= 0 ? 0 : (brows < 16 ? brows : 16) * row_bytes;
+        const int64_t off = brows > 0 ? page_offset(tok) : 0;
+        const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + off, nb);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + off, nb);
 #pragma unroll
-          for (int kk = 0; kk < KK; ++kk) {
-            if constexpr ((kWhich & 1) != 0) tile.k[j][kk] = buffer_load16(rk, koff[j] + kk * 64);
-            if constexpr ((kWhich & 2) != 0) tile.v[j][kk] = buffer_load16(rv, koff[j] + kk * 64);
-          }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int tok = t0 + 16 * j;
-          const int brows = rows - 16 * j;
-          const int nb = brows <= 0 ? 0 : (brows < 16 ? brows : 16) * row_bytes;
-          const int64_t off = brows > 0 ? row_offset(tok, page_of(tok)) : 0;
-          const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + off, nb);
-          const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + off, nb);
-#pragma unroll
-          for (int kk = 0; kk < KK; ++kk) {
-            const int o = c * row_bytes + 16 * g + kk * 64;
-            if constexpr ((kWhich & 1) != 0) tile.k[j][kk] = buffer_load16(rk, o);
-            if constexpr ((kWhich & 2) != 0) tile.v[j][kk] = buffer_load16(rv, o);
-          }
+        for (int kk = 0; kk < KK; ++kk) {
+          const int o = c * row_bytes + 16 * g + kk * 64;
+          if constexpr ((kWhich & 1) != 0) tile.k[j][kk] = buffer_load16(rk, o);
+          if constexpr ((kWhich & 2) != 0) tile.v[j][kk] = buffer_load16(rv, o);
         }
       }
     } else {
@@ -409,7 +411,13 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   end64 = end64 < 0 ? 0 : end64;
   end64 = end64 < mask_len ? end64 : mask_len;
   end64 = end64 < capacity ? end64 : capacity;
-  const int end = static_cast<int>(end64);  // host guarantees capacity < 2^30
+  // Host guarantees capacity < 2^30.  The length is one sequence's, so the
+  // end is wave-uniform: readfirstlane puts it (and every loop bound derived
+  // from it) in scalar registers.  Left in a vector register, the tile loop
+  // is compiled as a divergent loop whose exit paths differ in loads issued,
+  // and the compiler then waits for every load in flight (vmcnt(0)) at the
+  // top of each iteration, draining the tile prefetch.
+  const int end = __builtin_amdgcn_readfirstlane(static_cast<int>(end64));
   LenAdvance adv{nullptr, 0, nullptr, 0, nullptr, capacity};
   // ROPE: rotate the new key and write its row (and the value's) from the
   // workgroup of the chunk holding it (the last chunk when it lies past the
@@ -465,6 +473,11 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   using First = std::conditional_t<EXACT, KOnly, KV>;
   Tile ta, tb;
   load_tile(t_first, ta, chunk_end, First{});
+  // Keep tile A's loads ahead of tile B's.  The loop's first step waits for
+  // A; issued last, A would need every load drained (vmcnt(0)), and that
+  // wait, placed in the loop header, would then drain the prefetch on every
+  // iteration.
+  __builtin_amdgcn_sched_barrier(0);
   load_tile(t_first + kStride, tb, chunk_end, First{});
   if constexpr (ROPE) {
     rope_slices<T, KK>(qraw, cs, sn);
@@ -601,6 +614,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   };
   auto sweep = [&](auto body, auto which) {
     for (int t0 = t_first; t0 < chunk_end; t0 += 2 * kStride) {
+      if (t0 + 2 * kStride < chunk_end) move_window(t0 + 2 * kStride, t0 + 3 * kStride + kTile - 1);
       patch(t0, ta);
       body(t0, ta);
       load_tile(t0 + 2 * kStride, ta, chunk_end, which);
@@ -617,6 +631,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   if constexpr (EXACT) {
     // Pass 1, then the row max and sum over the 4 lane groups and the waves.
     sweep(score_tile, KOnly{});
+    move_window(t_first, t_first + kStride + kTile - 1);
     load_tile(t_first, ta, chunk_end, VOnly{});  // pass 2's first tiles fly
     load_tile(t_first + kStride, tb, chunk_end, VOnly{});  // during the combine
     l_run += __shfl_xor(l_run, 16, 64);
@@ -941,7 +956,7 @@ int64_t exact_max_tokens(int64_t head_dim) {
 // Status of a fused call the kernels cannot take (nothing was launched).
 constexpr int kUnsupported = -2;
 
-template <typename T, int D, int MK, bool L64, bool ROPE, bool EXACT, bool PG = false>
+template <typename T, int D, int MK, bool L64, bool ROPE, bool EXACT, int PG = 0>
 hipError_t exact_lds_limit(int bytes) {
   // Dynamic LDS above the 64 KB default needs the kernel's opt-in (once per
   // instantiation; the attribute is per function).

@@ -29,7 +29,9 @@ int page_shift_of(int64_t page_tokens) {
   return shift;
 }
 
-template <typename T, int D>
+// PGM: the kernel's page regime (1: pages hold whole 32-token tiles, 2:
+// 16-token pages).
+template <typename T, int D, int PGM>
 int launch_paged(const void* query, const void* kp, const void* vp, const void* lengths,
                  int lengths_dtype, const void* mask, int mask_dtype, void* output,
                  void* workspace, int* counters, int64_t batch, int64_t q_heads,
@@ -54,10 +56,10 @@ int launch_paged(const void* query, const void* kp, const void* vp, const void* 
   const RopeStore rs{};
 #define SLC_PAGED_K(MK, L64, EX)                                                            \
   do {                                                                                      \
-    if (EX && exact_lds_limit<T, D, MK, L64, false, EX, true>(static_cast<int>(dyn_lds)) !=  \
+    if (EX && exact_lds_limit<T, D, MK, L64, false, EX, PGM>(static_cast<int>(dyn_lds)) !=  \
                   hipSuccess)                                                               \
       return slc_host::check_launch("slc_hip_paged_decode_attention(exact LDS opt-in)");    \
-    hipLaunchKernelGGL((decode_attention_mfma_kernel<T, D, MK, L64, false, EX, true>), grid, \
+    hipLaunchKernelGGL((decode_attention_mfma_kernel<T, D, MK, L64, false, EX, PGM>), grid, \
                        dim3(kThreads), dyn_lds, stream, static_cast<const T*>(query),       \
                        static_cast<const T*>(kp), static_cast<const T*>(vp), lengths,       \
                        lengths_dtype, mask, mask_dtype, static_cast<T*>(output), part_o,    \
@@ -203,10 +205,11 @@ extern "C" int slc_hip_paged_decode_attention(
                          mask_stride_b, mask_stride_s, out_stride_b, out_stride_h};
   const Paging pg{block_table, table_stride_b, shift, page_stride};
   hipStream_t s = static_cast<hipStream_t>(stream);
-#define SLC_PAGED_CALL(TT, DD)                                                                  \
-  launch_paged<TT, DD>(query, key_pool, value_pool, lengths, lengths_dtype, mask, mask_dtype,  \
-                       output, workspace, counters, batch, q_heads, kv_heads, capacity,        \
-                       mask_len, st, scale, chunk, nchunks, exact, pg, s)
+#define SLC_PAGED_CALL(TT, DD)                                                              \
+  (shift >= 5 ? launch_paged<TT, DD, 1> : launch_paged<TT, DD, 2>)(                          \
+      query, key_pool, value_pool, lengths, lengths_dtype, mask, mask_dtype, output, workspace, \
+      counters, batch, q_heads, kv_heads, capacity, mask_len, st, scale, chunk, nchunks, exact, \
+      pg, s)
   if (dtype == SLC_BF16) {
     if (head_dim == 64) return SLC_PAGED_CALL(slc::bf16_t, 64);
     return SLC_PAGED_CALL(slc::bf16_t, 128);
