@@ -25,7 +25,8 @@ __device__ __forceinline__ void merge_if_last(const float* part_o, const float* 
                                               int nchunks, const LenAdvance& adv) {
   const int tid = threadIdx.x;
   __shared__ int is_last;
-  __syncthreads();  // every wave's partial stores precede thread 0's release
+  stores_complete();  // this thread's partial stores are done ...
+  __syncthreads();    // ... and, past the barrier, every thread's
   if (tid == 0) {
     int* counter = counters + b * kv_heads + kvh;
     const int len_before = adv.counter != nullptr ? count_arrival(adv.counter) : 0;

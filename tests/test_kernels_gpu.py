@@ -262,6 +262,30 @@ def test_decode_attention_balanced_is_deterministic(gpu):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
 
 
+@pytest.mark.parametrize("split", [0, 256, SPLIT_BALANCED])
+def test_decode_attention_merge_reads_fresh_partials(gpu, split):
+    # Back-to-back calls on one workspace alternate between two inputs whose
+    # partials differ everywhere: a merge that read a partial of the previous
+    # call (a stale copy in some XCD's L2) would break bitwise repeatability.
+    from stateful_llm_compiler_hip.backends import hip_decode_attention
+
+    announce(f"decode bf16 merge freshness B=32 L=8192 split_tokens={split}")
+    g = generator(6)
+    lengths = torch.randint(4096, 8193, (32,), generator=g).to(gpu)
+    k = torch.randn(32, 8192, 2, 64, generator=g).bfloat16().to(gpu)
+    v = torch.randn(32, 8192, 2, 64, generator=g).bfloat16().to(gpu)
+    queries = [torch.randn(32, 14, 1, 64, generator=g).bfloat16().to(gpu) for _ in range(2)]
+    first = [hip_decode_attention(q, k, v, lengths, None, scale=0.125, split_tokens=split)
+             for q in queries]
+    torch.cuda.synchronize()
+    assert not torch.equal(first[0], first[1])
+    outs = [hip_decode_attention(queries[i % 2], k, v, lengths, None, scale=0.125, split_tokens=split)
+            for i in range(40)]
+    torch.cuda.synchronize()
+    for i, out in enumerate(outs):
+        assert torch.equal(out, first[i % 2]), f"call {i} differs from the first call on its input"
+
+
 @pytest.mark.parametrize("split", [0, 64, SPLIT_BALANCED])
 def test_decode_attention_empty_sequences(gpu, split):
     # A sequence with no attended token is a softmax over an empty row: NaN,
