@@ -25,14 +25,16 @@ __device__ __forceinline__ void merge_if_last(const float* part_o, const float* 
                                               int nchunks, const LenAdvance& adv) {
   const int tid = threadIdx.x;
   __shared__ int is_last;
-  stores_complete();  // this thread's partial stores are done ...
-  __syncthreads();    // ... and, past the barrier, every thread's
+  __syncthreads();  // every wave's partial stores precede thread 0's release
   if (tid == 0) {
     int* counter = counters + b * kv_heads + kvh;
-    const int len_before = adv.counter != nullptr ? count_arrival(adv.counter) : 0;
+    const int len_before = adv.counter != nullptr ? count_only(adv.counter) : 0;
     const int before = count_arrival(counter);
     is_last = before == nchunks - 1;
-    if (is_last) rearm(counter);
+    if (is_last) {
+      acquire_partials();
+      rearm(counter);
+    }
     finish_advance(adv, len_before);
   }
   __syncthreads();
@@ -714,7 +716,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   if constexpr (ROPE) {
     // One chunk: no merge to carry the advance.  Every wave read the length
     // before the combine's barriers, so the count may be bumped now.
-    if (nchunks == 1 && tid == 0) finish_advance(adv, count_arrival(adv.counter));
+    if (nchunks == 1 && tid == 0) finish_advance(adv, count_only(adv.counter));
   }
   if (nchunks > 1 && counters != nullptr) {
     __syncthreads();  // the merge reuses the LDS

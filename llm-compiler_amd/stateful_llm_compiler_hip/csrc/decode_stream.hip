@@ -18,11 +18,10 @@
 //    into another sequence would refill its load pipeline at loaded-memory
 //    latency).  The host sizes the grid from the CU count and the capacity.
 //  * A sequence of one piece is written directly.  Otherwise each piece
-//    stores its (max, sum, acc) in the workgroup's slot with agent-scope
-//    atomic stores, waits for them to complete and counts its arrival; the
-//    workgroup whose arrival completes the sequence's count folds the pieces
-//    in order (deterministic for given lengths), read with agent-scope
-//    atomic loads.
+//    stores its (max, sum, acc) in the workgroup's slot; after one agent-
+//    scope release fence per workgroup, the workgroup whose arrival completes
+//    the sequence's count takes an acquire fence and folds the pieces in
+//    order (deterministic for given lengths).
 //  * The fused RoPE + KV store + attention op keeps the fixed-chunk grid, so
 //    this variant is the plain op's only.
 // One workgroup = 4 wavefronts; the tile math (MFMA scores, lazy-rescale
@@ -448,18 +447,14 @@ __global__ __launch_bounds__(kThreads) void decode_stream_kernel(StreamParams p)
         out[2] = slc::from_f32<T>(osum.z / lsum);
         out[3] = slc::from_f32<T>(osum.w / lsum);
       } else {
-        publish(slot + hd * D + d0, osum.x);
-        publish(slot + hd * D + d0 + 1, osum.y);
-        publish(slot + hd * D + d0 + 2, osum.z);
-        publish(slot + hd * D + d0 + 3, osum.w);
+        *reinterpret_cast<float4*>(slot + hd * D + d0) = osum;
         if (d0 == 0) {
-          publish(slot + cols * D + hd, mmax);
-          publish(slot + cols * D + cols + hd, lsum);
+          slot[cols * D + hd] = mmax;
+          slot[cols * D + cols + hd] = lsum;
         }
       }
     }
-    stores_complete();  // the partial's stores are done before the arrival
-    __syncthreads();    // the combine area is reused by the next piece
+    __syncthreads();  // the combine area is reused by the next piece
   };
 
   // ---- the workgroup's piece(s) ----------------------------------------------
@@ -495,18 +490,20 @@ __global__ __launch_bounds__(kThreads) void decode_stream_kernel(StreamParams p)
   // ---- arrival: merge a completed sequence, advance the lengths -------------
   if (part_seg < 0) return;
   if (tid == 0) {
-    // Every thread's partial stores completed before the barrier that ended
-    // the piece; the partials travel as agent-scope atomics (no L2 write-back
-    // or invalidation needed, see decode_tiles.hpp).
+    // The barrier ending the piece ordered every wave's partial stores before
+    // this thread's release.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     int last = 0;
     if (part_seg >= 0) {
       int* counter = p.seg_counters + part_seg;
-      const int before = count_arrival(counter);
+      const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
       if (before == part_np - 1) {
         rearm(counter);
         last |= 1;
       }
     }
+    if (last != 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     s_last = last;
   }
   __syncthreads();
@@ -533,10 +530,9 @@ __global__ __launch_bounds__(kThreads) void decode_stream_kernel(StreamParams p)
 #pragma unroll
         for (int k = 0; k < U; ++k) {
           const float* sl = slot_of(k0 + k < np ? k0 + k : 0);
-          m[k] = fetch_partial(sl + cols * D + hd);
-          l[k] = fetch_partial(sl + cols * D + cols + hd);
-          a[k] = make_float4(fetch_partial(sl + hd * D + d0), fetch_partial(sl + hd * D + d0 + 1),
-                             fetch_partial(sl + hd * D + d0 + 2), fetch_partial(sl + hd * D + d0 + 3));
+          m[k] = sl[cols * D + hd];
+          l[k] = sl[cols * D + cols + hd];
+          a[k] = *reinterpret_cast<const float4*>(sl + hd * D + d0);
         }
 #pragma unroll
         for (int k = 0; k < U; ++k) {

@@ -101,18 +101,17 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int 
 // per batch for the RoPE variant's length advance); it is zero-filled once by
 // its owner and every kernel leaves it zero again.
 //
-// Every value that crosses workgroups inside a kernel -- the partials and the
-// counters -- is written and read with agent-scope atomic accesses.  On
-// gfx950 those carry the sc1 scope bit: a store is written through the XCD's
-// L2 and a load reads coherently, so they need none of the L2 write-back and
-// invalidation that an agent-scope release / acquire fence adds for plain
-// accesses (about 2.6 us per launch at batch 32 x 8192 tokens).  What the
-// protocol needs from a fence is the order, and it gets that explicitly:
-//  * every thread waits for its own partial stores to complete
-//    (stores_complete: vmcnt(0)) before the workgroup barrier;
-//  * after the barrier one thread bumps the (batch, kv-head)'s counter;
-//  * the workgroup that completes the count learns so from the add's return
-//    value and only then, behind a second barrier, loads the partials.
+// Every split workgroup publishes its partial, meets its waves at a barrier,
+// and one thread counts the workgroup's arrival with an agent-scope release
+// add: the barrier (a workgroup-scope fence) orders every wave's stores before
+// that thread, and the release orders them before the count.  Only the
+// workgroup whose add completes the count takes an agent-scope acquire fence
+// before its waves, behind a second barrier, load the partials.  Release
+// sequence + acquire fence: the HIP memory model's synchronisation, with the
+// L2 invalidation of the acquire paid once per (batch, kv-head) instead of
+// by every workgroup.  (Relaxed adds with only the hardware ordering of
+// completed stores would save the release's L2 write-back too, 1.9 us per
+// launch at batch 32 x 8192 tokens, but the model does not order them.)
 // The merge weighs the chunks exactly as the separate merge kernel does, so
 // both paths give bit-identical outputs.  Two calls that share counters must
 // not run concurrently (calls on one stream never do).
@@ -122,12 +121,16 @@ __device__ __forceinline__ void publish(float* p, float v) {
 __device__ __forceinline__ float fetch_partial(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// Wait until every store this thread issued has completed (vmcnt(0); the
-// expcnt and lgkmcnt fields of the encoding are left at their maxima).
-__device__ __forceinline__ void stores_complete() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 __device__ __forceinline__ int count_arrival(int* counter) {
+  return __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+// A count that orders no data: the length advance's last arrival writes the
+// new length, which only later kernels read; the add's atomicity suffices.
+__device__ __forceinline__ int count_only(int* counter) {
   return __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// The completing workgroup's side of the pairing.
+__device__ __forceinline__ void acquire_partials() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
 __device__ __forceinline__ void rearm(int* counter) {
   __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
