@@ -313,3 +313,44 @@ def test_paged_state_rejects_layout_mismatch(gpu):
         paged_rt.decode(token, dmask, plain)
     with pytest.raises(ExecutionError):
         PagedKVCacheState.from_layer_tensors(cache, capacity=CAPACITY, page_tokens=24)
+
+
+def test_two_graph_decoders_replay_concurrently(gpu):
+    """Two decoders (each with its own workspace and its own copy of the KV
+    state) replayed at the same time on two streams give the tokens and
+    logits of a sequential run: their cross-workgroup counters and partials
+    are not shared."""
+
+    from dataclasses import replace
+
+    announce("two graph decoders replayed concurrently on two streams")
+    weights = {k: v.to(gpu) for k, v in init_weights(CONFIG1, seed=0).items()}
+    rt = Qwen2Runtime(CONFIG1, weights, capacity=CAPACITY, device=str(gpu))
+    ids, mask, pos = _prompt()
+    logits, state = rt.prefill(ids.to(gpu), mask.to(gpu), pos.to(gpu))
+    first = logits[:, -1].argmax(-1)
+
+    def copy(s):
+        return replace(s, keys=tuple(k.clone() for k in s.keys), values=tuple(v.clone() for v in s.values),
+                       lengths=tuple(n.clone() for n in s.lengths),
+                       overflow=torch.zeros(1, dtype=torch.int32, device=gpu), zero_slots=None)
+
+    # Sequential reference on a third copy.
+    reference = rt.graph_decoder(copy(state), first)
+    expected = []
+    for _ in range(STEPS):
+        reference.step()
+        torch.cuda.synchronize()
+        expected.append((reference.tokens.clone().cpu(), reference.logits.clone().cpu()))
+
+    decoders = [rt.graph_decoder(copy(state), first), rt.graph_decoder(copy(state), first)]
+    streams = [torch.cuda.Stream(device=gpu), torch.cuda.Stream(device=gpu)]
+    torch.cuda.synchronize()
+    for step in range(STEPS):
+        for decoder, stream in zip(decoders, streams):
+            with torch.cuda.stream(stream):
+                decoder.step()
+        torch.cuda.synchronize()
+        for decoder in decoders:
+            assert torch.equal(decoder.tokens.cpu(), expected[step][0])
+            assert torch.equal(decoder.logits.cpu(), expected[step][1])
