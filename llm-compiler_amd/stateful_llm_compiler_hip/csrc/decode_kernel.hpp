@@ -474,14 +474,18 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   using KOnly = std::integral_constant<int, 1>;
   using VOnly = std::integral_constant<int, 2>;
   using First = std::conditional_t<EXACT, KOnly, KV>;
-  Tile ta, tb;
-  load_tile(t_first, ta, chunk_end, First{});
-  // Keep tile A's loads ahead of tile B's.  The loop's first step waits for
-  // A; issued last, A would need every load drained (vmcnt(0)), and that
-  // wait, placed in the loop header, would then drain the prefetch on every
-  // iteration.
-  __builtin_amdgcn_sched_barrier(0);
-  load_tile(t_first + kStride, tb, chunk_end, First{});
+  // kTilesInFlight tiles per wave: tile i is consumed, then refilled
+  // kTilesInFlight sweeps ahead.  sched_barrier keeps each prologue tile's
+  // loads ahead of the next one's: the loop consumes them in that order, and
+  // a later tile issued first would make the first step wait for every load
+  // (vmcnt(0)) -- a wait that, sitting in the loop header, would then drain
+  // the prefetch on every iteration.
+  Tile tiles[kTilesInFlight];
+#pragma unroll
+  for (int i = 0; i < kTilesInFlight; ++i) {
+    load_tile(t_first + i * kStride, tiles[i], chunk_end, First{});
+    __builtin_amdgcn_sched_barrier(0);
+  }
   if constexpr (ROPE) {
     rope_slices<T, KK>(qraw, cs, sn);
 #pragma unroll
@@ -615,17 +619,22 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
       }
     }
   };
+  constexpr int kAhead = kTilesInFlight * kStride;
+  // The exit past the chunk end leaves the whole sweep (not just the inner
+  // step): every path back to the loop header then carries the same loads.
   auto sweep = [&](auto body, auto which) {
-    for (int t0 = t_first; t0 < chunk_end; t0 += 2 * kStride) {
-      if (t0 + 2 * kStride < chunk_end) move_window(t0 + 2 * kStride, t0 + 3 * kStride + kTile - 1);
-      patch(t0, ta);
-      body(t0, ta);
-      load_tile(t0 + 2 * kStride, ta, chunk_end, which);
-      if (t0 + kStride >= chunk_end) break;
-      patch(t0 + kStride, tb);
-      body(t0 + kStride, tb);
-      load_tile(t0 + 3 * kStride, tb, chunk_end, which);
+    for (int t0 = t_first; t0 < chunk_end; t0 += kAhead) {
+      if (t0 + kAhead < chunk_end) move_window(t0 + kAhead, t0 + kAhead + kAhead - kStride + kTile - 1);
+#pragma unroll
+      for (int i = 0; i < kTilesInFlight; ++i) {
+        const int tt = t0 + i * kStride;
+        if (i > 0 && tt >= chunk_end) goto done;
+        patch(tt, tiles[i]);
+        body(tt, tiles[i]);
+        load_tile(tt + kAhead, tiles[i], chunk_end, which);
+      }
     }
+  done:;
   };
 
   float* sm_m = reinterpret_cast<float*>(smem);
@@ -634,9 +643,12 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   if constexpr (EXACT) {
     // Pass 1, then the row max and sum over the 4 lane groups and the waves.
     sweep(score_tile, KOnly{});
-    move_window(t_first, t_first + kStride + kTile - 1);
-    load_tile(t_first, ta, chunk_end, VOnly{});  // pass 2's first tiles fly
-    load_tile(t_first + kStride, tb, chunk_end, VOnly{});  // during the combine
+    move_window(t_first, t_first + kAhead - kStride + kTile - 1);
+#pragma unroll
+    for (int i = 0; i < kTilesInFlight; ++i) {  // pass 2's first tiles fly during the combine
+      load_tile(t_first + i * kStride, tiles[i], chunk_end, VOnly{});
+      __builtin_amdgcn_sched_barrier(0);
+    }
     l_run += __shfl_xor(l_run, 16, 64);
     l_run += __shfl_xor(l_run, 32, 64);
     if (g == 0) {

@@ -21,6 +21,10 @@ constexpr int kTile = 32;   // tokens per wave iteration
 #endif
 constexpr int kWaves = SLC_DECODE_WAVES;  // wavefronts per split-kernel workgroup
 constexpr int kThreads = kWaves * 64;
+#ifndef SLC_DECODE_TILES
+#define SLC_DECODE_TILES 2
+#endif
+constexpr int kTilesInFlight = SLC_DECODE_TILES;  // K/V tiles in flight per wave (split kernel)
 constexpr int kGenericWaves = 4;          // wavefronts of the generic kernel
 constexpr int kMaxGroups = 16;
 constexpr int kMaxChunks = 256;  // split-sequence chunks per (batch, kv-head), merge LDS
