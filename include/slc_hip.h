@@ -16,7 +16,8 @@
  *   slc_hip_decode_attention   backends/triton_attention.py:134-210
  *                              (triton_decode_attention; semantics of
  *                              execution.py:281-327)
- *   slc_hip_paged_decode_attention, slc_hip_paged_kv_store: the paged layout
+ *   slc_hip_paged_decode_attention, slc_hip_paged_kv_store,
+ *   slc_hip_paged_rope_decode_attention: the paged layout
  *                              the reference plans next (docs/kv-bufferization.md:317-323)
  *   slc_hip_kv_store           backends/triton_kv.py:71-129 (triton_kv_store;
  *                              semantics of execution.py:743-781 native_kv_store)
@@ -246,6 +247,30 @@ SLC_API int slc_hip_paged_kv_store(
     int* overflow, int dtype, int64_t batch, int64_t heads, int64_t tokens, int64_t head_dim,
     int64_t key_stride_b, int64_t key_stride_h, int64_t key_stride_t, int64_t value_stride_b,
     int64_t value_stride_h, int64_t value_stride_t, void* stream);
+
+/*
+ * slc_hip_paged_rope_decode_attention: slc_hip_rope_decode_attention over the
+ * paged layout (the paged attention's pool, block-table and page arguments,
+ * the RoPE variant's key/value/cosine/sine, lengths_out and overflow): RoPE of
+ * the query and the new key, the new key and value row written at position
+ * lengths[b] of sequence b (its page from the block table), the length
+ * advance and the attention, in one kernel; equal bit for bit to RoPE, the
+ * paged KV store and the paged attention run in turn.  Returns
+ * SLC_ERR_UNSUPPORTED (nothing launched) for the cases its kernel does not
+ * take, as slc_hip_rope_decode_attention does.  Workspace and counters as for
+ * slc_hip_decode_attention_workspace_size(..., 0) / _counter_count.
+ */
+SLC_API int slc_hip_paged_rope_decode_attention(
+    const void* query, const void* key, const void* value, const void* cosine, const void* sine,
+    void* key_pool, void* value_pool, const int* block_table, int64_t table_stride_b,
+    int64_t pages_per_seq, int64_t page_tokens, int64_t page_stride, const int64_t* lengths,
+    int64_t* lengths_out, int* overflow, const void* mask, int mask_dtype, void* output,
+    void* workspace, int64_t workspace_bytes, int* counters, int64_t num_counters, int dtype,
+    int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t mask_len,
+    int64_t q_stride_b, int64_t q_stride_h, int64_t k_stride_b, int64_t k_stride_h,
+    int64_t v_stride_b, int64_t v_stride_h, int64_t cos_stride_b, int64_t sin_stride_b,
+    int64_t kv_stride_s, int64_t kv_stride_h, int64_t mask_stride_b, int64_t mask_stride_s,
+    int64_t out_stride_b, int64_t out_stride_h, float scale, int softmax_order, void* stream);
 
 /* Longest mask the SLC_SOFTMAX_EXACT order takes (INT64_MAX: no limit). */
 SLC_API int64_t slc_hip_decode_attention_exact_max_tokens(int64_t head_dim, int dtype);

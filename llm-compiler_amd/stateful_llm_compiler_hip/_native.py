@@ -95,6 +95,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_P, _P, _P, _P, _L, _L, _L, _L, _P, _I, _P, _I, _P, _P, _L, _P, _L, _I]
         + [_L] * 13 + [_F, _L, _I, _P],
     ),
+    "slc_hip_paged_rope_decode_attention": (
+        _I,
+        [_P] * 7 + [_P, _L, _L, _L, _L, _P, _P, _P, _P, _I, _P, _P, _L, _P, _L, _I]
+        + [_L] * 4 + [_L] * 15 + [_F, _I, _P],
+    ),
     "slc_hip_paged_kv_store": (
         _I,
         [_P, _P, _P, _L, _L, _L, _L, _L, _L, _P, _P, _P, _P, _I] + [_L] * 10 + [_P],

@@ -12,7 +12,7 @@ from .hip_fused import (
     hip_rope_kv_store,
 )
 from .hip_kv import hip_kv_store
-from .hip_paged import hip_paged_decode_attention, hip_paged_kv_store
+from .hip_paged import hip_paged_decode_attention, hip_paged_kv_store, hip_paged_rope_decode_attention
 from .hip_linear import hip_linear
 from .hip_ops import (
     hip_add,
@@ -43,6 +43,7 @@ __all__ = [
     "hip_kv_store",
     "hip_paged_decode_attention",
     "hip_paged_kv_store",
+    "hip_paged_rope_decode_attention",
     "hip_linear",
     "hip_prefill_attention",
     "hip_rms_norm",

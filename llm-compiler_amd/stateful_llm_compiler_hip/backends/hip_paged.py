@@ -153,3 +153,90 @@ def hip_paged_kv_store(
         value.stride(0), value.stride(1), value.stride(2), _native.current_stream(key.device),
     )
     _native.check(status, "slc_hip_paged_kv_store")
+
+
+_UNSUPPORTED = -2  # SLC_ERR_UNSUPPORTED
+
+
+def hip_paged_rope_decode_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    cosine: torch.Tensor,
+    sine: torch.Tensor,
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    block_table: torch.Tensor,
+    lengths: torch.Tensor,
+    lengths_out: torch.Tensor,
+    attention_mask: torch.Tensor | None,
+    *,
+    scale: float,
+    overflow: torch.Tensor | None = None,
+    softmax_order: str = "online",
+    workspace: _native.DeviceWorkspace | None = None,
+) -> torch.Tensor | None:
+    """``hip_rope_decode_attention`` over paged K/V: RoPE, the new row written
+    at ``lengths[b]`` of sequence b (its page from ``block_table``), the
+    length advance into ``lengths_out`` and the attention, in one kernel; bit
+    for bit RoPE, ``hip_paged_kv_store`` and ``hip_paged_decode_attention``
+    run in turn.  Returns None, having done nothing, when the fused kernel does
+    not take the case (the caller then runs the three ops)."""
+
+    what = "HIP paged rope decode attention"
+    order = _native.softmax_order_tag(softmax_order)
+    check_flag(overflow, what)
+    tensors = [query, key, value, cosine, sine, key_pool, value_pool, block_table, lengths, lengths_out]
+    if attention_mask is not None:
+        tensors.append(attention_mask)
+    if not all(t.is_cuda for t in tensors):
+        return None
+    if (query.ndim != 4 or query.shape[2] != 1 or key.ndim != 4 or key.shape != value.shape
+            or key.shape[2] != 1 or cosine.ndim != 3 or cosine.shape != sine.shape):
+        return None
+    batch, query_heads, _, head_dim = query.shape
+    try:
+        pages_per_seq, page_tokens = _check_pools(key_pool, value_pool, block_table, batch, what)
+    except ValueError:
+        return None
+    kv_heads = key.shape[1]
+    if (key.shape[0] != batch or key_pool.shape[2] != kv_heads or key_pool.shape[3] != head_dim
+            or key.shape[3] != head_dim or cosine.shape != (batch, 1, head_dim)
+            or query_heads % kv_heads or lengths.shape != (batch,) or lengths_out.shape != (batch,)
+            or lengths.dtype != torch.int64 or lengths_out.dtype != torch.int64
+            or any(t.dtype != query.dtype for t in (key, value, cosine, sine, key_pool))
+            or any(t.stride(-1) != 1 for t in (query, key, value, cosine, sine))):
+        return None
+    if attention_mask is not None and (
+        attention_mask.ndim != 4 or attention_mask.shape[:3] != (batch, 1, 1)
+        or attention_mask.dtype not in (torch.float16, torch.bfloat16, torch.float32)
+    ):
+        return None
+    capacity = pages_per_seq * page_tokens
+    output = torch.empty_like(query)
+    if batch == 0:
+        return output
+    lib = _native.library()
+    dtype = _native.dtype_tag(query.dtype)
+    mask_ptr, mask_dtype, mask_sb, mask_ss, mask_len = _mask_args(attention_mask, capacity)
+    if mask_len > capacity:
+        return None
+    nbytes = lib.slc_hip_decode_attention_workspace_size(
+        batch, query_heads, head_dim, mask_len, kv_heads, dtype, 0)
+    buffer, counters, count = _workspace(lib, query.device, nbytes, batch, kv_heads, workspace)
+    status = lib.slc_hip_paged_rope_decode_attention(
+        query.data_ptr(), key.data_ptr(), value.data_ptr(), cosine.data_ptr(), sine.data_ptr(),
+        key_pool.data_ptr(), value_pool.data_ptr(), block_table.data_ptr(), block_table.stride(0),
+        pages_per_seq, page_tokens, key_pool.stride(0), lengths.data_ptr(), lengths_out.data_ptr(),
+        None if overflow is None else overflow.data_ptr(), mask_ptr, mask_dtype, output.data_ptr(),
+        None if buffer is None else buffer.data_ptr(), nbytes, counters.data_ptr(), count, dtype,
+        batch, query_heads, kv_heads, head_dim, mask_len,
+        query.stride(0), query.stride(1), key.stride(0), key.stride(1), value.stride(0),
+        value.stride(1), cosine.stride(0), sine.stride(0), key_pool.stride(1), key_pool.stride(2),
+        mask_sb, mask_ss, output.stride(0), output.stride(1), float(scale), order,
+        _native.current_stream(query.device),
+    )
+    if status == _UNSUPPORTED:
+        return None
+    _native.check(status, "slc_hip_paged_rope_decode_attention")
+    return output

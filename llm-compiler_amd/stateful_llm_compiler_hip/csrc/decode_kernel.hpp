@@ -151,7 +151,7 @@ constexpr float kRescaleThreshold = 8.0f;
 // sum; pass 2 streams V and weighs it with the normalised, rounded
 // probabilities.  K and V are each read once.
 // PG: K/V read through a block table (Paging; key_buffer/value_buffer are
-// the page pools); not combined with ROPE.  PG 1: pages of 32 tokens or more
+// the page pools; with ROPE the new row is written to its position's page).  PG 1: pages of 32 tokens or more
 // (one page per 32-row tile); PG 2: 16-token pages (one per 16-row block).
 template <typename T, int D, int MK, bool L64, bool ROPE, bool EXACT, int PG = 0>
 __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
@@ -164,7 +164,6 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     int64_t kv_sb, int kv_ss, int64_t kv_sh, int64_t m_sb, int m_ss,
     int64_t o_sb, int64_t o_sh, float scale, int chunk_tokens,
     int nchunks, int* __restrict__ counters, RopeStore rs, Paging pg) {
-  static_assert(!(PG && ROPE), "the paged kernel has no RoPE variant");
   using M = Mfma<T>;
   using Layout = SharedLayout<T, D>;
   constexpr int KK = D / 32;            // MFMA k-steps over head_dim
@@ -433,11 +432,17 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
       const int64_t owner =
           in_range ? min(pos / chunk_tokens, static_cast<int64_t>(nchunks) - 1) : 0;
       if (in_range && chunk == owner && wave == 0 && c == 0) {
-        char* krow = reinterpret_cast<char*>(static_cast<T*>(rs.key_out) + b * kv_sb + kvh * kv_sh) +
-                     pos * static_cast<int64_t>(kv_ss) * 2;
-        char* vrow =
-            reinterpret_cast<char*>(static_cast<T*>(rs.value_out) + b * kv_sb + kvh * kv_sh) +
-            pos * static_cast<int64_t>(kv_ss) * 2;
+        // The row's element offset: contiguous, or through the block table.
+        int64_t row;
+        if constexpr (PG) {
+          const int64_t page = pg.table[b * pg.table_sb + (pos >> pg.page_shift)];
+          row = page * pg.page_stride + kvh * kv_sh +
+                (pos & ((int64_t{1} << pg.page_shift) - 1)) * static_cast<int64_t>(kv_ss);
+        } else {
+          row = b * kv_sb + kvh * kv_sh + pos * static_cast<int64_t>(kv_ss);
+        }
+        char* krow = reinterpret_cast<char*>(static_cast<T*>(rs.key_out) + row);
+        char* vrow = reinterpret_cast<char*>(static_cast<T*>(rs.value_out) + row);
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
           *reinterpret_cast<uint4*>(krow + kk * 64 + 16 * g) = knew[kk];

@@ -37,7 +37,7 @@ int launch_paged(const void* query, const void* kp, const void* vp, const void* 
                  void* workspace, int* counters, int64_t batch, int64_t q_heads,
                  int64_t kv_heads, int64_t capacity, int64_t mask_len, const int64_t* st,
                  float scale, int64_t chunk, int64_t nchunks, bool exact, const Paging& pg,
-                 hipStream_t stream) {
+                 hipStream_t stream, const RopeStore* rope = nullptr) {
   float* part_o = nullptr;
   float* part_ml = nullptr;
   if (nchunks > 1) {
@@ -53,13 +53,13 @@ int launch_paged(const void* query, const void* kp, const void* vp, const void* 
                    : nullptr;
   const size_t dyn_lds =
       exact ? static_cast<size_t>(slc_host::ceil_div(std::min(mask_len, capacity), kTile) * 1024) : 0;
-  const RopeStore rs{};
-#define SLC_PAGED_K(MK, L64, EX)                                                            \
+  RopeStore rs{};
+#define SLC_PAGED_K(MK, L64, ROPE, EX)                                                      \
   do {                                                                                      \
-    if (EX && exact_lds_limit<T, D, MK, L64, false, EX, PGM>(static_cast<int>(dyn_lds)) !=  \
+    if (EX && exact_lds_limit<T, D, MK, L64, ROPE, EX, PGM>(static_cast<int>(dyn_lds)) !=   \
                   hipSuccess)                                                               \
       return slc_host::check_launch("slc_hip_paged_decode_attention(exact LDS opt-in)");    \
-    hipLaunchKernelGGL((decode_attention_mfma_kernel<T, D, MK, L64, false, EX, PGM>), grid, \
+    hipLaunchKernelGGL((decode_attention_mfma_kernel<T, D, MK, L64, ROPE, EX, PGM>), grid,  \
                        dim3(kThreads), dyn_lds, stream, static_cast<const T*>(query),       \
                        static_cast<const T*>(kp), static_cast<const T*>(vp), lengths,       \
                        lengths_dtype, mask, mask_dtype, static_cast<T*>(output), part_o,    \
@@ -69,28 +69,37 @@ int launch_paged(const void* query, const void* kp, const void* vp, const void* 
                        st[7], st[8], scale, static_cast<int>(chunk),                        \
                        static_cast<int>(nchunks), merge, rs, pg);                           \
   } while (0)
-#define SLC_PAGED_ORDER(MK, L64)     \
-  if (exact) {                       \
-    SLC_PAGED_K(MK, L64, true);      \
-  } else {                           \
-    SLC_PAGED_K(MK, L64, false);     \
+#define SLC_PAGED_ORDER(MK, L64, ROPE) \
+  if (exact) {                         \
+    SLC_PAGED_K(MK, L64, ROPE, true);  \
+  } else {                             \
+    SLC_PAGED_K(MK, L64, ROPE, false); \
   }
-#define SLC_PAGED_MASK(L64)                  \
-  if (mask == nullptr) {                     \
-    SLC_PAGED_ORDER(0, L64)                  \
-  } else if (mask_dtype == SLC_BF16) {       \
-    SLC_PAGED_ORDER(SLC_BF16 + 1, L64)       \
-  } else if (mask_dtype == SLC_F16) {        \
-    SLC_PAGED_ORDER(SLC_F16 + 1, L64)        \
-  } else {                                   \
-    SLC_PAGED_ORDER(SLC_F32 + 1, L64)        \
+#define SLC_PAGED_MASK(L64, ROPE)              \
+  if (mask == nullptr) {                       \
+    SLC_PAGED_ORDER(0, L64, ROPE)              \
+  } else if (mask_dtype == SLC_BF16) {         \
+    SLC_PAGED_ORDER(SLC_BF16 + 1, L64, ROPE)   \
+  } else if (mask_dtype == SLC_F16) {          \
+    SLC_PAGED_ORDER(SLC_F16 + 1, L64, ROPE)    \
+  } else {                                     \
+    SLC_PAGED_ORDER(SLC_F32 + 1, L64, ROPE)    \
+  }
+  if (rope != nullptr) {
+    // The RoPE variant: int64 lengths; its length advance rides on the
+    // in-kernel merge (or, with one chunk, on the workgroup's end).
+    if (lengths_dtype != SLC_I64 || (nchunks > 1 && merge == nullptr)) return kUnsupported;
+    rs = *rope;
+    rs.counters = counters + batch * kv_heads;
+    SLC_PAGED_MASK(true, true)
+    return slc_host::check_launch("slc_hip_paged_rope_decode_attention");
   }
   slc_host::mark_kernel_begin(stream);
   for (int rep = slc_host::timed_repeats(); rep > 0; --rep) {
     if (lengths_dtype == SLC_I64) {
-      SLC_PAGED_MASK(true)
+      SLC_PAGED_MASK(true, false)
     } else {
-      SLC_PAGED_MASK(false)
+      SLC_PAGED_MASK(false, false)
     }
   }
   slc_host::mark_kernel_end(stream);
@@ -209,7 +218,7 @@ extern "C" int slc_hip_paged_decode_attention(
   (shift >= 5 ? launch_paged<TT, DD, 1> : launch_paged<TT, DD, 2>)(                          \
       query, key_pool, value_pool, lengths, lengths_dtype, mask, mask_dtype, output, workspace, \
       counters, batch, q_heads, kv_heads, capacity, mask_len, st, scale, chunk, nchunks, exact, \
-      pg, s)
+      pg, s, nullptr)
   if (dtype == SLC_BF16) {
     if (head_dim == 64) return SLC_PAGED_CALL(slc::bf16_t, 64);
     return SLC_PAGED_CALL(slc::bf16_t, 128);
@@ -257,4 +266,89 @@ extern "C" int slc_hip_paged_kv_store(
                      key_stride_b / u, key_stride_h / u, key_stride_t / u, value_stride_b / u,
                      value_stride_h / u, value_stride_t / u);
   return slc_host::check_launch("slc_hip_paged_kv_store");
+}
+
+extern "C" int slc_hip_paged_rope_decode_attention(
+    const void* query, const void* key, const void* value, const void* cosine, const void* sine,
+    void* key_pool, void* value_pool, const int* block_table, int64_t table_stride_b,
+    int64_t pages_per_seq, int64_t page_tokens, int64_t page_stride, const int64_t* lengths,
+    int64_t* lengths_out, int* overflow, const void* mask, int mask_dtype, void* output,
+    void* workspace, int64_t workspace_bytes, int* counters, int64_t num_counters, int dtype,
+    int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t mask_len,
+    int64_t q_stride_b, int64_t q_stride_h, int64_t k_stride_b, int64_t k_stride_h,
+    int64_t v_stride_b, int64_t v_stride_h, int64_t cos_stride_b, int64_t sin_stride_b,
+    int64_t kv_stride_s, int64_t kv_stride_h, int64_t mask_stride_b, int64_t mask_stride_s,
+    int64_t out_stride_b, int64_t out_stride_h, float scale, int softmax_order, void* stream) {
+  SLC_REQUIRE(mask == nullptr || slc_host::is_float_dtype(mask_dtype),
+              "slc_hip_paged_rope_decode_attention: bad mask dtype %d", mask_dtype);
+  SLC_REQUIRE(softmax_order == SLC_SOFTMAX_ONLINE || softmax_order == SLC_SOFTMAX_EXACT,
+              "slc_hip_paged_rope_decode_attention: bad softmax order %d", softmax_order);
+  SLC_REQUIRE(batch >= 0 && q_heads > 0 && kv_heads > 0 && head_dim > 0 && pages_per_seq > 0 &&
+                  mask_len >= 0 && q_heads % kv_heads == 0,
+              "slc_hip_paged_rope_decode_attention: bad sizes");
+  SLC_REQUIRE(batch <= 65535 && kv_heads <= 65535,
+              "slc_hip_paged_rope_decode_attention: batch/kv_heads exceed grid limits");
+  const int shift = page_shift_of(page_tokens);
+  SLC_REQUIRE(shift >= 0, "slc_hip_paged_rope_decode_attention: page_tokens must be a power of "
+                          "two >= 16, got %lld", (long long)page_tokens);
+  if (batch == 0) return SLC_OK;
+  SLC_REQUIRE(query && key && value && cosine && sine && key_pool && value_pool && block_table &&
+                  lengths && lengths_out && output,
+              "slc_hip_paged_rope_decode_attention: null pointer");
+  const bool exact = softmax_order == SLC_SOFTMAX_EXACT;
+  const int64_t groups = q_heads / kv_heads;
+  const int64_t capacity = pages_per_seq * page_tokens;
+  // The fused kernel's cases; everything else is the caller's three-kernel
+  // path (RoPE, paged store, paged attention).
+  if (!(dtype == SLC_BF16 || dtype == SLC_F16) || !(head_dim == 64 || head_dim == 128) ||
+      groups > kMaxGroups || mask_len <= 0)
+    return kUnsupported;
+  if (exact && std::min(mask_len, capacity) > exact_max_tokens(head_dim)) return kUnsupported;
+  const uint64_t bits =
+      reinterpret_cast<uintptr_t>(query) | reinterpret_cast<uintptr_t>(key) |
+      reinterpret_cast<uintptr_t>(value) | reinterpret_cast<uintptr_t>(cosine) |
+      reinterpret_cast<uintptr_t>(sine) | reinterpret_cast<uintptr_t>(key_pool) |
+      reinterpret_cast<uintptr_t>(value_pool);
+  const int64_t strides = q_stride_b | q_stride_h | k_stride_b | k_stride_h | v_stride_b |
+                          v_stride_h | cos_stride_b | sin_stride_b | kv_stride_s | kv_stride_h |
+                          page_stride;
+  const int64_t mask_es = mask == nullptr ? 0 : slc_host::dtype_size(mask_dtype);
+  if ((bits & 15) != 0 || (strides & 7) != 0 || kv_stride_s <= 0 || mask_stride_s < 0 ||
+      page_tokens * kv_stride_s * 2 >= (int64_t{1} << 31) ||
+      mask_len * mask_stride_s * mask_es >= (int64_t{1} << 31) || capacity >= (int64_t{1} << 30))
+    return kUnsupported;
+  int64_t chunk, nchunks;
+  if (exact) {
+    chunk = mask_len;
+    nchunks = 1;
+  } else {
+    chunk = choose_chunk(batch, kv_heads, mask_len, 0);
+    nchunks = slc_host::ceil_div(mask_len, chunk);
+  }
+  const int64_t need = partial_bytes(batch, q_heads, head_dim, nchunks);
+  SLC_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need),
+              "slc_hip_paged_rope_decode_attention: workspace of %lld bytes needed, got %lld",
+              (long long)need, (long long)workspace_bytes);
+  SLC_REQUIRE(counters != nullptr && num_counters >= counter_count(batch, kv_heads),
+              "slc_hip_paged_rope_decode_attention: %lld counters needed, got %lld",
+              (long long)counter_count(batch, kv_heads), (long long)num_counters);
+  const int64_t st[9] = {q_stride_b,    q_stride_h,    0,            kv_stride_s, kv_stride_h,
+                         mask_stride_b, mask_stride_s, out_stride_b, out_stride_h};
+  const Paging pg{block_table, table_stride_b, shift, page_stride};
+  RopeStore rope{key,          value,        cosine,      sine,         k_stride_b,
+                 k_stride_h,   v_stride_b,   v_stride_h,  cos_stride_b, sin_stride_b,
+                 key_pool,     value_pool,   lengths_out, overflow,     nullptr};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define SLC_PAGED_ROPE_CALL(TT, DD)                                                              \
+  (shift >= 5 ? launch_paged<TT, DD, 1> : launch_paged<TT, DD, 2>)(                              \
+      query, key_pool, value_pool, lengths, SLC_I64, mask, mask_dtype, output, workspace,        \
+      counters, batch, q_heads, kv_heads, capacity, mask_len, st, scale, chunk, nchunks, exact, \
+      pg, s, &rope)
+  if (dtype == SLC_BF16) {
+    if (head_dim == 64) return SLC_PAGED_ROPE_CALL(slc::bf16_t, 64);
+    return SLC_PAGED_ROPE_CALL(slc::bf16_t, 128);
+  }
+  if (head_dim == 64) return SLC_PAGED_ROPE_CALL(slc::f16_t, 64);
+  return SLC_PAGED_ROPE_CALL(slc::f16_t, 128);
+#undef SLC_PAGED_ROPE_CALL
 }

@@ -38,6 +38,7 @@ from .backends import (
     hip_norm_linear_swiglu,
     hip_paged_decode_attention,
     hip_paged_kv_store,
+    hip_paged_rope_decode_attention,
     hip_prefill_attention,
     hip_rms_norm,
     hip_rope,
@@ -415,8 +416,9 @@ class PagedKVCacheState(PreallocatedKVCacheState):
     shared by every layer) names the pool page of each sequence's tokens
     [j * page_tokens, (j + 1) * page_tokens).  Lengths, versions, the overflow
     flag and the workspace behave as in the contiguous state, and every op
-    gives the contiguous state's result bit for bit.  RoPE + store runs as two
-    kernels here (the fused kernels address contiguous rows).
+    gives the contiguous state's result bit for bit.  The model's decode step
+    (RoPE, store, advance, attention) runs as one paged kernel like the
+    contiguous one; RoPE + store alone runs as two kernels.
     """
 
     block_table: torch.Tensor | None = None
@@ -579,10 +581,30 @@ class PagedKVCacheState(PreallocatedKVCacheState):
 
     def rope_store_attention(self, slot, query, key, value, cosine, sine, attention_mask, *,
                              groups, scale, softmax_order="online"):
-        self._check_attention(slot, query, attention_mask, groups)
-        q_rot, state = self.rope_store_advance(slot, query, key, value, cosine, sine, delta=1)
-        return state.decode_attention(slot, q_rot, attention_mask, groups=groups, scale=scale,
-                                      softmax_order=softmax_order), state
+        """One kernel where it takes the case (RoPE, the paged store of the new
+        row, the length advance and the paged attention), else the three ops;
+        the same result either way."""
+
+        positions = self._check_attention(slot, query, attention_mask, groups)
+        self._validate_store(slot, key, value, positions)
+        out = positions if self.in_place_lengths else torch.empty_like(positions)
+        result = None
+        if key.shape[2] == 1:
+            result = hip_paged_rope_decode_attention(
+                query, key, value, cosine, sine, self.keys[slot], self.values[slot],
+                self.block_table, positions, out, attention_mask, scale=scale,
+                overflow=self.overflow,
+                softmax_order=attention_order(softmax_order, attention_mask.shape[-1], query),
+                workspace=self.workspace)
+        if result is None:
+            q_rot, state = self.rope_store_advance(slot, query, key, value, cosine, sine, delta=1)
+            return state.decode_attention(slot, q_rot, attention_mask, groups=groups, scale=scale,
+                                          softmax_order=softmax_order), state
+        lengths = list(self.lengths)
+        lengths[slot] = out
+        zero = None if self.zero_slots is None else self.zero_slots - {slot}
+        return result, replace(self, lengths=tuple(lengths), generation=self.generation + 1,
+                               zero_slots=zero)
 
 
 def _device_workspace(device: torch.device) -> _native.DeviceWorkspace | None:

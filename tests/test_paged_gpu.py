@@ -212,3 +212,55 @@ def test_paged_operand_checks(gpu):
     out = hip_paged_decode_attention(q, pool, pool, table, lengths + 3, None, scale=0.125)
     torch.cuda.synchronize()
     assert np.count_nonzero(out.float().cpu().numpy()) == 0
+
+
+@pytest.mark.parametrize("order", ["online", "exact"])
+@pytest.mark.parametrize("page_tokens", [16, 64])
+def test_paged_rope_decode_attention_equals_contiguous_and_unfused(gpu, order, page_tokens):
+    # One decode token: RoPE, store at lengths[b], advance, attention -- the
+    # fused paged kernel against (a) the fused contiguous kernel on the
+    # gathered buffers and (b) RoPE, paged store and paged attention in turn.
+    from stateful_llm_compiler_hip.backends import (
+        hip_paged_decode_attention, hip_paged_kv_store, hip_paged_rope_decode_attention,
+        hip_rope, hip_rope_decode_attention)
+
+    announce(f"paged rope decode attention order={order} page_tokens={page_tokens}")
+    g = generator(570 + page_tokens)
+    batch, qh, kvh, d, cap = 4, 14, 2, 64, 512
+    pages = cap // page_tokens
+    table, num_pages = _paging(g, batch, pages)
+    key_buffer = torch.randn(batch, cap, kvh, d, generator=g).to(torch.bfloat16)
+    value_buffer = torch.randn(batch, cap, kvh, d, generator=g).to(torch.bfloat16)
+    kp = _scatter(key_buffer, table, num_pages, page_tokens).to(gpu)
+    vp = _scatter(value_buffer, table, num_pages, page_tokens).to(gpu)
+    kb, vb = key_buffer.to(gpu), value_buffer.to(gpu)
+    table = table.to(gpu)
+    lengths = torch.tensor([0, 17, 300, 511], dtype=torch.int64, device=gpu)
+    q = torch.randn(batch, qh, 1, d, generator=g).to(torch.bfloat16).to(gpu)
+    k = torch.randn(batch, kvh, 1, d, generator=g).to(torch.bfloat16).to(gpu)
+    v = torch.randn(batch, kvh, 1, d, generator=g).to(torch.bfloat16).to(gpu)
+    cos = torch.randn(batch, 1, d, generator=g).to(torch.bfloat16).to(gpu)
+    sin = torch.randn(batch, 1, d, generator=g).to(torch.bfloat16).to(gpu)
+    mask = torch.zeros(batch, 1, 1, cap, dtype=torch.bfloat16, device=gpu)
+
+    kp2, vp2 = kp.clone(), vp.clone()
+    out_paged = lengths.clone()
+    fused = hip_paged_rope_decode_attention(q, k, v, cos, sin, kp, vp, table, lengths, out_paged,
+                                            mask, scale=d**-0.5, softmax_order=order)
+    assert fused is not None
+    out_contig = lengths.clone()
+    contiguous = hip_rope_decode_attention(q, k, v, cos, sin, kb, vb, lengths, out_contig, mask,
+                                           scale=d**-0.5, softmax_order=order)
+    assert contiguous is not None
+    q_rot, k_rot = hip_rope(q, k, cos, sin)
+    hip_paged_kv_store(kp2, vp2, table, k_rot, v, lengths)
+    unfused = hip_paged_decode_attention(q_rot, kp2, vp2, table, lengths + 1, mask, scale=d**-0.5,
+                                         softmax_order=order)
+    torch.cuda.synchronize()
+    assert torch.equal(out_paged, lengths + 1) and torch.equal(out_contig, lengths + 1)
+    assert_bitwise_equal(fused, contiguous)
+    assert_bitwise_equal(fused, unfused)
+    gathered_k = kp.view(torch.int16)[table.long()].reshape(batch, cap, kvh, d)
+    assert_bitwise_equal(gathered_k, kb.view(torch.int16))
+    assert_bitwise_equal(kp.view(torch.int16), kp2.view(torch.int16))
+    assert_bitwise_equal(vp.view(torch.int16), vp2.view(torch.int16))
