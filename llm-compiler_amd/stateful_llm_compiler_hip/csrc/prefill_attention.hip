@@ -667,16 +667,28 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
           float v = slc::round_to<T>(st[kb][qb][r]);
           if constexpr (!POW2) v = slc::round_to<T>(v * scale);
           if constexpr (MK != 0) v = fmaf(v, c_log2, mv[r] * kLog2e);
-          if (!full) {
-            const int kidx = k0 + 16 * kb + 4 * g + r;
-            bool valid = kidx < tokens;
-            if constexpr (CAUSAL) valid = valid && kidx <= my_query;
-            v = valid ? v : -INFINITY;
-          }
           st[kb][qb][r] = v;
-          mx = fmaxf(mx, v);
         }
       }
+      if (!full) {
+        // Only the diagonal and the last tile get here (`full` is uniform).
+        // The empty asm keeps this block a branch: if-converted, its compares
+        // and selects would run on every tile.  Key 16kb + 4g + r of the tile
+        // is valid iff it is at most `last` (the last key this query sees,
+        // relative to the lane's first key).
+        asm volatile("" ::: "memory");
+        int last = tokens - 1 - k0 - 4 * g;
+        if constexpr (CAUSAL) last = min(last, my_query - k0 - 4 * g);
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            st[kb][qb][r] = 16 * kb + r <= last ? st[kb][qb][r] : -INFINITY;
+      }
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[kb][qb][r]);
       if (pass2) continue;
       mx = slc::max_xor32(slc::max_xor16(mx));
       if constexpr (MK == 0) mx *= c_log2;
