@@ -395,6 +395,13 @@ template <int MK>
 constexpr int stage_bytes() { return 2 * kV2TileBytes + kV2Queries * kKeys * mask_elem_bytes<MK>(); }
 
 typedef short v4s_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// bf16(a) in the low half, bf16(b) in the high half: one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t round_pair_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
 typedef uint32_t v2u_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, unsigned char* lds,
@@ -656,6 +663,16 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
             }
           }
         }
+        if constexpr (std::is_same_v<T, slc::bf16_t>) {
+          // Two scores per v_cvt_pk_bf16_f32 (round to nearest even, as
+          // round_to), back to fp32 by a shift and a mask.
+#pragma unroll
+          for (int r = 0; r < 4; r += 2) {
+            const uint32_t pk = round_pair_bf16(st[kb][qb][r], st[kb][qb][r + 1]);
+            st[kb][qb][r] = __uint_as_float(pk << 16);
+            st[kb][qb][r + 1] = __uint_as_float(pk & 0xffff0000u);
+          }
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           // r = the executor's rounded score: bf16(bf16(q.k) * scale), or
@@ -664,7 +681,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
           // the row max is taken over r (times the positive factor c it is
           // the max of the log2-domain scores); with one the scores become
           // c * r + mask * log2(e).
-          float v = slc::round_to<T>(st[kb][qb][r]);
+          float v = std::is_same_v<T, slc::bf16_t> ? st[kb][qb][r] : slc::round_to<T>(st[kb][qb][r]);
           if constexpr (!POW2) v = slc::round_to<T>(v * scale);
           if constexpr (MK != 0) v = fmaf(v, c_log2, mv[r] * kLog2e);
           st[kb][qb][r] = v;
@@ -690,9 +707,13 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[kb][qb][r]);
       if (pass2) continue;
-      mx = slc::max_xor32(slc::max_xor16(mx));
+      // The row max spans the 4 lane groups, but it only matters when it
+      // moves the running max, i.e. when some lane's own max is past the
+      // threshold (times c > 0 commutes with max): the cross-group
+      // reduction runs only then.
       if constexpr (MK == 0) mx *= c_log2;
       if (__any(mx > m_run[qb] + kRescaleThreshold)) {
+        mx = slc::max_xor32(slc::max_xor16(mx));
         const float m_new = fmaxf(m_run[qb], mx);
         const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - (m_new == -INFINITY ? 0.0f : m_new));
         if constexpr (EXACT) {
