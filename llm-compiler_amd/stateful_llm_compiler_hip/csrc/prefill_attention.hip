@@ -111,10 +111,12 @@ __global__ __launch_bounds__(256) void prefill_attention_mfma_kernel(
   using M = Mfma<T>;
   __shared__ __attribute__((aligned(16))) unsigned char smem[2][2][kTileBytes];
 
-  const int nqb = gridDim.x;
-  const int qb = CAUSAL ? nqb - 1 - static_cast<int>(blockIdx.x) : blockIdx.x;
-  const int h = blockIdx.y;
-  const int64_t b = blockIdx.z;
+  // Grid (heads, batch, query blocks): workgroups dispatch in that order,
+  // so with the causal flag every row's heaviest query block goes first.
+  const int nqb = gridDim.z;
+  const int qb = CAUSAL ? nqb - 1 - static_cast<int>(blockIdx.z) : blockIdx.z;
+  const int h = blockIdx.x;
+  const int64_t b = blockIdx.y;
   const int kvh = h / groups;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -442,10 +444,15 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
   constexpr int kMaskTile = kV2Queries * kMaskRow;
   __shared__ __attribute__((aligned(16))) unsigned char ring[kV2Stages][stage_bytes<MK>()];
 
-  const int nqb = gridDim.x;
-  const int qblk = CAUSAL ? nqb - 1 - static_cast<int>(blockIdx.x) : blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int64_t b = blockIdx.z;
+  // Grid (KV heads, batch, query blocks): workgroups dispatch in that
+  // order, and the last query blocks go first.  Under the causal flag (or a
+  // causal-shaped mask, whose skipped tiles make the work alike) those are
+  // the heaviest, so the light ones fill the tail: longest-first list
+  // scheduling.  Any other shape is indifferent to the order.
+  const int nqb = gridDim.z;
+  const int qblk = nqb - 1 - static_cast<int>(blockIdx.z);
+  const int kvh = blockIdx.x;
+  const int64_t b = blockIdx.y;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -800,7 +807,7 @@ template <typename T, int G, int MK, bool CAUSAL>
 int launch_v2(const void* q, const void* k, const void* v, const void* mask, void* out,
               int64_t batch, int tokens, int kv_heads, const int64_t* st, float scale,
               bool exact, hipStream_t stream) {
-  const dim3 grid((tokens + kV2Queries - 1) / kV2Queries, kv_heads, static_cast<unsigned>(batch));
+  const dim3 grid(kv_heads, static_cast<unsigned>(batch), (tokens + kV2Queries - 1) / kV2Queries);
   int exponent = 0;
   const bool pow2 = std::is_same_v<T, slc::bf16_t> && std::frexp(scale, &exponent) == 0.5f &&
                     exponent > -100;
@@ -847,7 +854,7 @@ template <typename T, int MK, bool CAUSAL>
 int launch_mfma(const void* q, const void* k, const void* v, const void* mask, void* out,
                 int64_t batch, int tokens, int q_heads, int groups, const int64_t* st,
                 float scale, hipStream_t stream) {
-  const dim3 grid((tokens + kQueries - 1) / kQueries, q_heads, static_cast<unsigned>(batch));
+  const dim3 grid(q_heads, static_cast<unsigned>(batch), (tokens + kQueries - 1) / kQueries);
   hipLaunchKernelGGL((prefill_attention_mfma_kernel<T, MK, CAUSAL>), grid, dim3(256), 0, stream,
                      static_cast<const T*>(q), static_cast<const T*>(k),
                      static_cast<const T*>(v), mask, static_cast<T*>(out), tokens, q_heads,
@@ -934,7 +941,9 @@ extern "C" int slc_hip_prefill_attention(
   // The MFMA kernel addresses one (batch, kv-head) K/V slice with 32-bit offsets.
   const bool mfma_ok = (dtype == SLC_BF16 || dtype == SLC_F16) && head_dim == kD &&
                        (bits & 15) == 0 && (strides & 7) == 0 && k_st >= kD && v_st >= kD &&
-                       tokens * (k_st > v_st ? k_st : v_st) * 2 < (1LL << 31);
+                       tokens * (k_st > v_st ? k_st : v_st) * 2 < (1LL << 31) &&
+                       (tokens + kV2Queries - 1) / kV2Queries <= 65535 &&
+                       (tokens + kQueries - 1) / kQueries <= 65535;  // grid z: query blocks
   // The grouped kernel: GQA groups of 1, 2, 4, 7 or 8 heads, and a mask (if
   // any) with unit key stride and 16-byte aligned rows.
   const bool group_ok = groups == 1 || groups == 2 || groups == 4 || groups == 7 || groups == 8;
