@@ -459,8 +459,10 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
   const int g = lane >> 4;
   const int c = lane & 15;
   const int q0 = qblk * kV2Queries;
-  // Factor from the rounded score to log2 units.
-  const float c_log2 = POW2 ? scale * kLog2e : kLog2e;
+  // Factor from the stored score to log2 units: without a mask and with a
+  // power-of-two scale the stored score is bf16(q.k), unscaled; otherwise it
+  // is the reference's fp32 score itself (scaled, mask added).
+  const float c_log2 = POW2 && MK == 0 ? scale * kLog2e : kLog2e;
   const int key_end = CAUSAL ? min(q0 + kV2Queries, tokens) : tokens;
   const int ntiles = (key_end + kKeys - 1) / kKeys;
   const int nsteps = EXACT ? 2 * ntiles : ntiles;  // ring steps (tile visits)
@@ -661,10 +663,11 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
             const uint32_t w2[2] = {raw.x, raw.y};
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const uint16_t bits = static_cast<uint16_t>(w2[r >> 1] >> (16 * (r & 1)));
               if constexpr (MK == SLC_BF16 + 1) {
-                mv[r] = slc::to_f32(slc::bf16_t{bits});
+                // bf16 to fp32: the element moved into the high half.
+                mv[r] = __uint_as_float((r & 1) ? (w2[r >> 1] & 0xffff0000u) : (w2[r >> 1] << 16));
               } else {
+                const uint16_t bits = static_cast<uint16_t>(w2[r >> 1] >> (16 * (r & 1)));
                 mv[r] = slc::to_f32(slc::f16_t{bits});
               }
             }
@@ -682,15 +685,17 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          // r = the executor's rounded score: bf16(bf16(q.k) * scale), or
+          // v = the executor's rounded score: bf16(bf16(q.k) * scale), or
           // bf16(q.k) when the scale is a power of two (POW2; the product is
-          // then exact and scaled inside the exp2 argument).  Without a mask
-          // the row max is taken over r (times the positive factor c it is
-          // the max of the log2-domain scores); with one the scores become
-          // c * r + mask * log2(e).
+          // then exact, so without a mask it moves into the exp2 argument).
+          // With a mask the stored score is the executor's fp32 score
+          // v * scale + mask: one FMA, exact in the product (POW2), so the
+          // sum is rounded once as the executor's fp32 add rounds it.  The
+          // row max is taken over the stored scores (times the positive
+          // factor c_log2 it is the max of the log2-domain scores).
           float v = std::is_same_v<T, slc::bf16_t> ? st[kb][qb][r] : slc::round_to<T>(st[kb][qb][r]);
           if constexpr (!POW2) v = slc::round_to<T>(v * scale);
-          if constexpr (MK != 0) v = fmaf(v, c_log2, mv[r] * kLog2e);
+          if constexpr (MK != 0) v = POW2 ? fmaf(v, scale, mv[r]) : v + mv[r];
           st[kb][qb][r] = v;
         }
       }
@@ -718,7 +723,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
       // moves the running max, i.e. when some lane's own max is past the
       // threshold (times c > 0 commutes with max): the cross-group
       // reduction runs only then.
-      if constexpr (MK == 0) mx *= c_log2;
+      mx *= c_log2;
       if (__any(mx > m_run[qb] + kRescaleThreshold)) {
         mx = slc::max_xor32(slc::max_xor16(mx));
         const float m_new = fmaxf(m_run[qb], mx);
@@ -741,7 +746,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float x = st[kb][qb][r];
-            sum += __builtin_amdgcn_exp2f(MK == 0 ? fmaf(x, c_log2, -m_use) : x - m_use);
+            sum += __builtin_amdgcn_exp2f(fmaf(x, c_log2, -m_use));
           }
         l_part[qb] += sum;
       }
@@ -761,7 +766,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const float x = st[2 * half + (i >> 2)][qb][i & 3];
-          const float p = __builtin_amdgcn_exp2f(MK == 0 ? fmaf(x, c_log2, -m_use) : x - m_use);
+          const float p = __builtin_amdgcn_exp2f(fmaf(x, c_log2, -m_use));
           bits.v[i] = bits_of<T>(p);
         }
         pv[qb] = __builtin_bit_cast(typename M::vec, bits);
