@@ -122,7 +122,16 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
   constexpr int XB = BM * kBK * 2;  // bytes per X tile
   constexpr int WB = BN * kBK * 2;
 
-  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * (XB + WB)];
+  // One LDS tile pair (the next k-tile waits in registers while this one is
+  // read), or the epilogue's staging if larger: 36 KB at 128 x 128, so three
+  // workgroups share a CU (two with a double-buffered 64 KB ring: the third
+  // workgroup hides more load latency than the second barrier per k-tile
+  // costs, 362 -> 333 us at M32768 N4864 K896).
+  constexpr int kStage = XB + WB;
+  constexpr int kEpi = (BM * (BN + 8) * 2 > WM * WN * TM * (TN + 8) * 2) ? BM * (BN + 8) * 2
+                                                                        : WM * WN * TM * (TN + 8) * 2;
+  constexpr int kSmem = kStage > kEpi ? kStage : kEpi;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[kSmem];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -225,8 +234,8 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
       wr[i] = ok ? buffer_load16(rw, (row * K + k0 + col) * 2) : make_uint4(0, 0, 0, 0);
     }
   };
-  auto stash = [&](int buf) {
-    unsigned char* xs = smem + buf * (XB + WB);
+  auto stash = [&]() {
+    unsigned char* xs = smem;
     unsigned char* ws = xs + XB;
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
@@ -250,12 +259,11 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
 
   const int ktiles = (K + kBK - 1) / kBK;
   fetch(0);
-  stash(0);
+  stash();
   __syncthreads();
   for (int kt = 0; kt < ktiles; ++kt) {
-    const int buf = kt & 1;
     if (kt + 1 < ktiles) fetch((kt + 1) * kBK);
-    const unsigned char* xs = smem + buf * (XB + WB);
+    const unsigned char* xs = smem;
     const unsigned char* ws = xs + XB;
 #pragma unroll
     for (int kk = 0; kk < kBK / 32; ++kk) {
@@ -275,7 +283,8 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = MF::run(a[i], b[j], acc[i][j]);
     }
-    if (kt + 1 < ktiles) stash(buf ^ 1);
+    __syncthreads();  // every wave's reads of the tile are done
+    if (kt + 1 < ktiles) stash();
     __syncthreads();
   }
 
@@ -284,7 +293,7 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
     // barrier), then SwiGLU of each feature's gate (column j) and up (column
     // BN / 2 + j) values, 8 features per 16-byte store.
     constexpr int kRow = BN + 8;
-    static_assert(BM * kRow * 2 <= 2 * (XB + WB), "staging fits the LDS");
+    static_assert(BM * kRow * 2 <= kSmem, "staging fits the LDS");
     uint16_t* cs = reinterpret_cast<uint16_t*>(smem);
 #pragma unroll
     for (int j = 0; j < FN; ++j)
@@ -327,7 +336,7 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
     // The loop ended on a barrier, so the LDS is free: wave-private staging
     // of its TM x TN tile as T, rows padded to keep 16-byte alignment.
     constexpr int kCPad = TN + 8;
-    static_assert(TM * kCPad * 2 * WM * WN <= 2 * (XB + WB), "staging fits the LDS");
+    static_assert(TM * kCPad * 2 * WM * WN <= kSmem, "staging fits the LDS");
     uint16_t* cs = reinterpret_cast<uint16_t*>(smem) + wave * TM * kCPad;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
