@@ -580,7 +580,9 @@ int dispatch_mfma(const void* x, const void* w, const void* bias, void* y, int M
   if (M <= 16) return launch_skinny<T, 1>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
   if (M <= 32) return launch_skinny<T, 2>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
   if (M <= 64) return launch_skinny<T, 4>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
-  return launch_mfma<T, 128, 128, 2, 2>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
+  // Eight waves of 64 x 32 (78 registers, six waves per SIMD): 4-9 % faster
+  // than four of 64 x 64 at M 4096, equal at 32768.
+  return launch_mfma<T, 128, 128, 2, 4>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
 }
 
 template <typename T>
@@ -615,9 +617,9 @@ int gemm_residual(const void* x, int64_t x_rs, int64_t rows, int64_t K, int64_t 
   if (!ok) return SLC_ERR_UNSUPPORTED;
   const int M = static_cast<int>(rows), n = static_cast<int>(N), k = static_cast<int>(K);
   const int rc = dtype == SLC_BF16
-                     ? launch_mfma<slc::bf16_t, 128, 128, 2, 2>(x, w, bias, y, M, n, k, x_rs, y_rs,
+                     ? launch_mfma<slc::bf16_t, 128, 128, 2, 4>(x, w, bias, y, M, n, k, x_rs, y_rs,
                                                                 stream, residual, r_rs)
-                     : launch_mfma<slc::f16_t, 128, 128, 2, 2>(x, w, bias, y, M, n, k, x_rs, y_rs,
+                     : launch_mfma<slc::f16_t, 128, 128, 2, 4>(x, w, bias, y, M, n, k, x_rs, y_rs,
                                                                stream, residual, r_rs);
   return rc == kNoResidualPath ? SLC_ERR_UNSUPPORTED : rc;
 }
