@@ -641,8 +641,8 @@ int gemm_swiglu(const void* x, int64_t x_rs, int64_t rows, int64_t K, int64_t N,
   const int M = static_cast<int>(rows), n = static_cast<int>(N), k = static_cast<int>(K);
   const dim3 grid((n + 63) / 64, (M + 127) / 128);
 #define SLC_DUAL(TT)                                                                         \
-  hipLaunchKernelGGL((linear_mfma_kernel<TT, 128, 128, 2, 2, true, true, true>), grid,       \
-                     dim3(256), 0, stream, static_cast<const TT*>(x),                         \
+  hipLaunchKernelGGL((linear_mfma_kernel<TT, 128, 128, 2, 4, true, true, true>), grid,       \
+                     dim3(512), 0, stream, static_cast<const TT*>(x),                         \
                      static_cast<const TT*>(w_gate), static_cast<const TT*>(nullptr),         \
                      static_cast<TT*>(y), M, n, k, x_rs, y_rs, static_cast<const TT*>(nullptr), \
                      int64_t{0}, static_cast<const TT*>(w_up))
@@ -686,8 +686,8 @@ int gemm_group(const void* x, int64_t x_rs, int64_t rows, int64_t K, int count,
   const int M = static_cast<int>(rows), k = static_cast<int>(K);
   const dim3 grid(static_cast<unsigned>(tiles), (M + 127) / 128);
 #define SLC_GROUP(TT)                                                                          \
-  hipLaunchKernelGGL((linear_mfma_kernel<TT, 128, 128, 2, 2, true, true, false, true>), grid, \
-                     dim3(256), 0, stream, static_cast<const TT*>(x),                           \
+  hipLaunchKernelGGL((linear_mfma_kernel<TT, 128, 128, 2, 4, true, true, false, true>), grid, \
+                     dim3(512), 0, stream, static_cast<const TT*>(x),                           \
                      static_cast<const TT*>(nullptr), static_cast<const TT*>(nullptr),          \
                      static_cast<TT*>(nullptr), M, 0, k, x_rs, int64_t{0},                      \
                      static_cast<const TT*>(nullptr), int64_t{0}, static_cast<const TT*>(nullptr), g)
