@@ -239,13 +239,18 @@ def test_prefill_bidirectional_zero_mask_bf16(gpu):
 
 @pytest.mark.parametrize("q_heads,kv_heads", [(14, 2), (8, 1), (4, 4), (8, 4), (16, 4)])
 @pytest.mark.parametrize("tokens", [7, 64, 100, 257])
-@pytest.mark.parametrize("variant", ["causal-flag", "bf16-causal-mask", "f32-random-mask-causal", "f16-zeros"])
+@pytest.mark.parametrize(
+    "variant", ["causal-flag", "bf16-causal-mask", "f32-random-mask-causal", "f16-zeros", "bidirectional"]
+)
 def test_prefill_grouped_kernel(gpu, q_heads, kv_heads, tokens, variant):
     # GQA groups of 7, 8, 1, 2 and 4 heads take the grouped-head kernel, with
     # no mask, a 2-byte mask, or an fp32 mask (all with unit key stride).
+    # "bidirectional" (no mask, no causal flag) bounds the last tile by the
+    # token count alone.
     announce(f"prefill grouped QH{q_heads} KVH{kv_heads} T={tokens} {variant}")
     kind, causal, mdt = {
         "causal-flag": ("none", True, torch.float32),
+        "bidirectional": ("none", False, torch.float32),
         "bf16-causal-mask": ("causal", False, torch.bfloat16),
         "f32-random-mask-causal": ("random", True, torch.float32),
         "f16-zeros": ("zeros", False, torch.float16),
