@@ -27,6 +27,8 @@
  *                              semantics of execution.py:741-767)
  *   slc_hip_linear             backends/triton_linear.py:87-148 (triton_linear)
  *                              and triton_executor.py:159-176 (kernel.cublas.linear)
+ *   slc_hip_linear_tile        the same, tile chosen by a profile plan
+ *                              (cost_model.py:125-245, lowering_selection.py:12-72)
  *   slc_hip_prefill_attention  backends/triton_prefill_attention.py:152-232
  *                              (semantics of execution.py:707-739)
  */
@@ -93,6 +95,9 @@ SLC_API int slc_hip_version(void);
 SLC_API const char* slc_hip_last_error(void);
 
 /*
+ * BENCH-ONLY.  Not for serving code: while armed, the calling thread's
+ * entry points change what they launch (see slc_hip_set_timing_repeats).
+ *
  * Measurement hook (no counterpart in the reference, which times whole calls
  * with torch events): arm two hipEvent_t handles for the calling thread; each
  * later entry point with a multi-kernel launch sequence records `begin` just
@@ -102,6 +107,9 @@ SLC_API const char* slc_hip_last_error(void);
 SLC_API void slc_hip_set_timing_events(void* begin, void* end);
 
 /*
+ * BENCH-ONLY.  Not for serving code: a repeat count above 1 makes every
+ * armed call launch its dominant kernel that many times.
+ *
  * Measurement hook (no counterpart in the reference): while timing events are
  * armed, launch the dominant kernel `repeats` times back to back between them
  * (it rewrites the same outputs each time), so the per-launch average excludes
@@ -327,6 +335,28 @@ SLC_API int slc_hip_linear(const void* input, const void* weight,
                            int64_t rows, int64_t out_features,
                            int64_t in_features, int64_t in_stride_row,
                            int64_t out_stride_row, void* stream);
+
+/*
+ * linear_tile: slc_hip_linear with the workgroup tile of the prefill-sized
+ * (rows > 64, bf16/fp16) MFMA path chosen by the caller: the variant a
+ * profile plan selects, as the reference's planner selects an RMSNorm backend
+ * from measured latencies (cost_model.py:125-245,
+ * passes/lowering_selection.py:12-72).  Every tile gives bit-identical
+ * results (each output's k range accumulates in the same order); only the
+ * launch shape differs.  SLC_TILE_AUTO is slc_hip_linear's choice (128 x 128);
+ * decode-sized rows and the fp32 path ignore the tile.
+ */
+#define SLC_TILE_AUTO 0
+#define SLC_TILE_128X128 1
+#define SLC_TILE_128X64 2
+#define SLC_TILE_64X128 3
+#define SLC_TILE_64X64 4
+#define SLC_TILE_32X64 5
+SLC_API int slc_hip_linear_tile(const void* input, const void* weight,
+                                const void* bias, void* output, int dtype,
+                                int64_t rows, int64_t out_features,
+                                int64_t in_features, int64_t in_stride_row,
+                                int64_t out_stride_row, int tile, void* stream);
 
 /*
  * prefill_attention: multi-token GQA attention.

@@ -30,6 +30,8 @@ SLC_I64 = 4
 
 # slc_softmax_order
 SOFTMAX_ORDERS = {"online": 0, "exact": 1}
+# Workgroup tiles of the prefill-sized linear (SLC_TILE_* in slc_hip.h).
+LINEAR_TILES = {"auto": 0, "t128x128": 1, "t128x64": 2, "t64x128": 3, "t64x64": 4, "t32x64": 5}
 
 # slc_split: decode attention's length-balanced split-sequence variant
 SPLIT_BALANCED = -1
@@ -113,6 +115,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "slc_hip_linear": (
         _I,
         [_P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _P],
+    ),
+    "slc_hip_linear_tile": (
+        _I,
+        [_P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _I, _P],
     ),
     "slc_hip_prefill_attention": (
         _I,

@@ -17,8 +17,14 @@ def hip_linear(
     tensor: torch.Tensor,
     weight: torch.Tensor,
     bias: torch.Tensor | None = None,
+    *,
+    tile: str = "auto",
 ) -> torch.Tensor:
-    """2-D or 3-D ``tensor`` [..., K] times ``weight`` [N, K]^T (+ ``bias`` [N])."""
+    """2-D or 3-D ``tensor`` [..., K] times ``weight`` [N, K]^T (+ ``bias`` [N]).
+
+    ``tile`` picks the workgroup tile of the prefill-sized MFMA path (a
+    profile plan's choice, ``cost_model``); every tile gives the same bits.
+    """
 
     if not tensor.is_cuda or not weight.is_cuda or (bias is not None and not bias.is_cuda):
         raise ValueError("HIP linear: tensors must be on the GPU")
@@ -41,13 +47,15 @@ def hip_linear(
             or not bias.is_contiguous()
         ):
             raise ValueError("HIP linear: bias shape, dtype or device mismatch")
+    if tile not in _native.LINEAR_TILES:
+        raise ValueError(f"HIP linear: unknown tile {tile!r}")
     rows = tensor.numel() // input_features
     output = torch.empty(
         (*tensor.shape[:-1], output_features), device=tensor.device, dtype=tensor.dtype
     )
     if rows == 0:
         return output
-    status = _native.library().slc_hip_linear(
+    status = _native.library().slc_hip_linear_tile(
         tensor.data_ptr(),
         weight.data_ptr(),
         None if bias is None else bias.data_ptr(),
@@ -58,7 +66,8 @@ def hip_linear(
         input_features,
         input_features,
         output_features,
+        _native.LINEAR_TILES[tile],
         _native.current_stream(tensor.device),
     )
-    _native.check(status, "slc_hip_linear")
+    _native.check(status, "slc_hip_linear_tile")
     return output

@@ -3,7 +3,7 @@
 Mirrors the reference's ``compile_exported_program`` / ``CompileOptions``
 (src/stateful_llm_compiler/compiler.py:25-79) for graphs that already are
 ServeIR: optional profile-guided plans of kernel variants (RMSNorm launch
-width, decode-attention split), the KernelIR lowering in the chosen numerical
+width, decode-attention split, GEMM tile), the KernelIR lowering in the chosen numerical
 mode, and ``require_full_lowering`` when strict.
 """
 
@@ -17,7 +17,8 @@ from .cost_model import KernelProfile
 from .ir import Module
 from .lowering import LoweringCoverage, LowerToKernelIRPass, analyze_lowering_coverage, require_full_lowering
 from .pass_manager import PassManager, PassResult, operation_counts
-from .passes import FuseDecodeKernelsPass, SelectDecodeSplitPass, SelectRMSNormLoweringPass
+from .passes import (FuseDecodeKernelsPass, SelectDecodeSplitPass, SelectLinearTilePass,
+                     SelectRMSNormLoweringPass)
 
 
 @dataclass(frozen=True)
@@ -25,7 +26,8 @@ class CompileOptions:
     numerical_mode: str = "fast"
     require_full_lowering: bool = True
     # Schema-v1 profile (the reference's option name): its RMSNorm rows plan
-    # serve.rms_norm, its decode_attention rows (an extension) the split.
+    # serve.rms_norm, its decode_attention and linear rows (extensions) the
+    # attention split and the GEMM tile.
     rmsnorm_profile: str | Path | None = None
     # Fuse decode-step op chains into single kernels (fast mode only; the
     # fused kernels are bit-identical to the chains they replace).
@@ -62,6 +64,7 @@ def compile_module(module: Module, options: CompileOptions | None = None) -> Com
         profile = KernelProfile.load(options.rmsnorm_profile)
         manager.add(SelectRMSNormLoweringPass(profile))
         manager.add(SelectDecodeSplitPass(profile))
+        manager.add(SelectLinearTilePass(profile))
     manager.add(LowerToKernelIRPass(numerical_mode=options.numerical_mode,
                                     attention_softmax=options.attention_softmax,
                                     linear_backend=options.linear_backend))

@@ -13,11 +13,16 @@ kernel an op launches, so this module plans *variants*:
 * ``decode_attention``: ``fixed`` (a fixed chunk per (batch, kv head), sized
   to fill the GPU), ``balanced`` (the length-balanced split) or ``chunk<N>``
   (a fixed chunk of N tokens); the run-time axis is batch x mask length.
+* ``linear``: the workgroup tile of the prefill-sized MFMA GEMM
+  (``t128x128``, ``t128x64``, ``t64x128``, ``t64x64``, ``t32x64``; all give
+  the same bits); static key (out_features, in_features, dtype), run-time
+  axis the row count M.
 
 A profile keeps the schema-v1 layout -- ``schema_version``, ``target`` and a
 ``results`` list of RMSNorm rows keyed ``rows`` / ``hidden_size`` / ``dtype``,
 so a reference profile loads unchanged -- and adds per-row ``hip_variants``
-(variant -> microseconds) plus a ``decode_attention`` list of the same form.
+(variant -> microseconds) plus ``decode_attention`` and ``linear`` lists of
+the same form.
 A reference row without ``hip_variants`` contributes its ``hip_us`` (if any)
 as the automatic variant and nothing else.
 
@@ -44,6 +49,7 @@ SCHEMA_VERSION = 1
 VARIANTS: dict[str, tuple[str, ...]] = {
     "rms_norm": ("auto", "wave", "block"),
     "decode_attention": ("auto", "fixed", "balanced"),
+    "linear": ("auto", "t128x128", "t128x64", "t64x128", "t64x64", "t32x64"),
 }
 _CHUNK = re.compile(r"chunk(\d+)$")
 
@@ -158,6 +164,14 @@ def choose_variant(plan: Mapping[str, Any] | None, size: int, *,
     return VariantChoice(best[0], "profile", size, best[1])
 
 
+def linear_tile(variant: str) -> str:
+    """linear variant -> the tile name hip_linear takes (SLC_TILE_*)."""
+
+    if variant not in VARIANTS["linear"]:
+        raise ProfileError(f"not a linear tile variant: {variant!r}")
+    return variant
+
+
 def waves_per_row(variant: str) -> int:
     """rms_norm variant -> the waves_per_row argument of slc_hip_rms_norm."""
 
@@ -230,6 +244,15 @@ class KernelProfile:
                 raise ProfileError(f"illegal decode_attention row {row!r}") from error
             curve("decode_attention", static, "batch*mask_len").add(
                 size, row.get("hip_variants") or {}, key=(int(row["batch"]), int(row["mask_len"])))
+        for row in payload.get("linear", []) or []:
+            try:
+                static = (("out_features", int(row["out_features"])),
+                          ("in_features", int(row["in_features"])),
+                          ("dtype", canonical_dtype(row["dtype"])))
+                size = int(row["rows"])
+            except (KeyError, TypeError, ValueError) as error:
+                raise ProfileError(f"illegal linear row {row!r}") from error
+            curve("linear", static, "rows").add(size, row.get("hip_variants") or {})
         return cls(payload.get("target") or {}, [c for c in curves.values() if c.samples],
                    source=source)
 
@@ -240,6 +263,7 @@ class KernelProfile:
         if "dtype" in static:
             static["dtype"] = canonical_dtype(static["dtype"])
         keys = {"rms_norm": ("hidden_size", "dtype"),
-                "decode_attention": ("q_heads", "kv_heads", "head_dim", "dtype")}[op]
+                "decode_attention": ("q_heads", "kv_heads", "head_dim", "dtype"),
+                "linear": ("out_features", "in_features", "dtype")}[op]
         curve = self.curves.get((op, tuple((k, static[k]) for k in keys)))
         return None if curve is None else curve.to_plan(self.source, self.target)

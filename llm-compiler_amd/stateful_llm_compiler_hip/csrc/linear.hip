@@ -572,7 +572,7 @@ int launch_mfma(const void* x, const void* w, const void* bias, void* y, int M,
 
 template <typename T>
 int dispatch_mfma(const void* x, const void* w, const void* bias, void* y, int M,
-                  int N, int K, int64_t x_rs, int64_t y_rs, hipStream_t s) {
+                  int N, int K, int64_t x_rs, int64_t y_rs, hipStream_t s, int tile = SLC_TILE_AUTO) {
   // Up to 32 rows: the decode-step linear kernel the fused ops share.
   const int dtype = sizeof(T) == 2 && std::is_same<T, slc::bf16_t>::value ? SLC_BF16 : SLC_F16;
   if (M <= 32 && slc_host::rows_linear_eligible(x, x_rs, M, K, N, dtype))
@@ -580,9 +580,25 @@ int dispatch_mfma(const void* x, const void* w, const void* bias, void* y, int M
   if (M <= 16) return launch_skinny<T, 1>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
   if (M <= 32) return launch_skinny<T, 2>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
   if (M <= 64) return launch_skinny<T, 4>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
-  // Eight waves of 64 x 32 (78 registers, six waves per SIMD): 4-9 % faster
-  // than four of 64 x 64 at M 4096, equal at 32768.
-  return launch_mfma<T, 128, 128, 2, 4>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
+  // Tile variants (a profile plan picks one): every tile accumulates each
+  // output's k range in the same order, 32 k at a time on one MFMA chain, so
+  // the variants differ in speed only, never in a bit of the result.  The
+  // smaller tiles launch more workgroups for shapes whose 128 x 128 grid
+  // leaves CUs idle (M 4096 x N 128 is 32 workgroups on 256 CUs).
+  switch (tile) {
+    case SLC_TILE_128X64:
+      return launch_mfma<T, 128, 64, 2, 2>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
+    case SLC_TILE_64X128:
+      return launch_mfma<T, 64, 128, 2, 2>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
+    case SLC_TILE_64X64:
+      return launch_mfma<T, 64, 64, 2, 2>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
+    case SLC_TILE_32X64:
+      return launch_mfma<T, 32, 64, 2, 2>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
+    default:
+      // Eight waves of 64 x 32 (78 registers, six waves per SIMD): 4-9 %
+      // faster than four of 64 x 64 at M 4096, equal at 32768.
+      return launch_mfma<T, 128, 128, 2, 4>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
+  }
 }
 
 template <typename T>
@@ -733,11 +749,13 @@ extern "C" int slc_hip_linear_swiglu(const void* input, int64_t in_stride_row, i
                                output, out_stride_row, dtype, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int slc_hip_linear(const void* input, const void* weight,
-                              const void* bias, void* output, int dtype,
-                              int64_t rows, int64_t out_features,
-                              int64_t in_features, int64_t in_stride_row,
-                              int64_t out_stride_row, void* stream) {
+extern "C" int slc_hip_linear_tile(const void* input, const void* weight,
+                                   const void* bias, void* output, int dtype,
+                                   int64_t rows, int64_t out_features,
+                                   int64_t in_features, int64_t in_stride_row,
+                                   int64_t out_stride_row, int tile, void* stream) {
+  SLC_REQUIRE(tile >= SLC_TILE_AUTO && tile <= SLC_TILE_32X64, "slc_hip_linear_tile: bad tile %d",
+              tile);
   SLC_REQUIRE(slc_host::is_float_dtype(dtype), "slc_hip_linear: bad dtype %d", dtype);
   SLC_REQUIRE(rows >= 0 && out_features > 0 && in_features > 0,
               "slc_hip_linear: bad sizes M=%lld N=%lld K=%lld", (long long)rows,
@@ -759,10 +777,10 @@ extern "C" int slc_hip_linear(const void* input, const void* weight,
                       128 * in_stride_row * 2 < (1LL << 31);
   if (vec_ok && dtype == SLC_BF16)
     return dispatch_mfma<slc::bf16_t>(input, weight, bias, output, M, N, K,
-                                      in_stride_row, out_stride_row, s);
+                                      in_stride_row, out_stride_row, s, tile);
   if (vec_ok && dtype == SLC_F16)
     return dispatch_mfma<slc::f16_t>(input, weight, bias, output, M, N, K,
-                                     in_stride_row, out_stride_row, s);
+                                     in_stride_row, out_stride_row, s, tile);
   switch (dtype) {
     case SLC_F32:
       return launch_generic<float>(input, weight, bias, output, M, N, K,
@@ -774,4 +792,13 @@ extern "C" int slc_hip_linear(const void* input, const void* weight,
       return launch_generic<slc::f16_t>(input, weight, bias, output, M, N, K,
                                         in_stride_row, out_stride_row, s);
   }
+}
+
+extern "C" int slc_hip_linear(const void* input, const void* weight,
+                              const void* bias, void* output, int dtype,
+                              int64_t rows, int64_t out_features,
+                              int64_t in_features, int64_t in_stride_row,
+                              int64_t out_stride_row, void* stream) {
+  return slc_hip_linear_tile(input, weight, bias, output, dtype, rows, out_features, in_features,
+                             in_stride_row, out_stride_row, SLC_TILE_AUTO, stream);
 }

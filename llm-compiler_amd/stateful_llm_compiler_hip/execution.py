@@ -48,7 +48,7 @@ from .backends import (
 )
 from . import _native
 from .backends.hip_attention import exact_max_tokens
-from .cost_model import choose_variant, split_tokens, waves_per_row
+from .cost_model import choose_variant, linear_tile, split_tokens, waves_per_row
 from .ir import (
     Function,
     IRType,
@@ -722,14 +722,23 @@ class HipExecutor:
             round_before_weight=bool(attributes.get("round_before_weight", False)),
         )
 
-    @staticmethod
-    def _linear(operands, attributes):
+    def _linear(self, operands, attributes):
         if len(operands) not in (2, 3):
             raise ExecutionError("kernel.hip.linear takes input, weight and an optional bias")
         bias = operands[2] if len(operands) == 3 else None
         if bool(attributes.get("has_bias")) != (bias is not None):
             raise ExecutionError("kernel.hip.linear has_bias does not match its operands")
-        return hip_linear(operands[0], operands[1], bias)
+        plan = attributes.get("tile_plan")
+        tile = "auto"
+        if plan is not None:
+            rows = operands[0].numel() // max(operands[0].shape[-1], 1)
+            choice = choose_variant(plan, max(rows, 1))
+            tile = linear_tile(choice.variant)
+            self.lowering_trace.append({
+                "op": "linear", "backend": "hip", "variant": choice.variant,
+                "source": choice.source, "rows": rows, "estimated_us": choice.estimated_us,
+            })
+        return hip_linear(operands[0], operands[1], bias, tile=tile)
 
     @staticmethod
     def _rope(operands, attributes):

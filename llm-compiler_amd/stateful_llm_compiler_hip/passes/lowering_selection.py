@@ -4,7 +4,9 @@
 ``lowering_plan`` attribute on ``serve.rms_norm`` and its statistics keys
 (src/stateful_llm_compiler/passes/lowering_selection.py:12-72); what the plan
 chooses is a HIP kernel variant (``cost_model``).  ``SelectDecodeSplitPass``
-does the same for the split of ``serve.decode_attention`` (``split_plan``).
+does the same for the split of ``serve.decode_attention`` (``split_plan``)
+and ``SelectLinearTilePass`` for the GEMM tile of ``serve.linear``
+(``tile_plan``).
 """
 
 from __future__ import annotations
@@ -100,3 +102,19 @@ class SelectDecodeSplitPass(_PlanPass):
             return None
         return {"q_heads": dims[0], "kv_heads": dims[0] // groups, "head_dim": dims[1],
                 "dtype": query_type.dtype}
+
+
+class SelectLinearTilePass(_PlanPass):
+    name = "select-linear-tile"
+    op_name = "serve.linear"
+    plan_op = "linear"
+    attribute = "tile_plan"
+
+    def static_key(self, operation: Operation) -> dict[str, Any] | None:
+        if len(operation.operands) < 2:
+            return None
+        dims = _static_dims(operation.operands[1].type, 0, 1)  # weight [N, K]
+        if dims is None:
+            return None
+        return {"out_features": dims[0], "in_features": dims[1],
+                "dtype": operation.operands[0].type.dtype}

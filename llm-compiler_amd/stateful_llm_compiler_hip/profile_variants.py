@@ -21,12 +21,17 @@ from pathlib import Path
 
 import torch
 
-from .backends import hip_decode_attention, hip_rms_norm
+from ._native import LINEAR_TILES
+from .backends import hip_decode_attention, hip_linear, hip_rms_norm
 from .cost_model import SCHEMA_VERSION, split_tokens, waves_per_row
 
 RMS_ROWS = (1, 8, 64, 512, 4096, 32768)
 DECODE_SHAPES = ((1, 1024), (8, 1024), (8, 2048), (8, 8192), (32, 8192), (64, 8192), (8, 32768))
 DECODE_VARIANTS = ("fixed", "balanced", "chunk512", "chunk1024")
+# Qwen2-0.5B projections (N, K) and prefill row counts (batch x tokens).
+LINEAR_SHAPES = ((896, 896), (128, 896), (4864, 896), (896, 4864))
+LINEAR_ROWS = (128, 512, 1024, 2048, 4096, 8192, 32768)
+LINEAR_VARIANTS = tuple(name for name in LINEAR_TILES if name != "auto")
 
 
 def _graph_us(fn, calls: int = 20, replays: int = 5) -> float:
@@ -94,6 +99,35 @@ def profile_decode_attention(dtype: torch.dtype, device, q_heads=14, kv_heads=2,
     return rows_out
 
 
+def profile_linear(dtype: torch.dtype, device, shapes=LINEAR_SHAPES, rows=LINEAR_ROWS,
+                   variants=LINEAR_VARIANTS) -> list[dict]:
+    """Every tile of the prefill-sized linear at each (rows, N, K); the
+    weights rotate over copies totalling at least 256 MB so each call streams
+    its operands from HBM, as in a model's prefill."""
+
+    rows_out = []
+    g = torch.Generator(device=device).manual_seed(2)
+    for n, k in shapes:
+        for m in rows:
+            per_call = (m * k + n * k) * dtype.itemsize
+            copies = max(1, min(16, -(-(256 << 20) // per_call)))
+            xs = [torch.randn(m, k, device=device, generator=g, dtype=dtype) for _ in range(copies)]
+            ws = [(torch.randn(n, k, device=device, generator=g, dtype=dtype) * 0.02) for _ in range(copies)]
+            latencies = {}
+            for variant in variants:
+                turn = itertools.cycle(list(zip(xs, ws)))
+
+                def call(variant=variant, turn=turn):
+                    x, w = next(turn)
+                    hip_linear(x, w, tile=variant)
+
+                latencies[variant] = round(_graph_us(call, calls=2 * copies), 3)
+            rows_out.append({"rows": m, "out_features": n, "in_features": k, "dtype": _name(dtype),
+                             "hip_variants": latencies})
+            del xs, ws
+    return rows_out
+
+
 def _name(dtype: torch.dtype) -> str:
     return {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[dtype]
 
@@ -112,6 +146,7 @@ def build_profile(device="cuda:0") -> dict:
         "benchmark": {"timing": "HIP graph of 20 back-to-back calls, 5 replays, mean per call"},
         "results": profile_rms_norm(896, torch.bfloat16, device),
         "decode_attention": profile_decode_attention(torch.bfloat16, device),
+        "linear": profile_linear(torch.bfloat16, device),
     }
 
 

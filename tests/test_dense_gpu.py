@@ -93,6 +93,76 @@ def test_linear_bf16_bench_rows(gpu, k, n):
     print(f"bitwise agreement with the oracle: {sum(agree) / len(agree):.4f}")
 
 
+TILES = ("t128x128", "t128x64", "t64x128", "t64x64", "t32x64")
+
+
+@pytest.mark.parametrize("rows,k,n,bias", [(4096, 896, 128, True), (300, 896, 896, True),
+                                           (1000, 4864, 896, False), (77, 200, 136, True),
+                                           (520, 896, 4864, False)])
+def test_linear_tiles_are_bit_identical_and_exact(gpu, rows, k, n, bias):
+    """Every GEMM tile variant a plan may pick: within the fp64 product's bar
+    and bit-identical to every other tile (same k order per output)."""
+
+    from stateful_llm_compiler_hip.backends import hip_linear
+
+    g = generator(rows + 7 * k + n)
+    x = torch.randn(rows, k, generator=g).bfloat16()
+    w = (torch.randn(n, k, generator=g) * 0.02).bfloat16()
+    b = (torch.randn(n, generator=g) * 0.02).bfloat16() if bias else None
+    xg, wg, bg = x.to(gpu), w.to(gpu), None if b is None else b.to(gpu)
+    outputs = {}
+    for tile in TILES:
+        announce(f"linear tile {tile} M={rows} K={k} N={n}")
+        outputs[tile] = hip_linear(xg, wg, bg, tile=tile)
+        torch.cuda.synchronize()
+    _check_linear_bf16(outputs["t128x128"], x, w, b)
+    for tile in TILES[1:]:
+        assert torch.equal(outputs[tile], outputs["t128x128"]), tile
+
+
+def test_linear_tile_plan_reaches_the_c_abi(gpu, monkeypatch):
+    """A profile plan's tile choice is the tile argument slc_hip_linear_tile
+    receives (recorded by a pass-through proxy of the loaded library)."""
+
+    from stateful_llm_compiler_hip import _native
+    from stateful_llm_compiler_hip.cost_model import KernelProfile
+    from stateful_llm_compiler_hip.execution import HipExecutor
+
+    lib = _native.library()
+    calls = []
+
+    class Proxy:
+        def __getattr__(self, name):
+            return getattr(lib, name)
+
+        def slc_hip_linear_tile(self, *args):
+            calls.append(args[10])
+            return lib.slc_hip_linear_tile(*args)
+
+    profile = KernelProfile.from_dict({"schema_version": 1, "linear": [
+        {"rows": 512, "out_features": 128, "in_features": 896, "dtype": "bf16",
+         "hip_variants": {"t128x128": 12.0, "t32x64": 9.0}},
+        {"rows": 32768, "out_features": 128, "in_features": 896, "dtype": "bf16",
+         "hip_variants": {"t128x128": 22.0, "t32x64": 28.0}}]})
+    plan = profile.plan("linear", out_features=128, in_features=896, dtype="bf16")
+    g = generator(11)
+    w = (torch.randn(128, 896, generator=g) * 0.02).bfloat16().to(gpu)
+    small = torch.randn(512, 896, generator=g).bfloat16().to(gpu)
+    large = torch.randn(32768, 896, generator=g).bfloat16().to(gpu)
+    executor = HipExecutor()
+    announce("linear tile plan through the executor")
+    monkeypatch.setattr(_native, "_library", Proxy())
+    y_small = executor._linear([small, w], {"has_bias": False, "tile_plan": plan})
+    y_large = executor._linear([large, w], {"has_bias": False, "tile_plan": plan})
+    y_auto = executor._linear([small, w], {"has_bias": False})
+    torch.cuda.synchronize()
+    monkeypatch.undo()
+    tiles = _native.LINEAR_TILES
+    assert calls == [tiles["t32x64"], tiles["t128x128"], tiles["auto"]]
+    assert torch.equal(y_small, y_auto)
+    _check_linear_bf16(y_large[:4096], large[:4096].cpu(), w.cpu(), None, against_oracle=False)
+
+
 @pytest.mark.parametrize("k", [72, 40, 100])
 def test_linear_bf16_k_tails(gpu, k):
     from stateful_llm_compiler_hip.backends import hip_linear

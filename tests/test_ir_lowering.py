@@ -246,6 +246,12 @@ VARIANT_PROFILE = {
         {"batch": 64, "mask_len": 8192, "q_heads": 14, "kv_heads": 2, "head_dim": 64, "dtype": "bf16",
          "hip_variants": {"fixed": 52.0, "balanced": 46.0, "chunk1024": 60.0}},
     ],
+    "linear": [
+        {"rows": 128, "out_features": 128, "in_features": 896, "dtype": "bf16",
+         "hip_variants": {"t128x128": 11.7, "t64x64": 9.0, "t32x64": 5.9}},
+        {"rows": 32768, "out_features": 128, "in_features": 896, "dtype": "bf16",
+         "hip_variants": {"t128x128": 22.0, "t64x64": 20.6, "t32x64": 28.7}},
+    ],
 }
 
 
@@ -317,6 +323,10 @@ def test_profile_plan_passes_attach_plans(tmp_path):
     assert norms and all(op.attributes["lowering_plan"]["op"] == "rms_norm" for op in norms)
     assert attention and all(op.attributes["split_plan"]["op"] == "decode_attention" for op in attention)
     stats = {r.name: r.statistics for r in result.passes}
+    # SMALL's K/V projections are 896 -> 128 (the profiled shape); the
+    # others have no samples and stay unplanned.
+    assert stats["select-linear-tile"]["planned_operations"] == 2 * SMALL.num_layers
+    assert stats["select-linear-tile"]["missing_profile"] > 0
     assert stats["select-rmsnorm-lowering"]["planned_operations"] == len(norms)
     assert stats["select-decode-attention-split"]["planned_operations"] == len(attention)
     # A planned attention keeps its own launch (the fused RoPE + attention
@@ -385,3 +395,42 @@ def test_plan_changes_the_variant_the_executor_launches(monkeypatch):
     assert executor.lowering_trace[-1]["variant"] == "fixed"
 
 
+
+
+def test_linear_tile_plan_follows_rows_and_reaches_the_wrapper(monkeypatch):
+    """The GEMM tile plan: static key (N, K, dtype), run-time axis M; the
+    executor passes the chosen tile to hip_linear (which hands it to
+    slc_hip_linear_tile) and records it in the lowering trace."""
+
+    import torch
+
+    from stateful_llm_compiler_hip import execution
+    from stateful_llm_compiler_hip.cost_model import linear_tile
+
+    profile = KernelProfile.from_dict(VARIANT_PROFILE)
+    plan = profile.plan("linear", out_features=128, in_features=896, dtype="bfloat16")
+    assert plan["axis"] == "rows"
+    assert choose_variant(plan, 128).variant == "t32x64"
+    assert choose_variant(plan, 32768).variant == "t64x64"
+    assert profile.plan("linear", out_features=896, in_features=896, dtype="bf16") is None
+    with pytest.raises(ProfileError):
+        linear_tile("t16x16")
+    with pytest.raises(ProfileError):
+        KernelProfile.from_dict({"schema_version": 1, "linear": [
+            {"rows": 128, "out_features": 128, "in_features": 896, "dtype": "bf16",
+             "hip_variants": {"t256x256": 1.0}}]})
+
+    seen = []
+
+    def fake_linear(tensor, weight, bias=None, *, tile="auto"):
+        seen.append(tile)
+        return tensor
+
+    monkeypatch.setattr(execution, "hip_linear", fake_linear)
+    executor = execution.HipExecutor()
+    w = torch.zeros(128, 896)
+    executor._linear([torch.zeros(2, 64, 896), w], {"has_bias": False, "tile_plan": plan})
+    executor._linear([torch.zeros(32768, 896), w], {"has_bias": False, "tile_plan": plan})
+    executor._linear([torch.zeros(32768, 896), w], {"has_bias": False})
+    assert seen == ["t32x64", "t64x64", "auto"]
+    assert [(t["variant"], t["rows"]) for t in executor.lowering_trace] == [("t32x64", 128), ("t64x64", 32768)]
