@@ -352,6 +352,13 @@ SLC_API int slc_hip_linear(const void* input, const void* weight,
 #define SLC_TILE_64X128 3
 #define SLC_TILE_64X64 4
 #define SLC_TILE_32X64 5
+/* Deep-pipelined forms (producer waves stream k-tiles into a multi-stage LDS
+ * ring); shapes they cannot take (K not a multiple of 64, outputs not
+ * 16-byte aligned) run SLC_TILE_128X128. */
+#define SLC_TILE_R128X128 6
+#define SLC_TILE_R256X128 7
+#define SLC_TILE_R128X64 8
+#define SLC_TILE_R64X64 9
 SLC_API int slc_hip_linear_tile(const void* input, const void* weight,
                                 const void* bias, void* output, int dtype,
                                 int64_t rows, int64_t out_features,

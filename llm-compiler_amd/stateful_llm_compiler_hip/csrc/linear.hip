@@ -403,6 +403,280 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
 }
 
 
+// ---------------------------------------------------------------------------
+// Prefill GEMM with a deep direct-to-LDS ring (KFULL and 16-byte-store shapes).
+//
+// The register-staged kernel above keeps one k-tile in flight per workgroup:
+// each k-tile waits a full memory round trip (~0.7 us under load), so a
+// K = 896 GEMM of any size takes >= 14 round trips and the large shapes sit
+// near 30 % of MFMA peak.  Here PW producer waves stream X and W k-tiles
+// straight into an S-stage LDS ring with buffer_load ... lds (no registers,
+// so S - 1 tiles fly at once), and CWM x CWN consumer waves only read LDS
+// and issue MFMAs.  One workgroup barrier per k-tile: before it the
+// producers wait until their loads of tile kt have landed (vmcnt), after it
+// they refill the stage every consumer has just finished reading.  The
+// producers' barrier is a bare s_barrier: __syncthreads() would also wait
+// for all their in-flight loads and drain the ring.
+//
+// LDS rows are 128 bytes (64 bf16 of K) with 16-byte chunks XOR-swizzled by
+// row, as above: lane L of DMA instruction n fills LDS row 8n + L/8 at chunk
+// position L%8 with global chunk (L%8) ^ (row & 7).  Consumer fragment reads
+// and the k order of every MFMA chain are those of linear_mfma_kernel, so
+// the two kernels give bit-identical outputs.  Past the last k-tile the
+// producers keep issuing loads through an empty buffer range (no traffic,
+// zeros into a stage nobody reads) so every wait counts the same number of
+// loads; they drain them before the epilogue reuses the ring.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, unsigned char* lds,
+                                          int voffset, int soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      rsrc, (__attribute__((address_space(3))) void*)lds, 16, voffset, soffset, 0, 0);
+}
+
+// Workgroup id -> (m_blk, n_blk): gathered per XCD, then groups of 8 M-tiles
+// (see linear_mfma_kernel).
+template <int kGroupM>
+__device__ __forceinline__ void xcd_tile(int n_tiles, int m_tiles, int& m_blk, int& n_blk) {
+  constexpr int kXcds = 8;
+  const int total = n_tiles * m_tiles;
+  const int id = blockIdx.y * n_tiles + blockIdx.x;
+  const int per = total / kXcds;
+  const int t = id < per * kXcds ? (id % kXcds) * per + id / kXcds : id;
+  const int span = kGroupM * n_tiles;
+  const int first_m = (t / span) * kGroupM;
+  const int gm = m_tiles - first_m < kGroupM ? m_tiles - first_m : kGroupM;
+  m_blk = first_m + (t % span) % gm;
+  n_blk = (t % span) / gm;
+}
+
+template <typename T, int BM, int BN, int CWM, int CWN, int PW, int S, int GM = 8,
+          bool DUAL = false, bool GROUP = false>
+__global__ __launch_bounds__((CWM * CWN + PW) * 64) void linear_ring_kernel(
+    const T* __restrict__ x, const T* __restrict__ w_arg, const T* __restrict__ bias_arg,
+    T* __restrict__ y_arg, int M, int N_arg, int K, int64_t x_rs, int64_t y_rs_arg,
+    const T* __restrict__ residual, int64_t r_rs, const T* __restrict__ w2 = nullptr,
+    LinearGroup grp = {}) {
+  using MF = Mfma<T>;
+  constexpr int CW = CWM * CWN;      // consumer waves
+  constexpr int CT = CW * 64;        // consumer threads
+  constexpr int TM = BM / CWM;
+  constexpr int TN = BN / CWN;
+  constexpr int FM = TM / 16;
+  constexpr int FN = TN / 16;
+  constexpr int XB = BM * kBK * 2;   // bytes of an X tile
+  constexpr int kStage = (BM + BN) * kBK * 2;
+  constexpr int kOps = (BM + BN) / 8 / PW;  // 1 KB DMA instructions per producer wave per tile
+  static_assert(((BM + BN) / 8) % PW == 0, "DMA instructions split evenly over the producers");
+  static_assert((S - 2) * kOps <= 63, "the wait count fits vmcnt");
+  static_assert(TM % 16 == 0 && TN % 16 == 0, "whole MFMA fragments per wave");
+  constexpr int kEpiWave = TM * (TN + 8) * 2;
+  constexpr int kEpiDual = BM * (BN + 8) * 2;
+  static_assert(CW * kEpiWave <= S * kStage && (!DUAL || kEpiDual <= S * kStage),
+                "epilogue staging fits in the ring");
+  __shared__ __attribute__((aligned(16))) unsigned char ring[S * kStage];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  int m_blk, n_blk;
+  xcd_tile<GM>(gridDim.x, gridDim.y, m_blk, n_blk);
+  const T* w = w_arg;
+  const T* bias = bias_arg;
+  T* y = y_arg;
+  int N = N_arg;
+  int64_t y_rs = y_rs_arg;
+  if constexpr (GROUP) {
+    const int j = n_blk < grp.tile_end[0] ? 0 : (n_blk < grp.tile_end[1] ? 1 : 2);
+    n_blk -= j == 0 ? 0 : grp.tile_end[j - 1];
+    w = static_cast<const T*>(grp.w[j]);
+    bias = static_cast<const T*>(grp.bias[j]);
+    y = static_cast<T*>(grp.y[j]);
+    N = grp.n[j];
+    y_rs = grp.y_rs[j];
+  }
+  const int n0 = n_blk * (DUAL ? BN / 2 : BN);
+  const int m0 = m_blk * BM;
+  const int ktiles = K / kBK;
+
+  if (wave >= CW) {
+    // ---- producers ------------------------------------------------------
+    const int pw = wave - CW;
+    const int64_t x_rows = M - m0 < BM ? M - m0 : BM;
+    const int64_t w_rows = DUAL ? (N - n0 < BN / 2 ? N - n0 : BN / 2) : (N - n0 < BN ? N - n0 : BN);
+    const __amdgpu_buffer_rsrc_t rx =
+        make_rsrc(x + m0 * x_rs, x_rows > 0 ? (x_rows - 1) * x_rs * 2 + K * 2 : 0);
+    const __amdgpu_buffer_rsrc_t rw =
+        make_rsrc(w + static_cast<int64_t>(n0) * K, w_rows > 0 ? w_rows * K * 2 : 0);
+    const __amdgpu_buffer_rsrc_t rw2 = make_rsrc(DUAL ? w2 + static_cast<int64_t>(n0) * K : w,
+                                                 DUAL && w_rows > 0 ? w_rows * K * 2 : 0);
+    const __amdgpu_buffer_rsrc_t rnone = make_rsrc(x, 0);
+    // The X tile's BM / 8 DMA instructions, then the W tile's BN / 8 (gate
+    // rows then up rows under DUAL), are dealt round-robin to the producers:
+    // instruction i of a wave has a compile-time operand (X, W or up) and
+    // covers the ring rows 8 * (pw + PW * i') .. + 7 of that operand.
+    constexpr int XO = BM / 8 / PW;
+    constexpr int WO = (DUAL ? BN / 2 : BN) / 8 / PW;
+    static_assert(XO * PW * 8 == BM && WO * PW * 8 == (DUAL ? BN / 2 : BN) &&
+                      XO + WO * (DUAL ? 2 : 1) == kOps,
+                  "operands split evenly over the producers");
+    int voff[kOps];
+#pragma unroll
+    for (int i = 0; i < kOps; ++i) {
+      const int local = i < XO ? i : (i - XO) % WO;  // instruction index inside its operand
+      const int row = 8 * (pw + PW * local) + lane / 8;
+      const int chunk = (lane % 8) ^ (row & 7);
+      voff[i] = i < XO ? static_cast<int>(row * x_rs * 2) + chunk * 16 : row * K * 2 + chunk * 16;
+    }
+    auto issue = [&](int kt) {
+      unsigned char* dst = ring + (kt % S) * kStage;
+      const bool live = kt < ktiles;
+      const int kb = __builtin_amdgcn_readfirstlane(live ? kt * kBK * 2 : 0);
+      const __amdgpu_buffer_rsrc_t lx = live ? rx : rnone;
+      const __amdgpu_buffer_rsrc_t lw = live ? rw : rnone;
+      const __amdgpu_buffer_rsrc_t lw2 = live ? rw2 : rnone;
+#pragma unroll
+      for (int i = 0; i < kOps; ++i) {
+        if (i < XO) {
+          lds_dma16(lx, dst + (pw + PW * i) * 1024, voff[i], kb);
+        } else if (i < XO + WO) {
+          lds_dma16(lw, dst + XB + (pw + PW * (i - XO)) * 1024, voff[i], kb);
+        } else {
+          lds_dma16(lw2, dst + XB + (BN / 2) * 128 + (pw + PW * (i - XO - WO)) * 1024, voff[i], kb);
+        }
+      }
+    };
+#pragma unroll
+    for (int t = 0; t < S - 1; ++t) issue(t);
+    for (int kt = 0; kt < ktiles; ++kt) {
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"i"((S - 2) * kOps) : "memory");
+      issue(kt + S - 1);
+    }
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    return;
+  }
+
+  // ---- consumers ----------------------------------------------------------
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int wm = wave / CWN;
+  const int wn = wave % CWN;
+  f32x4_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int kt = 0; kt < ktiles; ++kt) {
+    __syncthreads();  // tile kt is in its stage; the stage of kt - 1 may be refilled
+    const unsigned char* xs = ring + (kt % S) * kStage;
+    const unsigned char* ws = xs + XB;
+#pragma unroll
+    for (int kk = 0; kk < kBK / 32; ++kk) {
+      typename MF::vec a[FM], b[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        a[i] = *reinterpret_cast<const typename MF::vec*>(xs + lds_offset(wm * TM + i * 16 + c, kk * 4 + g));
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        b[j] = *reinterpret_cast<const typename MF::vec*>(ws + lds_offset(wn * TN + j * 16 + c, kk * 4 + g));
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = MF::run(a[i], b[j], acc[i][j]);
+    }
+  }
+  __syncthreads();  // the producers drained their loads; the ring is free
+
+  if constexpr (DUAL) {
+    constexpr int kRow = BN + 8;
+    uint16_t* cs = reinterpret_cast<uint16_t*>(ring);
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          cs[(wm * TM + i * 16 + 4 * g + r) * kRow + wn * TN + j * 16 + c] =
+              slc::from_f32<T>(acc[i][j][r]).bits;
+    __syncthreads();  // consumers only (the producers have ended)
+    const int rows = M - m0 < BM ? M - m0 : BM;
+    const __amdgpu_buffer_rsrc_t ry =
+        make_rsrc(y + m0 * y_rs, (static_cast<int64_t>(rows) - 1) * y_rs * 2 + N * 2);
+    constexpr int kPerRow = BN / 2 / 8;
+    static_assert((BM * kPerRow) % CT == 0, "whole store rounds");
+#pragma unroll
+    for (int q = 0; q < BM * kPerRow / CT; ++q) {
+      const int id = q * CT + tid;
+      const int row = id / kPerRow, chunk = id % kPerRow;
+      const uint4 gv = *reinterpret_cast<const uint4*>(cs + row * kRow + chunk * 8);
+      const uint4 uv = *reinterpret_cast<const uint4*>(cs + row * kRow + BN / 2 + chunk * 8);
+      const uint16_t* gb = reinterpret_cast<const uint16_t*>(&gv);
+      const uint16_t* ub = reinterpret_cast<const uint16_t*>(&uv);
+      uint4 o;
+      uint16_t* ob = reinterpret_cast<uint16_t*>(&o);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        T ge, ue;
+        ge.bits = gb[e];
+        ue.bits = ub[e];
+        ob[e] = slc::from_f32<T>(slc::swiglu_value<T>(slc::to_f32(ge), slc::to_f32(ue))).bits;
+      }
+      const int n = n0 + chunk * 8;
+      if (row < rows && n < N)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, o), ry,
+                                               static_cast<int>(row * y_rs + n) * 2, 0, 0);
+    }
+    return;
+  } else {
+    constexpr int kCPad = TN + 8;
+    uint16_t* cs = reinterpret_cast<uint16_t*>(ring) + wave * TM * kCPad;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = n0 + wn * TN + j * 16 + c;
+      const float bv = bias != nullptr && n < N ? slc::to_f32(bias[n]) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          cs[(i * 16 + 4 * g + r) * kCPad + j * 16 + c] = slc::from_f32<T>(acc[i][j][r] + bv).bits;
+    }
+    const int rows = M - m0 < BM ? M - m0 : BM;
+    const __amdgpu_buffer_rsrc_t ry =
+        make_rsrc(y + m0 * y_rs, (static_cast<int64_t>(rows) - 1) * y_rs * 2 + N * 2);
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(
+        residual != nullptr ? residual + m0 * r_rs : y,
+        residual != nullptr ? (static_cast<int64_t>(rows) - 1) * r_rs * 2 + N * 2 : 0);
+    constexpr int kPerRow = TN / 8;
+    static_assert((TM * kPerRow) % 64 == 0, "whole store rounds per wave");
+#pragma unroll
+    for (int q = 0; q < TM * kPerRow / 64; ++q) {
+      const int id = q * 64 + lane;
+      const int row = id / kPerRow, chunk = id % kPerRow;
+      const int m_local = wm * TM + row;
+      const int n = n0 + wn * TN + chunk * 8;
+      uint4 v = *reinterpret_cast<const uint4*>(cs + row * kCPad + chunk * 8);
+      if (residual != nullptr) {
+        const uint4 rv = buffer_load16(rr, static_cast<int>(m_local * r_rs + n) * 2);
+        const uint16_t* lin = reinterpret_cast<const uint16_t*>(&v);
+        const uint16_t* res = reinterpret_cast<const uint16_t*>(&rv);
+        uint4 o;
+        uint16_t* out = reinterpret_cast<uint16_t*>(&o);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          T a, r;
+          a.bits = lin[e];
+          r.bits = res[e];
+          out[e] = slc::from_f32<T>(slc::to_f32(r) + slc::to_f32(a)).bits;
+        }
+        v = o;
+      }
+      if (m_local < rows && n < N)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v), ry,
+                                               static_cast<int>(m_local * y_rs + n) * 2, 0, 0);
+    }
+  }
+}
+
+
 // Decode-sized M (<= 64): Y is a handful of rows, W streams from HBM once.
 // One workgroup owns 16 output features and all M rows; its KW waves split K
 // between them (partial sums meet in LDS at the end), so even a 896-wide
@@ -570,6 +844,57 @@ int launch_mfma(const void* x, const void* w, const void* bias, void* y, int M,
   return slc_host::check_launch("slc_hip_linear");
 }
 
+// The ring kernel where the shape allows it (K a multiple of the k-tile, the
+// 16-byte store path), else the register-staged kernel of the same tile.
+template <typename T, int BM, int BN, int CWM, int CWN, int PW, int S, int GM = 8>
+int launch_ring(const void* x, const void* w, const void* bias, void* y, int M, int N, int K,
+                int64_t x_rs, int64_t y_rs, hipStream_t stream, const void* residual = nullptr,
+                int64_t r_rs = 0) {
+  const bool vst = N % 8 == 0 && y_rs % 8 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0 &&
+                   static_cast<int64_t>(BM) * y_rs * 2 < (int64_t{1} << 31) &&
+                   static_cast<int64_t>(BM) * x_rs * 2 < (int64_t{1} << 31) &&
+                   (residual == nullptr || static_cast<int64_t>(BM) * r_rs * 2 < (int64_t{1} << 31));
+  if (K % kBK != 0 || !vst) return kNoResidualPath;
+  const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
+  hipLaunchKernelGGL((linear_ring_kernel<T, BM, BN, CWM, CWN, PW, S, GM>), grid,
+                     dim3((CWM * CWN + PW) * 64), 0, stream, static_cast<const T*>(x),
+                     static_cast<const T*>(w), static_cast<const T*>(bias), static_cast<T*>(y), M, N,
+                     K, x_rs, y_rs, static_cast<const T*>(residual), r_rs);
+  return slc_host::check_launch("slc_hip_linear(ring)");
+}
+
+// Ring-kernel tile for a shape when the caller leaves it to the library:
+// 256 x 128 once that grid holds at least half a workgroup per CU per round
+// (two rounds of 128 on 256 CUs), else 128 x 128 under the same rule, else
+// the 64 x 64 tile (small grids: most CUs would idle at larger tiles, and the
+// deep ring hides the latency of K's many k-tiles).  Measured on MI355X at
+// the Qwen2-0.5B projection shapes for M = 128 .. 32768.
+inline int auto_ring_tile(int64_t M, int64_t n_tiles128) {
+  const int64_t n256 = ((M + 255) / 256) * n_tiles128;
+  const int64_t n128 = ((M + 127) / 128) * n_tiles128;
+  return n256 >= 128 ? SLC_TILE_R256X128 : (n128 >= 128 ? SLC_TILE_R128X128 : SLC_TILE_R64X64);
+}
+
+// One of the ring tiles; kNoResidualPath (nothing launched) where the shape
+// does not fit the ring kernel.
+template <typename T>
+int launch_ring_tile(int tile, const void* x, const void* w, const void* bias, void* y, int M,
+                     int N, int K, int64_t x_rs, int64_t y_rs, hipStream_t s,
+                     const void* residual = nullptr, int64_t r_rs = 0) {
+  switch (tile) {
+    case SLC_TILE_R128X128:
+      return launch_ring<T, 128, 128, 2, 4, 2, 4>(x, w, bias, y, M, N, K, x_rs, y_rs, s, residual, r_rs);
+    case SLC_TILE_R256X128:
+      // Groups of 4 M-tiles per XCD: eight 256-row X tiles (3.7 MB) would
+      // not stay in one XCD's 4 MB L2 beside the W tiles.
+      return launch_ring<T, 256, 128, 4, 2, 4, 3, 4>(x, w, bias, y, M, N, K, x_rs, y_rs, s, residual, r_rs);
+    case SLC_TILE_R128X64:
+      return launch_ring<T, 128, 64, 2, 2, 1, 3>(x, w, bias, y, M, N, K, x_rs, y_rs, s, residual, r_rs);
+    default:
+      return launch_ring<T, 64, 64, 2, 2, 1, 5>(x, w, bias, y, M, N, K, x_rs, y_rs, s, residual, r_rs);
+  }
+}
+
 template <typename T>
 int dispatch_mfma(const void* x, const void* w, const void* bias, void* y, int M,
                   int N, int K, int64_t x_rs, int64_t y_rs, hipStream_t s, int tile = SLC_TILE_AUTO) {
@@ -582,9 +907,8 @@ int dispatch_mfma(const void* x, const void* w, const void* bias, void* y, int M
   if (M <= 64) return launch_skinny<T, 4>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
   // Tile variants (a profile plan picks one): every tile accumulates each
   // output's k range in the same order, 32 k at a time on one MFMA chain, so
-  // the variants differ in speed only, never in a bit of the result.  The
-  // smaller tiles launch more workgroups for shapes whose 128 x 128 grid
-  // leaves CUs idle (M 4096 x N 128 is 32 workgroups on 256 CUs).
+  // the variants differ in speed only, never in a bit of the result.
+  if (tile == SLC_TILE_AUTO) tile = auto_ring_tile(M, (N + 127) / 128);
   switch (tile) {
     case SLC_TILE_128X64:
       return launch_mfma<T, 128, 64, 2, 2>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
@@ -594,10 +918,17 @@ int dispatch_mfma(const void* x, const void* w, const void* bias, void* y, int M
       return launch_mfma<T, 64, 64, 2, 2>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
     case SLC_TILE_32X64:
       return launch_mfma<T, 32, 64, 2, 2>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
-    default:
+    case SLC_TILE_128X128:
       // Eight waves of 64 x 32 (78 registers, six waves per SIMD): 4-9 %
       // faster than four of 64 x 64 at M 4096, equal at 32768.
       return launch_mfma<T, 128, 128, 2, 4>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
+    default: {
+      const int rc = launch_ring_tile<T>(tile, x, w, bias, y, M, N, K, x_rs, y_rs, s);
+      if (rc != kNoResidualPath) return rc;
+      // K not a multiple of the k-tile, or outputs the 16-byte stores cannot
+      // take: the register-staged kernel.
+      return launch_mfma<T, 128, 128, 2, 4>(x, w, bias, y, M, N, K, x_rs, y_rs, s);
+    }
   }
 }
 
@@ -632,11 +963,18 @@ int gemm_residual(const void* x, int64_t x_rs, int64_t rows, int64_t K, int64_t 
                   128 * r_rs * 2 < (int64_t{1} << 31) && rows < (int64_t{1} << 31);
   if (!ok) return SLC_ERR_UNSUPPORTED;
   const int M = static_cast<int>(rows), n = static_cast<int>(N), k = static_cast<int>(K);
-  const int rc = dtype == SLC_BF16
-                     ? launch_mfma<slc::bf16_t, 128, 128, 2, 4>(x, w, bias, y, M, n, k, x_rs, y_rs,
-                                                                stream, residual, r_rs)
-                     : launch_mfma<slc::f16_t, 128, 128, 2, 4>(x, w, bias, y, M, n, k, x_rs, y_rs,
-                                                               stream, residual, r_rs);
+  const int tile = auto_ring_tile(M, (n + 127) / 128);
+  int rc = dtype == SLC_BF16
+               ? launch_ring_tile<slc::bf16_t>(tile, x, w, bias, y, M, n, k, x_rs, y_rs, stream,
+                                               residual, r_rs)
+               : launch_ring_tile<slc::f16_t>(tile, x, w, bias, y, M, n, k, x_rs, y_rs, stream,
+                                              residual, r_rs);
+  if (rc != kNoResidualPath) return rc;
+  rc = dtype == SLC_BF16
+           ? launch_mfma<slc::bf16_t, 128, 128, 2, 4>(x, w, bias, y, M, n, k, x_rs, y_rs,
+                                                      stream, residual, r_rs)
+           : launch_mfma<slc::f16_t, 128, 128, 2, 4>(x, w, bias, y, M, n, k, x_rs, y_rs,
+                                                     stream, residual, r_rs);
   return rc == kNoResidualPath ? SLC_ERR_UNSUPPORTED : rc;
 }
 
@@ -655,17 +993,19 @@ int gemm_swiglu(const void* x, int64_t x_rs, int64_t rows, int64_t K, int64_t N,
                   128 * y_rs * 2 < (int64_t{1} << 31) && rows < (int64_t{1} << 31);
   if (!ok) return SLC_ERR_UNSUPPORTED;
   const int M = static_cast<int>(rows), n = static_cast<int>(N), k = static_cast<int>(K);
-  const dim3 grid((n + 63) / 64, (M + 127) / 128);
-#define SLC_DUAL(TT)                                                                         \
-  hipLaunchKernelGGL((linear_mfma_kernel<TT, 128, 128, 2, 4, true, true, true>), grid,       \
-                     dim3(512), 0, stream, static_cast<const TT*>(x),                         \
-                     static_cast<const TT*>(w_gate), static_cast<const TT*>(nullptr),         \
-                     static_cast<TT*>(y), M, n, k, x_rs, y_rs, static_cast<const TT*>(nullptr), \
-                     int64_t{0}, static_cast<const TT*>(w_up))
+  // The ring kernel; each 128-wide column tile holds 64 gate and 64 up rows.
+  const bool big = auto_ring_tile(M, (n + 63) / 64) == SLC_TILE_R256X128 &&
+                   256 * x_rs * 2 < (int64_t{1} << 31) && 256 * y_rs * 2 < (int64_t{1} << 31);
+#define SLC_DUAL(TT, BM, CWM, PW, S, GM)                                                          \
+  hipLaunchKernelGGL((linear_ring_kernel<TT, BM, 128, CWM, 2 * 4 / CWM, PW, S, GM, true>),         \
+                     dim3((n + 63) / 64, (M + BM - 1) / BM), dim3((8 + PW) * 64), 0, stream,      \
+                     static_cast<const TT*>(x), static_cast<const TT*>(w_gate),                   \
+                     static_cast<const TT*>(nullptr), static_cast<TT*>(y), M, n, k, x_rs, y_rs,   \
+                     static_cast<const TT*>(nullptr), int64_t{0}, static_cast<const TT*>(w_up))
   if (dtype == SLC_BF16) {
-    SLC_DUAL(slc::bf16_t);
+    if (big) SLC_DUAL(slc::bf16_t, 256, 4, 4, 3, 4); else SLC_DUAL(slc::bf16_t, 128, 2, 2, 4, 8);
   } else {
-    SLC_DUAL(slc::f16_t);
+    if (big) SLC_DUAL(slc::f16_t, 256, 4, 4, 3, 4); else SLC_DUAL(slc::f16_t, 128, 2, 2, 4, 8);
   }
 #undef SLC_DUAL
   return check_launch("slc_hip_linear_swiglu");
@@ -700,17 +1040,19 @@ int gemm_group(const void* x, int64_t x_rs, int64_t rows, int64_t K, int count,
   }
   if (!ok) return SLC_ERR_UNSUPPORTED;
   const int M = static_cast<int>(rows), k = static_cast<int>(K);
-  const dim3 grid(static_cast<unsigned>(tiles), (M + 127) / 128);
-#define SLC_GROUP(TT)                                                                          \
-  hipLaunchKernelGGL((linear_mfma_kernel<TT, 128, 128, 2, 4, true, true, false, true>), grid, \
-                     dim3(512), 0, stream, static_cast<const TT*>(x),                           \
-                     static_cast<const TT*>(nullptr), static_cast<const TT*>(nullptr),          \
-                     static_cast<TT*>(nullptr), M, 0, k, x_rs, int64_t{0},                      \
-                     static_cast<const TT*>(nullptr), int64_t{0}, static_cast<const TT*>(nullptr), g)
+  bool big = auto_ring_tile(M, tiles) == SLC_TILE_R256X128 && 256 * x_rs * 2 < (int64_t{1} << 31);
+  for (int j = 0; j < count; ++j) big = big && 256 * y_rs[j] * 2 < (int64_t{1} << 31);
+#define SLC_GROUP(TT, BM, CWM, PW, S, GM)                                                        \
+  hipLaunchKernelGGL((linear_ring_kernel<TT, BM, 128, CWM, 2 * 4 / CWM, PW, S, GM, false, true>), \
+                     dim3(static_cast<unsigned>(tiles), (M + BM - 1) / BM), dim3((8 + PW) * 64), \
+                     0, stream, static_cast<const TT*>(x), static_cast<const TT*>(nullptr),       \
+                     static_cast<const TT*>(nullptr), static_cast<TT*>(nullptr), M, 0, k, x_rs,   \
+                     int64_t{0}, static_cast<const TT*>(nullptr), int64_t{0},                     \
+                     static_cast<const TT*>(nullptr), g)
   if (dtype == SLC_BF16) {
-    SLC_GROUP(slc::bf16_t);
+    if (big) SLC_GROUP(slc::bf16_t, 256, 4, 4, 3, 4); else SLC_GROUP(slc::bf16_t, 128, 2, 2, 4, 8);
   } else {
-    SLC_GROUP(slc::f16_t);
+    if (big) SLC_GROUP(slc::f16_t, 256, 4, 4, 3, 4); else SLC_GROUP(slc::f16_t, 128, 2, 2, 4, 8);
   }
 #undef SLC_GROUP
   return check_launch("slc_hip_linear_group");
@@ -754,7 +1096,7 @@ extern "C" int slc_hip_linear_tile(const void* input, const void* weight,
                                    int64_t rows, int64_t out_features,
                                    int64_t in_features, int64_t in_stride_row,
                                    int64_t out_stride_row, int tile, void* stream) {
-  SLC_REQUIRE(tile >= SLC_TILE_AUTO && tile <= SLC_TILE_32X64, "slc_hip_linear_tile: bad tile %d",
+  SLC_REQUIRE(tile >= SLC_TILE_AUTO && tile <= SLC_TILE_R64X64, "slc_hip_linear_tile: bad tile %d",
               tile);
   SLC_REQUIRE(slc_host::is_float_dtype(dtype), "slc_hip_linear: bad dtype %d", dtype);
   SLC_REQUIRE(rows >= 0 && out_features > 0 && in_features > 0,

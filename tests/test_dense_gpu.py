@@ -93,7 +93,7 @@ def test_linear_bf16_bench_rows(gpu, k, n):
     print(f"bitwise agreement with the oracle: {sum(agree) / len(agree):.4f}")
 
 
-TILES = ("t128x128", "t128x64", "t64x128", "t64x64", "t32x64")
+TILES = ("t128x128", "t128x64", "t64x128", "t64x64", "t32x64", "r128x128", "r256x128", "r128x64", "r64x64")
 
 
 @pytest.mark.parametrize("rows,k,n,bias", [(4096, 896, 128, True), (300, 896, 896, True),
