@@ -200,8 +200,10 @@ def hip_decode_attention_noalloc(
     """``hip_decode_attention`` into the caller's ``output`` through the entry
     point that allocates nothing (``slc_hip_decode_attention_noalloc``): its
     split partials and counters live in the library's own device array, so
-    the call makes no device allocation at all.  Calls that overlap in time on
-    one GPU share that array and race."""
+    the call makes no device allocation at all.  Every call on one GPU shares
+    that array: calls that may overlap in time -- on two streams, or two
+    graphs replayed concurrently -- race, so issue them from one stream per
+    GPU.  Nothing checks this at run time."""
 
     order = _native.softmax_order_tag(softmax_order)
     batch, query_heads, head_dim, capacity, kv_heads = _check_decode_operands(

@@ -96,19 +96,11 @@ struct LinearGroup {
   int tile_end[3];
 };
 
-// DUAL (with KFULL and VST): the gate/up projections and SwiGLU in one pass.
-// A workgroup's BN columns are BN / 2 features of w (gate) followed by the
-// same features of w2 (up); its epilogue stages the rounded tile in LDS and
-// writes y = swiglu(gate, up) for those BN / 2 features (no bias).
-template <typename T, int BM, int BN, int WM, int WN, bool KFULL, bool VST, bool DUAL = false,
-          bool GROUP = false>
+template <typename T, int BM, int BN, int WM, int WN, bool KFULL, bool VST>
 __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
-    const T* __restrict__ x, const T* __restrict__ w_arg, const T* __restrict__ bias_arg,
-    T* __restrict__ y_arg, int M, int N_arg, int K, int64_t x_rs, int64_t y_rs_arg,
-    const T* __restrict__ residual, int64_t r_rs, const T* __restrict__ w2 = nullptr,
-    LinearGroup grp = {}) {
-  static_assert(!DUAL || (KFULL && VST), "the fused SwiGLU uses the K-multiple store path");
-  static_assert(!GROUP || (KFULL && VST && !DUAL), "grouped projections use the store path");
+    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
+    T* __restrict__ y, int M, int N, int K, int64_t x_rs, int64_t y_rs,
+    const T* __restrict__ residual, int64_t r_rs) {
   using MF = Mfma<T>;
   constexpr int NT = WM * WN * 64;  // threads per workgroup
   constexpr int TM = BM / WM;  // rows per wave
@@ -123,13 +115,12 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
   constexpr int WB = BN * kBK * 2;
 
   // One LDS tile pair (the next k-tile waits in registers while this one is
-  // read), or the epilogue's staging if larger: 36 KB at 128 x 128, so three
+  // read), or the epilogue's staging if larger: 40 KB at 128 x 128, so three
   // workgroups share a CU (two with a double-buffered 64 KB ring: the third
   // workgroup hides more load latency than the second barrier per k-tile
   // costs, 362 -> 333 us at M32768 N4864 K896).
   constexpr int kStage = XB + WB;
-  constexpr int kEpi = (BM * (BN + 8) * 2 > WM * WN * TM * (TN + 8) * 2) ? BM * (BN + 8) * 2
-                                                                        : WM * WN * TM * (TN + 8) * 2;
+  constexpr int kEpi = WM * WN * TM * (TN + 8) * 2;
   constexpr int kSmem = kStage > kEpi ? kStage : kEpi;
   __shared__ __attribute__((aligned(16))) unsigned char smem[kSmem];
 
@@ -160,35 +151,16 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
     m_blk = first_m + (t % span) % gm;
     n_blk = (t % span) / gm;
   }
-  // GROUP: the matrix of this N-tile and the tile's index inside it.
-  const T* w = w_arg;
-  const T* bias = bias_arg;
-  T* y = y_arg;
-  int N = N_arg;
-  int64_t y_rs = y_rs_arg;
-  if constexpr (GROUP) {
-    const int j = n_blk < grp.tile_end[0] ? 0 : (n_blk < grp.tile_end[1] ? 1 : 2);
-    n_blk -= j == 0 ? 0 : grp.tile_end[j - 1];
-    w = static_cast<const T*>(grp.w[j]);
-    bias = static_cast<const T*>(grp.bias[j]);
-    y = static_cast<T*>(grp.y[j]);
-    N = grp.n[j];
-    y_rs = grp.y_rs[j];
-  }
-  // DUAL: n0 is the first feature, BN / 2 of them per workgroup.
-  const int n0 = n_blk * (DUAL ? BN / 2 : BN);
+  const int n0 = n_blk * BN;
   const int m0 = m_blk * BM;
 
   // Buffer resources over the workgroup's rows: rows past M / N read zero.
   const int64_t x_rows = M - m0 < BM ? M - m0 : BM;
-  const int64_t w_rows = DUAL ? (N - n0 < BN / 2 ? N - n0 : BN / 2) : (N - n0 < BN ? N - n0 : BN);
+  const int64_t w_rows = N - n0 < BN ? N - n0 : BN;
   const __amdgpu_buffer_rsrc_t rx =
       make_rsrc(x + m0 * x_rs, x_rows > 0 ? (x_rows - 1) * x_rs * 2 + K * 2 : 0);
   const __amdgpu_buffer_rsrc_t rw =
       make_rsrc(w + static_cast<int64_t>(n0) * K, w_rows > 0 ? w_rows * K * 2 : 0);
-  // The up rows (DUAL): W-tile rows BN / 2 .. BN - 1.
-  const __amdgpu_buffer_rsrc_t rw2 =
-      make_rsrc(DUAL ? w2 + static_cast<int64_t>(n0) * K : w, DUAL && w_rows > 0 ? w_rows * K * 2 : 0);
 
   uint4 xr[XPT], wr[WPT];
   static_assert(!KFULL || (XCH % NT == 0 && WCH % NT == 0), "whole chunks per thread");
@@ -201,13 +173,8 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
 #pragma unroll
   for (int i = 0; i < WPT; ++i) {
     const int ch = tid + NT * i;
-    const int row = DUAL ? (ch / kChunks) % (BN / 2) : ch / kChunks;
-    woff[i] = (row * K + (ch % kChunks) * 8) * 2;
+    woff[i] = ((ch / kChunks) * K + (ch % kChunks) * 8) * 2;
   }
-  // DUAL: chunk set i covers W-tile rows NT * i / kChunks ..; the first half
-  // of the sets are gate rows, the rest up rows (a compile-time split).
-  static_assert(!DUAL || (WPT % 2 == 0 && (WPT / 2) * NT == (BN / 2) * kChunks),
-                "gate and up rows split evenly over the chunk sets");
   auto fetch = [&](int k0) {
     if constexpr (KFULL) {
       const int kb = __builtin_amdgcn_readfirstlane(k0 * 2);
@@ -215,7 +182,7 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
       for (int i = 0; i < XPT; ++i) xr[i] = buffer_load16(rx, xoff[i], kb);
 #pragma unroll
       for (int i = 0; i < WPT; ++i)
-        wr[i] = buffer_load16(DUAL && i >= WPT / 2 ? rw2 : rw, woff[i], kb);
+        wr[i] = buffer_load16(rw, woff[i], kb);
       return;
     }
 #pragma unroll
@@ -288,50 +255,6 @@ __global__ __launch_bounds__(WM * WN * 64) void linear_mfma_kernel(
     __syncthreads();
   }
 
-  if constexpr (DUAL) {
-    // The whole BM x BN tile, rounded to T, in LDS (the loop ended on a
-    // barrier), then SwiGLU of each feature's gate (column j) and up (column
-    // BN / 2 + j) values, 8 features per 16-byte store.
-    constexpr int kRow = BN + 8;
-    static_assert(BM * kRow * 2 <= kSmem, "staging fits the LDS");
-    uint16_t* cs = reinterpret_cast<uint16_t*>(smem);
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          cs[(wm * TM + i * 16 + 4 * g + r) * kRow + wn * TN + j * 16 + c] =
-              slc::from_f32<T>(acc[i][j][r]).bits;
-    __syncthreads();
-    const int rows = M - m0 < BM ? M - m0 : BM;
-    const __amdgpu_buffer_rsrc_t ry =
-        make_rsrc(y + m0 * y_rs, (static_cast<int64_t>(rows) - 1) * y_rs * 2 + N * 2);
-    constexpr int kPerRow = BN / 2 / 8;
-#pragma unroll
-    for (int q = 0; q < BM * kPerRow / NT; ++q) {
-      const int id = q * NT + tid;
-      const int row = id / kPerRow, chunk = id % kPerRow;
-      const uint4 gv = *reinterpret_cast<const uint4*>(cs + row * kRow + chunk * 8);
-      const uint4 uv = *reinterpret_cast<const uint4*>(cs + row * kRow + BN / 2 + chunk * 8);
-      const uint16_t* gb = reinterpret_cast<const uint16_t*>(&gv);
-      const uint16_t* ub = reinterpret_cast<const uint16_t*>(&uv);
-      uint4 o;
-      uint16_t* ob = reinterpret_cast<uint16_t*>(&o);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        T ge, ue;
-        ge.bits = gb[e];
-        ue.bits = ub[e];
-        ob[e] = slc::from_f32<T>(slc::swiglu_value<T>(slc::to_f32(ge), slc::to_f32(ue))).bits;
-      }
-      const int n = n0 + chunk * 8;
-      if (row < rows && n < N)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, o), ry,
-                                               static_cast<int>(row * y_rs + n) * 2, 0, 0);
-    }
-    return;
-  }
   if constexpr (VST) {
     // The loop ended on a barrier, so the LDS is free: wave-private staging
     // of its TM x TN tile as T, rows padded to keep 16-byte alignment.

@@ -4,9 +4,16 @@ slc_hip_decode_attention_noalloc keeps its split partials and counters in the
 library's own device array; its results must equal slc_hip_decode_attention's
 bit for bit (the same kernels), on consecutive calls that reuse the array, the
 second with a smaller input, and the call must make no device allocation.
+A fresh process makes its first no-alloc call inside a HIP graph capture and
+checks every replay against the workspace entry point.
 """
 
 from __future__ import annotations
+
+import subprocess
+import sys
+import textwrap
+from pathlib import Path
 
 import pytest
 import torch
@@ -82,3 +89,59 @@ def test_noalloc_rejects_before_any_device_call():
         *sizes, *strides, 0.125, 0, 0, None)
     assert status == -1
     assert "no-alloc scratch" in lib.slc_hip_last_error().decode()
+
+
+_CAPTURE_SCRIPT = textwrap.dedent("""
+    import sys
+    sys.path[:0] = [{root!r}, {pkg!r}, {tests!r}]
+    import torch
+    from helpers import generator
+    from stateful_llm_compiler_hip.backends import hip_decode_attention, hip_decode_attention_noalloc
+
+    gpu = torch.device("cuda:0")
+
+    def inputs(batch, capacity, seed):
+        g = generator(seed)
+        q = torch.randn(batch, 14, 1, 64, generator=g).bfloat16()
+        k = torch.randn(batch, capacity, 2, 64, generator=g).bfloat16()
+        v = torch.randn(batch, capacity, 2, 64, generator=g).bfloat16()
+        lengths = torch.randint(capacity // 2, capacity + 1, (batch,), generator=g)
+        return [t.to(gpu) for t in (q, k, v, lengths)]
+
+    for order in ("online", "exact"):
+        q, k, v, lengths = inputs(8, 2048, 7)
+        out = torch.empty_like(q)
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        # The first no-alloc call of this process (for order "online") is
+        # the one being captured: the scratch array's set-up runs inside the
+        # capture.
+        with torch.cuda.graph(graph, stream=stream):
+            hip_decode_attention_noalloc(q, k, v, lengths, None, out, scale=0.125, softmax_order=order)
+        torch.cuda.synchronize()
+        for replay in range(4):
+            if replay == 2:  # new contents in the captured input buffers
+                q2, k2, v2, l2 = inputs(8, 2048, 8 + replay)
+                q.copy_(q2); k.copy_(k2); v.copy_(v2); lengths.copy_(l2)
+            graph.replay()
+            torch.cuda.synchronize()
+            expected = hip_decode_attention(q, k, v, lengths, None, scale=0.125, softmax_order=order)
+            torch.cuda.synchronize()
+            # eager work between replays, as a serving loop has
+            _ = float(expected.float().abs().sum())
+            assert torch.equal(out.view(torch.int16), expected.view(torch.int16)), (order, replay)
+    print("capture ok", flush=True)
+""")
+
+
+@pytest.mark.gpu
+def test_noalloc_first_call_inside_graph_capture(gpu):
+    announce("decode noalloc: first call of a fresh process inside graph capture")
+    root = Path(__file__).resolve().parents[1]
+    script = _CAPTURE_SCRIPT.format(root=str(root), pkg=str(root / "llm-compiler_amd"),
+                                    tests=str(root / "tests"))
+    result = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True,
+                            timeout=300, cwd=str(root))
+    assert result.returncode == 0 and "capture ok" in result.stdout, (
+        result.stdout[-2000:] + result.stderr[-4000:])
