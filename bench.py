@@ -80,6 +80,8 @@ def cpu_baseline(seconds_budget: float = 20.0) -> dict:
         "value": round(gbs, 3),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
+        "cores_affinity": len(os.sched_getaffinity(0)),
+        "torch_threads": torch.get_num_threads(),
         "kind": "port",
         "sample": (
             f"oracle decode_attention (eager torch CPU, bf16), batch {sample_batch} "

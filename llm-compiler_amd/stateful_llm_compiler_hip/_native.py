@@ -11,6 +11,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
+from collections import OrderedDict
 from pathlib import Path
 
 import torch
@@ -240,7 +241,15 @@ class DeviceWorkspace:
         return buffer
 
 
-_stream_workspaces: dict[tuple[int, int], DeviceWorkspace] = {}
+# Workspaces of raw stream handles, least recently used first.  A server that
+# keeps creating streams would otherwise grow this without bound; past
+# MAX_STREAM_WORKSPACES the least recently used entry is dropped (its memory
+# returns to PyTorch's caching allocator, which reuses it in stream order).
+# A graph captured on a stream without an explicit workspace keeps using that
+# stream's workspace: callers that capture on more streams than the bound at
+# once pass their own DeviceWorkspace instead.
+MAX_STREAM_WORKSPACES = 64
+_stream_workspaces: "OrderedDict[tuple[int, int], DeviceWorkspace]" = OrderedDict()
 
 
 def stream_workspace(device: torch.device) -> DeviceWorkspace:
@@ -255,4 +264,8 @@ def stream_workspace(device: torch.device) -> DeviceWorkspace:
         if workspace is None:
             workspace = DeviceWorkspace(torch.device("cuda", index))
             _stream_workspaces[key] = workspace
+            while len(_stream_workspaces) > MAX_STREAM_WORKSPACES:
+                _stream_workspaces.popitem(last=False)
+        else:
+            _stream_workspaces.move_to_end(key)
     return workspace

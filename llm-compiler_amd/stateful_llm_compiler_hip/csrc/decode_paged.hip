@@ -257,6 +257,9 @@ extern "C" int slc_hip_paged_kv_store(
   const int64_t u = 16 / es;  // elements per 16-byte unit
   const int64_t row_units = row_bytes / 16;
   const int64_t total = batch * heads * tokens * row_units;
+  SLC_REQUIRE(slc_host::ceil_div(total, 256) <= INT32_MAX,
+              "slc_hip_paged_kv_store: %lld rows of 16-byte units exceed one launch's grid",
+              (long long)total);
   hipLaunchKernelGGL(paged_kv_store_kernel, dim3(static_cast<unsigned>(slc_host::ceil_div(total, 256))),
                      dim3(256), 0, static_cast<hipStream_t>(stream), static_cast<uint4*>(key_pool),
                      static_cast<uint4*>(value_pool), block_table, table_stride_b, shift,

@@ -19,6 +19,7 @@ PyTorch.
 from __future__ import annotations
 
 import re
+import weakref
 from dataclasses import dataclass, replace
 from typing import Any, Callable, Sequence
 
@@ -419,6 +420,11 @@ class PagedKVCacheState(PreallocatedKVCacheState):
     gives the contiguous state's result bit for bit.  The model's decode step
     (RoPE, store, advance, attention) runs as one paged kernel like the
     contiguous one; RoPE + store alone runs as two kernels.
+
+    One stream per state: every version of a state shares one device
+    workspace (arrival counters, split partials), so the state's kernels
+    must run in order on one stream (or inside one captured graph).  The
+    block table is checked once at construction (device and entry range).
     """
 
     block_table: torch.Tensor | None = None
@@ -442,6 +448,30 @@ class PagedKVCacheState(PreallocatedKVCacheState):
                 raise ExecutionError("KV pools must be equal-shaped pages x page_tokens x H x D tensors")
             if lengths.shape != (table.shape[0],) or lengths.dtype != torch.int64:
                 raise ExecutionError("KV lengths must be an int64 [B] tensor")
+        self._check_block_table(table, self.keys[0])
+
+    # Tables already checked against a pool size (every state version of one
+    # sequence set shares its table, so the host read happens once).
+    # id(table) -> (weak reference, pool pages); not a field (no annotation).
+    _checked_tables = {}
+
+    @classmethod
+    def _check_block_table(cls, table: torch.Tensor, pool: torch.Tensor) -> None:
+        """The kernels take every entry as a raw pool page index: check once,
+        on the host, that the table lives with the pools and that every entry
+        is in [0, pool pages)."""
+
+        if table.device != pool.device:
+            raise ExecutionError("the block table must be on the KV pools' device")
+        pages = pool.shape[0]
+        seen = cls._checked_tables.get(id(table))
+        if seen is not None and seen[0]() is table and seen[1] == pages:
+            return
+        if table.numel() and (int(table.min()) < 0 or int(table.max()) >= pages):
+            raise ExecutionError(f"block table entries must be pool page indices in [0, {pages})")
+        key = id(table)
+        cls._checked_tables[key] = (weakref.ref(table, lambda _, key=key: cls._checked_tables.pop(key, None)),
+                                    pages)
 
     @classmethod
     def empty_from_key_template(
@@ -775,11 +805,25 @@ class HipExecutor:
                 "op": "decode_attention", "backend": "hip", "variant": choice.variant,
                 "source": choice.source, "size": choice.size, "estimated_us": choice.estimated_us,
             })
+        order = str(attributes.get("softmax_order", "online"))
+        self._trace_order(order, mask, query)
         return state.decode_attention(
             int(attributes.get("slot", 0)), query, mask, groups=int(attributes["groups"]),
-            scale=float(attributes["scale"]),
-            softmax_order=str(attributes.get("softmax_order", "online")), split_tokens=split,
+            scale=float(attributes["scale"]), softmax_order=order, split_tokens=split,
         )
+
+    def _trace_order(self, requested: str, mask, query) -> None:
+        """Record a softmax order the kernel cannot honour: the exact order
+        holds each lane's scores in LDS, so masks longer than
+        exact_max_tokens run the online order instead."""
+
+        ran = attention_order(requested, mask.shape[-1], query)
+        if ran != requested:
+            self.lowering_trace.append({
+                "op": "decode_attention", "backend": "hip", "softmax_order": ran,
+                "requested_softmax_order": requested, "mask_len": int(mask.shape[-1]),
+                "reason": f"exact order takes at most {exact_max_tokens(query.shape[-1], query.dtype)} tokens",
+            })
 
     @staticmethod
     def _kv_store(operands, attributes):
@@ -839,8 +883,7 @@ class HipExecutor:
             return state.rope_store_advance(slot, query, key, value, cosine, sine, delta=delta)
         return state.rope_store(slot, query, key, value, cosine, sine, positions)
 
-    @staticmethod
-    def _rope_store_attention(operands, attributes):
+    def _rope_store_attention(self, operands, attributes):
         if len(operands) != 8 or not isinstance(operands[0], PreallocatedKVCacheState):
             raise ExecutionError(
                 "kernel.hip.rope_store_attention takes state, q, k, v, cos, sin, positions, mask"
@@ -850,10 +893,12 @@ class HipExecutor:
             raise ExecutionError("kernel.hip.rope_store_attention head dim mismatch")
         # positions is this slot's length tensor and the advance is one token
         # (the fusion pass checks both).
+        order = str(attributes.get("softmax_order", "online"))
+        self._trace_order(order, mask, query)
         return state.rope_store_attention(
             int(attributes.get("slot", 0)), query, key, value, cosine, sine, mask,
             groups=int(attributes["groups"]), scale=float(attributes["scale"]),
-            softmax_order=str(attributes.get("softmax_order", "online")),
+            softmax_order=order,
         )
 
     @staticmethod

@@ -434,3 +434,31 @@ def test_linear_tile_plan_follows_rows_and_reaches_the_wrapper(monkeypatch):
     executor._linear([torch.zeros(32768, 896), w], {"has_bias": False})
     assert seen == ["t32x64", "t64x64", "auto"]
     assert [(t["variant"], t["rows"]) for t in executor.lowering_trace] == [("t32x64", 128), ("t64x64", 32768)]
+
+
+def test_exact_order_downgrade_is_traced():
+    """A decode attention whose IR asks for the exact softmax order over a
+    mask longer than the kernel's exact limit runs the online order, and the
+    lowering trace says so."""
+
+    import torch
+
+    from stateful_llm_compiler_hip import execution
+
+    seen = {}
+
+    class RecordingState(execution.PreallocatedKVCacheState):
+        def decode_attention(self, slot, query, mask, **kwargs):
+            seen["order"] = kwargs["softmax_order"]
+            return query
+
+    state = object.__new__(RecordingState)
+    executor = execution.HipExecutor()
+    query = torch.zeros(2, 14, 1, 64, dtype=torch.bfloat16)
+    attrs = {"groups": 7, "scale": 0.125, "softmax_order": "exact"}
+    executor._decode_attention([state, query, torch.zeros(2, 1, 1, 1024)], attrs)
+    assert executor.lowering_trace == []
+    executor._decode_attention([state, query, torch.zeros(2, 1, 1, 8192)], attrs)
+    entry = executor.lowering_trace[-1]
+    assert entry["softmax_order"] == "online" and entry["requested_softmax_order"] == "exact"
+    assert entry["mask_len"] == 8192

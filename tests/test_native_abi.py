@@ -113,3 +113,33 @@ def test_fused_entry_points_decline_or_reject_before_any_device_call():
     sizes_long = [4, 14, 2, 64, 8192, 8192]
     assert lib.slc_hip_rope_decode_attention(*args, bf16, *sizes_long, *strides, 0.125, 1, None) == -2
     assert lib.slc_hip_rope_decode_attention(*args, bf16, *sizes, *strides, 0.125, 7, None) == -1
+
+
+def test_paged_kv_store_rejects_a_grid_past_one_launch():
+    # 2^43 16-byte units need 2^35 workgroups of 256, past a launch: rejected on
+    # the host (the pointers are never dereferenced).
+    lib = _native.library()
+    fake = 1 << 20
+    batch, heads, tokens, head_dim = 1 << 16, 512, 1 << 15, 64  # x 8 units per row
+    status = lib.slc_hip_paged_kv_store(
+        fake, fake, fake, 64, 64, 16, 16 * heads * head_dim, heads * head_dim, head_dim,
+        fake, fake, fake, None, _native.SLC_BF16, batch, heads, tokens, head_dim,
+        heads * tokens * head_dim, tokens * head_dim, head_dim,
+        heads * tokens * head_dim, tokens * head_dim, head_dim, None)
+    assert status == -1
+    assert b"exceed one launch's grid" in lib.slc_hip_last_error()
+
+
+def test_stream_workspaces_are_bounded(monkeypatch):
+    # The per-stream workspace cache keeps the most recently used streams
+    # only (no device memory is touched: workspaces allocate lazily).
+    import torch
+
+    handles = iter(range(1000, 2000))
+    monkeypatch.setattr(_native, "current_stream", lambda device: next(handles))
+    monkeypatch.setattr(_native, "_stream_workspaces", type(_native._stream_workspaces)())
+    first = _native.stream_workspace(torch.device("cuda", 0))
+    for _ in range(_native.MAX_STREAM_WORKSPACES + 10):
+        _native.stream_workspace(torch.device("cuda", 0))
+    assert len(_native._stream_workspaces) == _native.MAX_STREAM_WORKSPACES
+    assert first not in _native._stream_workspaces.values()

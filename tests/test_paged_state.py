@@ -28,6 +28,8 @@ def _state(batch=2, pages=4, page_tokens=16, heads=2, dim=8, num_pages=None, tab
     ({"page_tokens": 8}, "power of two"),
     ({"table": torch.zeros(2, 3, dtype=torch.int32)}, "capacity / page_tokens"),
     ({"table": torch.zeros(2, 4, dtype=torch.int64)}, "int32"),
+    ({"table": torch.tensor([[0, 1, 2, 3], [4, 5, 6, 8]], dtype=torch.int32)}, r"\[0, 8\)"),
+    ({"table": torch.tensor([[0, 1, 2, 3], [4, -1, 6, 7]], dtype=torch.int32)}, "pool page indices"),
 ])
 def test_paged_state_rejects_bad_geometry(kwargs, needle):
     with pytest.raises(ExecutionError, match=needle):
