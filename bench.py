@@ -276,7 +276,8 @@ def bench_kernels() -> dict:
     the roofline that bounds it (bf16; synthetic N(0,1) data)."""
 
     from stateful_llm_compiler_hip.backends import (
-        hip_kv_store, hip_linear, hip_prefill_attention, hip_rms_norm, hip_rope,
+        hip_kv_store, hip_linear, hip_prefill_attention, hip_prefill_mask_tiles, hip_rms_norm,
+        hip_rope,
     )
 
     dev = torch.device("cuda:0")
@@ -303,9 +304,14 @@ def bench_kernels() -> dict:
     us = _time_graph(lambda: hip_prefill_attention(q, k, v, None, scale=D**-0.5, causal=True), reps=5)
     mfma("prefill_attention_causal", us, flops, "B8 QH14 KVH2 T4096 D64")
     mask = torch.zeros(T, T, device=dev, dtype=bf).masked_fill(
-        torch.ones(T, T, device=dev, dtype=torch.bool).triu(1), float("-inf")).expand(B, 1, T, T)
-    us = _time_graph(lambda: hip_prefill_attention(q, k, v, mask, scale=D**-0.5), reps=5)
+        torch.ones(T, T, device=dev, dtype=torch.bool).triu(1), float("-inf")).expand(B, 1, T, T).contiguous()
+    # The mask's tile classes are computed once per mask (the model's 24
+    # layers share one), then every attention call uses them.
+    tiles = hip_prefill_mask_tiles(mask)
+    us = _time_graph(lambda: hip_prefill_attention(q, k, v, mask, scale=D**-0.5, mask_tiles=tiles), reps=5)
     mfma("prefill_attention_mask", us, flops, "B8 QH14 KVH2 T4096 D64, explicit [B,1,T,T] causal mask")
+    us = _time_graph(lambda: hip_prefill_mask_tiles(mask), reps=5)
+    hbm("prefill_mask_tiles", us, B * T * T * 2, "B8 T4096 bf16 [B,1,T,T] mask, classes per 64x64 tile")
     del q, k, v, mask
 
     # linear: the four projection shapes at M = 4096 and the MLP at M = 32768

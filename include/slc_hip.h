@@ -385,6 +385,37 @@ SLC_API int slc_hip_prefill_attention(
     int softmax_order, void* stream);
 
 /*
+ * prefill_attention_classes: slc_hip_prefill_attention with the mask's tile
+ * classes from slc_hip_prefill_mask_tiles (or NULL: every tile loads its
+ * mask).  Tiles of class 0 are not visited (no K/V or mask traffic), class 1
+ * applies the causal pattern from the indices, class 2 loads and adds the
+ * mask tile; the result equals adding the whole mask.  The reference loops
+ * over every key tile and reads the whole mask
+ * (backends/triton_prefill_attention.py:69); this is the same operation.
+ */
+SLC_API int slc_hip_prefill_attention_classes(
+    const void* query, const void* key, const void* value, const void* mask,
+    int mask_dtype, const unsigned char* mask_tile_classes, void* output, int dtype,
+    int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t tokens, int64_t head_dim,
+    int causal, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh,
+    int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t m_sb, int64_t m_sq,
+    int64_t m_sk, int64_t o_sb, int64_t o_sh, int64_t o_st, float scale,
+    int softmax_order, void* stream);
+
+/*
+ * prefill_mask_tiles: classify an additive [B, 1, T, T] mask (strides m_sb,
+ * m_sq, m_sk in elements) per (batch, 64-query block, 64-key tile) into
+ * classes[B][ceil(T/64)][ceil(T/64)]: 0 = every entry -inf, 1 = +0 where
+ * key <= query and -inf above (the causal pattern), 2 = anything else.
+ * prefill_mask_tile_count gives the number of class bytes.  (Supports
+ * serve.prefill_attention, execution.py:707-739; no reference counterpart.)
+ */
+SLC_API int64_t slc_hip_prefill_mask_tile_count(int64_t batch, int64_t tokens);
+SLC_API int slc_hip_prefill_mask_tiles(const void* mask, int mask_dtype, int64_t batch,
+                                       int64_t tokens, int64_t m_sb, int64_t m_sq,
+                                       int64_t m_sk, unsigned char* classes, void* stream);
+
+/*
  * Ops that complete a Qwen2 step without eager PyTorch kernels.  None has a
  * separate reference kernel: the reference runs them as PyTorch ops
  * (execution.py:500-528 handler table; qwen2.py model code cited per op).

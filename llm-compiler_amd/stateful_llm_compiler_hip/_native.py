@@ -122,6 +122,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I,
         [_P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _I, _P],
     ),
+    "slc_hip_prefill_attention_classes": (
+        _I,
+        [_P, _P, _P, _P, _I, _P, _P, _I, _L, _L, _L, _L, _L, _I] + [_L] * 15 + [_F, _I, _P],
+    ),
+    "slc_hip_prefill_mask_tile_count": (_L, [_L, _L]),
+    "slc_hip_prefill_mask_tiles": (_I, [_P, _I, _L, _L, _L, _L, _L, _P, _P]),
     "slc_hip_prefill_attention": (
         _I,
         [_P, _P, _P, _P, _I, _P, _I, _L, _L, _L, _L, _L, _I] + [_L] * 15 + [_F, _I, _P],

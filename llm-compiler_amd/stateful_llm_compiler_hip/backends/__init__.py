@@ -22,7 +22,7 @@ from .hip_ops import (
     hip_rope_table,
     hip_swiglu,
 )
-from .hip_prefill_attention import hip_prefill_attention
+from .hip_prefill_attention import hip_prefill_attention, hip_prefill_mask_tiles
 from .hip_rmsnorm import hip_rms_norm
 from .hip_rope import hip_rope
 
@@ -46,6 +46,7 @@ __all__ = [
     "hip_paged_rope_decode_attention",
     "hip_linear",
     "hip_prefill_attention",
+    "hip_prefill_mask_tiles",
     "hip_rms_norm",
     "hip_rope",
 ]

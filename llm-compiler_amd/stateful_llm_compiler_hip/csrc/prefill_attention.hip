@@ -371,6 +371,68 @@ __global__ __launch_bounds__(256) void prefill_attention_generic_kernel(
 }
 
 
+// ---- mask tile classes ---------------------------------------------------------
+// One byte per (batch, 64-query block, 64-key tile) of an explicit [B, 1, T, T]
+// mask, so the grouped kernel can leave out what the mask makes trivial:
+//   0 (dead)   every entry is -inf: the tile adds nothing to any row (the
+//              part of a causal mask past the diagonal); no K/V/mask loads.
+//   1 (causal) every entry is +0 where key <= query and -inf where key >
+//              query: the causal pattern, applied from the indices, so the
+//              tile's mask is not loaded.
+//   2          anything else: the mask tile is loaded and added.
+// Entries past T (a partial last tile) are not looked at; those keys are
+// invalid anyway.  Grid (key tiles, query blocks, batch), 256 threads.
+// VEC: unit key stride, 16-byte aligned rows and T a multiple of the 16-byte
+// chunk: each thread reads whole 16-byte chunks (2 KB per wave per load).
+template <int MK, bool VEC>
+__global__ __launch_bounds__(256) void mask_tile_class_kernel(const void* __restrict__ mask,
+                                                              unsigned char* __restrict__ classes,
+                                                              int tokens, int64_t m_sb, int64_t m_sq,
+                                                              int64_t m_sk) {
+  constexpr int ME = MK == SLC_F32 + 1 ? 4 : 2;
+  constexpr uint32_t kNinf = ME == 4 ? 0xff800000u : (MK == SLC_BF16 + 1 ? 0xff80u : 0xfc00u);
+  const int k0 = blockIdx.x * 64, q0 = blockIdx.y * 64;
+  const int64_t b = blockIdx.z;
+  const unsigned char* base = static_cast<const unsigned char*>(mask) + b * m_sb * ME;
+  bool live = false, general = false;
+  auto check = [&](uint32_t bits, int q, int key) {
+    live |= bits != kNinf;
+    general |= key <= q ? bits != 0u : bits != kNinf;
+  };
+  if constexpr (VEC) {
+    constexpr int kPer = 16 / ME;              // elements per chunk
+    constexpr int kChunksRow = 64 / kPer;      // chunks per tile row
+    for (int id = threadIdx.x; id < 64 * kChunksRow; id += 256) {
+      const int r = id / kChunksRow, key = k0 + (id % kChunksRow) * kPer;
+      const int q = q0 + r;
+      if (q >= tokens || key >= tokens) continue;  // T is a multiple of kPer
+      const uint4 v = *reinterpret_cast<const uint4*>(base + (static_cast<int64_t>(q) * m_sq + key) * ME);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) {
+        const uint32_t bits = ME == 4 ? w[e] : (w[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+        check(bits, q, key + e);
+      }
+    }
+  } else {
+    // Thread t: key column k0 + t % 64, query rows q0 + t / 64 + 4i.
+    const int key = k0 + (threadIdx.x & 63);
+    if (key < tokens) {
+      for (int r = threadIdx.x >> 6; r < 64 && q0 + r < tokens; r += 4) {
+        const int q = q0 + r;
+        const unsigned char* p = base + (static_cast<int64_t>(q) * m_sq + static_cast<int64_t>(key) * m_sk) * ME;
+        check(ME == 4 ? *reinterpret_cast<const uint32_t*>(p) : *reinterpret_cast<const uint16_t*>(p), q, key);
+      }
+    }
+  }
+  const bool any_live = __syncthreads_or(live);
+  const bool any_general = __syncthreads_or(general);
+  if (threadIdx.x == 0) {
+    const int64_t nqb = gridDim.y, nkt = gridDim.x;
+    classes[(b * nqb + blockIdx.y) * nkt + blockIdx.x] = !any_live ? 0 : (any_general ? 2 : 1);
+  }
+}
+
 // ---- grouped-head kernel (v2) ------------------------------------------------
 // A workgroup owns 64 queries of ALL the query heads of one KV head (GQA
 // group G): G compute waves (one query head each, 64 queries = 4 MFMA column
@@ -388,6 +450,8 @@ __global__ __launch_bounds__(256) void prefill_attention_generic_kernel(
 //    it to the consumers, then the producer refills the ring slot consumers
 //    released at that barrier.
 constexpr int kV2Queries = 64;
+// Longest key range (in 64-key tiles) the tile-class list covers: T <= 65536.
+constexpr int kMaxClassTiles = 1024;
 // Two ring stages: the producer refills one stage while the consumers read
 // the other (measured 2-3 % faster than three stages, equal to four).
 constexpr int kV2Stages = 2;
@@ -439,12 +503,16 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
     const void* __restrict__ mask, T* __restrict__ output, int tokens, int kv_heads,
     int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh, int64_t k_st,
     int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t m_sb, int64_t m_sq, int64_t o_sb,
-    int64_t o_sh, int64_t o_st, float scale) {
+    int64_t o_sh, int64_t o_st, float scale, const unsigned char* __restrict__ tile_class) {
   using M = Mfma<T>;
   constexpr int ME = mask_elem_bytes<MK>();
   constexpr int kMaskRow = kKeys * ME;                 // bytes of one mask tile row
   constexpr int kMaskTile = kV2Queries * kMaskRow;
   __shared__ __attribute__((aligned(16))) unsigned char ring[kV2Stages][stage_bytes<MK>()];
+  // With tile classes (MK != 0): the key tiles this query block visits, in
+  // order, bit 15 set where the mask tile is loaded (class 2), and their count.
+  __shared__ uint16_t live_tiles[MK != 0 ? kMaxClassTiles : 1];
+  __shared__ int live_count;
 
   // Grid (KV heads, batch, query blocks): workgroups dispatch in that
   // order, and the last query blocks go first.  Under the causal flag (or a
@@ -466,8 +534,31 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
   // is the reference's fp32 score itself (scaled, mask added).
   const float c_log2 = POW2 && MK == 0 ? scale * kLog2e : kLog2e;
   const int key_end = CAUSAL ? min(q0 + kV2Queries, tokens) : tokens;
-  const int ntiles = (key_end + kKeys - 1) / kKeys;
+  const int all_tiles = (key_end + kKeys - 1) / kKeys;
+  const bool classed = MK != 0 && tile_class != nullptr;
+  if (classed && wave == G) {
+    // The producer lists the live tiles (class != 0) before the first barrier.
+    const unsigned char* row = tile_class + (b * nqb + qblk) * static_cast<int64_t>((tokens + kKeys - 1) / kKeys);
+    int count = 0;
+    for (int base = 0; base < all_tiles; base += 64) {
+      const int t = base + lane;
+      const int cls = t < all_tiles ? row[t] : 0;
+      const uint64_t mask_live = __ballot(cls != 0);
+      const int before = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask_live >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask_live), 0));
+      if (cls != 0) live_tiles[count + before] = static_cast<uint16_t>(t | (cls == 2 ? 0x8000 : 0));
+      count += __popcll(mask_live);
+    }
+    if (lane == 0) live_count = count;
+  }
+  if constexpr (MK != 0) {
+    if (classed) __syncthreads();  // the list is ready (the producer matches it)
+  }
+  const int ntiles = classed ? live_count : all_tiles;
   const int nsteps = EXACT ? 2 * ntiles : ntiles;  // ring steps (tile visits)
+  // Key tile of list entry i, and whether its mask tile is loaded.
+  auto tile_of = [&](int i) { return classed ? (live_tiles[i] & 0x7fff) : i; };
+  auto mask_of = [&](int i) { return !classed || (live_tiles[i] & 0x8000) != 0; };
 
   if (wave == G) {
     // ---- producer ---------------------------------------------------------
@@ -481,10 +572,13 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
     // with the global 16-byte chunk (L%8) ^ (row & 7) of that row.
     auto issue = [&](int step, int stage) {
       unsigned char* dst = ring[stage];
-      const int tile = EXACT && step >= ntiles ? step - ntiles : step;
+      const int entry = EXACT && step >= ntiles ? step - ntiles : step;
+      const bool in_range = step < nsteps;
+      const int tile = in_range ? tile_of(entry) : 0;
       const bool want_v = !EXACT || step >= ntiles;
+      const bool want_mask = in_range && mask_of(entry);
       const int k0 = tile * kKeys;
-      const int rows = step < nsteps ? min(kKeys, tokens - k0) : 0;
+      const int rows = in_range ? min(kKeys, tokens - k0) : 0;
       const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + static_cast<int64_t>(k0) * k_st * 2,
                                                   rows > 0 ? (static_cast<int64_t>(rows) - 1) * k_st * 2 + kRowBytes : 0);
       const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + static_cast<int64_t>(k0) * v_st * 2,
@@ -499,7 +593,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
       if constexpr (MK != 0) {
         // Mask rows are queries, chunks 8 keys; whole rows stay inside the
         // [T, T] plane (keys past T are masked as invalid anyway).
-        const int64_t bytes = step < nsteps && q_rows > 0
+        const int64_t bytes = want_mask && q_rows > 0
                                   ? ((static_cast<int64_t>(q_rows) - 1) * m_sq + tokens - k0) * ME
                                   : 0;
         const __amdgpu_buffer_rsrc_t rm = make_rsrc(mbase + static_cast<int64_t>(k0) * ME, bytes);
@@ -572,7 +666,11 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
   for (int step = 0; step < nsteps; ++step) {
     __syncthreads();  // tile of this step is in ring[step % kStages]
     const bool pass2 = EXACT && step >= ntiles;
-    const int t = pass2 ? step - ntiles : step;
+    const int entry = pass2 ? step - ntiles : step;
+    const int t = tile_of(entry);
+    // A class-1 tile: its mask is the causal pattern, applied from indices.
+    const bool tile_mask = MK != 0 && mask_of(entry);
+    const bool causal_tile = CAUSAL || (MK != 0 && !tile_mask);
     if (EXACT && step == ntiles) {
       // Pass 1 done: row sums over the 4 lane groups, then the shift.
 #pragma unroll
@@ -590,7 +688,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
     const unsigned char* vt = kt + kV2TileBytes;
     const unsigned char* mt = kt + 2 * kV2TileBytes;  // mask tile, rows = queries
     const int k0 = t * kKeys;
-    if constexpr (MK != 0) {
+    if (MK != 0 && tile_mask) {
       // A mask tile that is -inf throughout (the part of a causal mask past
       // the diagonal) adds exp2(-inf) = 0 to every sum and no new maximum:
       // the tile is skipped (for finite scores the result is bit-identical;
@@ -641,7 +739,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
     }
 
     // Scores with the mask and validity (fp32, as the reference's fused kernel).
-    const bool full = !CAUSAL ? k0 + kKeys <= tokens : k0 + kKeys <= q0 && k0 + kKeys <= tokens;
+    const bool full = !causal_tile ? k0 + kKeys <= tokens : k0 + kKeys <= q0 && k0 + kKeys <= tokens;
 #pragma unroll
     for (int qb = 0; qb < 4; ++qb) {
       const int my_query = q0 + 16 * qb + c;
@@ -649,7 +747,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
         float mv[4] = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (MK != 0) {
+        if (MK != 0 && tile_mask) {
           // Mask of keys 16kb + 4g .. +3 for this lane's query row.
           const int row = 16 * qb + c;
           const int byte = (16 * kb + 4 * g) * ME;
@@ -709,7 +807,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
         // relative to the lane's first key).
         asm volatile("" ::: "memory");
         int last = tokens - 1 - k0 - 4 * g;
-        if constexpr (CAUSAL) last = min(last, my_query - k0 - 4 * g);
+        if (causal_tile) last = min(last, my_query - k0 - 4 * g);
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
@@ -792,9 +890,12 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
   for (int qb = 0; qb < 4; ++qb) {
     const int my_query = q0 + 16 * qb + c;
     if (my_query < tokens) {
-      // EXACT: the terms were normalised already (a NaN shift made an empty
-      // row NaN).
-      const float inv = EXACT ? 1.0f : 1.0f / acc[4][qb][0];
+      // EXACT: the terms were normalised already.  An empty row (every key
+      // masked) is NaN, as the reference's softmax over an all -inf row: its
+      // shift is NaN, or no tile was visited at all (every tile of the block
+      // masked out) -- then even pass 2's terms never ran.
+      const bool empty = ntiles == 0 || shift[qb] != shift[qb];
+      const float inv = EXACT ? (empty ? __builtin_nanf("") : 1.0f) : 1.0f / acc[4][qb][0];
       T* op = output + b * o_sb + h * o_sh + static_cast<int64_t>(my_query) * o_st;
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
@@ -813,7 +914,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
 template <typename T, int G, int MK, bool CAUSAL>
 int launch_v2(const void* q, const void* k, const void* v, const void* mask, void* out,
               int64_t batch, int tokens, int kv_heads, const int64_t* st, float scale,
-              bool exact, hipStream_t stream) {
+              bool exact, const unsigned char* classes, hipStream_t stream) {
   const dim3 grid(kv_heads, static_cast<unsigned>(batch), (tokens + kV2Queries - 1) / kV2Queries);
   int exponent = 0;
   const bool pow2 = std::is_same_v<T, slc::bf16_t> && std::frexp(scale, &exponent) == 0.5f &&
@@ -826,17 +927,18 @@ int launch_v2(const void* q, const void* k, const void* v, const void* mask, voi
                      stream, static_cast<const T*>(q), static_cast<const T*>(k),
                      static_cast<const T*>(v), mask, static_cast<T*>(out), tokens, kv_heads,
                      st[0], st[1], st[2], st[3], st[4], st[5], st[6], st[7], st[8], st[9], st[10],
-                     st[12], st[13], st[14], scale);
+                     st[12], st[13], st[14], scale, MK != 0 ? classes : nullptr);
   return slc_host::check_launch("slc_hip_prefill_attention(grouped)");
 }
 
 template <typename T, int G>
 int dispatch_v2(const void* q, const void* k, const void* v, const void* mask, int mask_dtype,
                 void* out, int64_t batch, int tokens, int kv_heads, int causal,
-                const int64_t* st, float scale, bool exact, hipStream_t s) {
+                const int64_t* st, float scale, bool exact, const unsigned char* classes,
+                hipStream_t s) {
 #define SLC_V2(MKV)                                                                       \
-  return causal ? launch_v2<T, G, MKV, true>(q, k, v, mask, out, batch, tokens, kv_heads, st, scale, exact, s) \
-                : launch_v2<T, G, MKV, false>(q, k, v, mask, out, batch, tokens, kv_heads, st, scale, exact, s)
+  return causal ? launch_v2<T, G, MKV, true>(q, k, v, mask, out, batch, tokens, kv_heads, st, scale, exact, classes, s) \
+                : launch_v2<T, G, MKV, false>(q, k, v, mask, out, batch, tokens, kv_heads, st, scale, exact, classes, s)
   if (mask == nullptr) SLC_V2(0);
   if (mask_dtype == SLC_BF16) SLC_V2(SLC_BF16 + 1);
   if (mask_dtype == SLC_F16) SLC_V2(SLC_F16 + 1);
@@ -847,13 +949,13 @@ int dispatch_v2(const void* q, const void* k, const void* v, const void* mask, i
 template <typename T>
 int try_v2(const void* q, const void* k, const void* v, const void* mask, int mask_dtype,
            void* out, int64_t batch, int tokens, int kv_heads, int groups, int causal,
-           const int64_t* st, float scale, bool exact, hipStream_t s) {
+           const int64_t* st, float scale, bool exact, const unsigned char* c, hipStream_t s) {
   switch (groups) {
-    case 1: return dispatch_v2<T, 1>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, exact, s);
-    case 2: return dispatch_v2<T, 2>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, exact, s);
-    case 4: return dispatch_v2<T, 4>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, exact, s);
-    case 7: return dispatch_v2<T, 7>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, exact, s);
-    default: return dispatch_v2<T, 8>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, exact, s);
+    case 1: return dispatch_v2<T, 1>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, exact, c, s);
+    case 2: return dispatch_v2<T, 2>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, exact, c, s);
+    case 4: return dispatch_v2<T, 4>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, exact, c, s);
+    case 7: return dispatch_v2<T, 7>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, exact, c, s);
+    default: return dispatch_v2<T, 8>(q, k, v, mask, mask_dtype, out, batch, tokens, kv_heads, causal, st, scale, exact, c, s);
   }
 }
 
@@ -916,12 +1018,12 @@ int launch_generic(const void* q, const void* k, const void* v, const void* mask
 
 }  // namespace
 
-extern "C" int slc_hip_prefill_attention(
+extern "C" int slc_hip_prefill_attention_classes(
     const void* query, const void* key, const void* value, const void* mask,
-    int mask_dtype, void* output, int dtype, int64_t batch, int64_t q_heads,
-    int64_t kv_heads, int64_t tokens, int64_t head_dim, int causal, int64_t q_sb,
-    int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh, int64_t k_st,
-    int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t m_sb, int64_t m_sq,
+    int mask_dtype, const unsigned char* mask_tile_classes, void* output, int dtype,
+    int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t tokens, int64_t head_dim,
+    int causal, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh,
+    int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t m_sb, int64_t m_sq,
     int64_t m_sk, int64_t o_sb, int64_t o_sh, int64_t o_st, float scale,
     int softmax_order, void* stream) {
   SLC_REQUIRE(slc_host::is_float_dtype(dtype), "slc_hip_prefill_attention: bad dtype %d", dtype);
@@ -966,11 +1068,16 @@ extern "C" int slc_hip_prefill_attention(
   // scale.
   if (mfma_ok && group_ok && mask_ok && out_ok && kv_heads <= 65535 && kUseGrouped &&
       scale > 0.0f) {
+    // The class list covers up to kMaxClassTiles key tiles.
+    const unsigned char* classes =
+        mask != nullptr && (tokens + kKeys - 1) / kKeys <= kMaxClassTiles ? mask_tile_classes : nullptr;
     if (dtype == SLC_BF16)
       return try_v2<slc::bf16_t>(query, key, value, mask, mask_dtype, output, batch, T_,
-                                 static_cast<int>(kv_heads), groups, causal, st, scale, exact, s);
+                                 static_cast<int>(kv_heads), groups, causal, st, scale, exact,
+                                 classes, s);
     return try_v2<slc::f16_t>(query, key, value, mask, mask_dtype, output, batch, T_,
-                              static_cast<int>(kv_heads), groups, causal, st, scale, exact, s);
+                              static_cast<int>(kv_heads), groups, causal, st, scale, exact,
+                              classes, s);
   }
   // The single-head MFMA kernel has only the online order; the exact order
   // of shapes the grouped kernel does not take runs on the generic kernel.
@@ -996,4 +1103,64 @@ extern "C" int slc_hip_prefill_attention(
                                         static_cast<int>(q_heads), groups,
                                         static_cast<int>(head_dim), causal, st, scale, exact, s);
   }
+}
+
+extern "C" int slc_hip_prefill_attention(
+    const void* query, const void* key, const void* value, const void* mask,
+    int mask_dtype, void* output, int dtype, int64_t batch, int64_t q_heads,
+    int64_t kv_heads, int64_t tokens, int64_t head_dim, int causal, int64_t q_sb,
+    int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    int64_t v_sb, int64_t v_sh, int64_t v_st, int64_t m_sb, int64_t m_sq,
+    int64_t m_sk, int64_t o_sb, int64_t o_sh, int64_t o_st, float scale,
+    int softmax_order, void* stream) {
+  return slc_hip_prefill_attention_classes(query, key, value, mask, mask_dtype, nullptr, output,
+                                           dtype, batch, q_heads, kv_heads, tokens, head_dim,
+                                           causal, q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh,
+                                           v_st, m_sb, m_sq, m_sk, o_sb, o_sh, o_st, scale,
+                                           softmax_order, stream);
+}
+
+extern "C" int64_t slc_hip_prefill_mask_tile_count(int64_t batch, int64_t tokens) {
+  if (batch < 0 || tokens < 0) return -1;
+  const int64_t tiles = (tokens + kKeys - 1) / kKeys;
+  return batch * tiles * tiles;
+}
+
+extern "C" int slc_hip_prefill_mask_tiles(const void* mask, int mask_dtype, int64_t batch,
+                                          int64_t tokens, int64_t m_sb, int64_t m_sq,
+                                          int64_t m_sk, unsigned char* classes, void* stream) {
+  SLC_REQUIRE(slc_host::is_float_dtype(mask_dtype), "slc_hip_prefill_mask_tiles: bad mask dtype %d",
+              mask_dtype);
+  SLC_REQUIRE(batch >= 0 && tokens >= 0 && batch <= 65535 && tokens < (1LL << 30),
+              "slc_hip_prefill_mask_tiles: bad sizes");
+  if (batch == 0 || tokens == 0) return SLC_OK;
+  SLC_REQUIRE(mask != nullptr && classes != nullptr, "slc_hip_prefill_mask_tiles: null pointer");
+  const int64_t tiles = (tokens + kKeys - 1) / kKeys;
+  SLC_REQUIRE(tiles <= 65535, "slc_hip_prefill_mask_tiles: too many tiles for the grid");
+  const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(tiles), static_cast<unsigned>(batch));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int T_ = static_cast<int>(tokens);
+  const int64_t me = slc_host::dtype_size(mask_dtype);
+  const bool vec = m_sk == 1 && (reinterpret_cast<uintptr_t>(mask) & 15) == 0 && (m_sq * me) % 16 == 0 &&
+                   (m_sb * me) % 16 == 0 && (tokens * me) % 16 == 0;
+#define SLC_CLASSES(MKV)                                                                          \
+  if (vec)                                                                                        \
+    hipLaunchKernelGGL((mask_tile_class_kernel<MKV, true>), grid, dim3(256), 0, s, mask, classes, \
+                       T_, m_sb, m_sq, m_sk);                                                     \
+  else                                                                                            \
+    hipLaunchKernelGGL((mask_tile_class_kernel<MKV, false>), grid, dim3(256), 0, s, mask, classes, \
+                       T_, m_sb, m_sq, m_sk)
+  switch (mask_dtype) {
+    case SLC_BF16:
+      SLC_CLASSES(SLC_BF16 + 1);
+      break;
+    case SLC_F16:
+      SLC_CLASSES(SLC_F16 + 1);
+      break;
+    default:
+      SLC_CLASSES(SLC_F32 + 1);
+      break;
+  }
+#undef SLC_CLASSES
+  return slc_host::check_launch("slc_hip_prefill_mask_tiles");
 }

@@ -41,6 +41,7 @@ from .backends import (
     hip_paged_kv_store,
     hip_paged_rope_decode_attention,
     hip_prefill_attention,
+    hip_prefill_mask_tiles,
     hip_rms_norm,
     hip_rope,
     hip_rope_kv_store,
@@ -665,6 +666,8 @@ class HipExecutor:
         self.strict = strict
         self.validate = validate
         self.lowering_trace: list[dict[str, Any]] = []
+        # id(mask) -> (mask, tile classes) for the run in progress.
+        self._mask_tiles: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
         self._handlers: dict[str, Callable[[list[Any], dict[str, Any]], Any]] = {
             "kernel.hip.rms_norm": self._rms_norm,
             "kernel.hip.linear": self._linear,
@@ -711,6 +714,7 @@ class HipExecutor:
             )
         environment: dict[str, Any] = {}
         symbols: dict[str, int] = {}
+        self._mask_tiles = {}
         for argument, value in zip(function.block.arguments, arguments):
             if self.validate:
                 validate_runtime_value(value, argument.type, symbols, context=f"argument {argument.name}")
@@ -731,6 +735,7 @@ class HipExecutor:
                 environment[ir_value.name] = runtime_value
             trace.append(operation.name)
         outputs = tuple(environment[v.name] for v in function.returns)
+        self._mask_tiles = {}
         return ExecutionResult(outputs, tuple(trace), dict(symbols))
 
     # -------------------------------------------------------------- kernels
@@ -778,18 +783,26 @@ class HipExecutor:
             raise ExecutionError("kernel.hip.rope head dim mismatch")
         return hip_rope(*operands)
 
-    @staticmethod
-    def _prefill_attention(operands, attributes):
+    def _prefill_attention(self, operands, attributes):
         if len(operands) != 4:
             raise ExecutionError("kernel.hip.prefill_attention takes query, key, value and mask")
         query, key, value, mask = operands
         groups = int(attributes["groups"])
         if query.shape[1] != key.shape[1] * groups:
             raise ExecutionError("kernel.hip.prefill_attention GQA groups do not match")
+        tiles = None
+        if mask is not None and mask.is_cuda:
+            # Every layer applies the function's one mask: classify it once
+            # per run (the entry keeps the mask alive, so its id is stable).
+            cached = self._mask_tiles.get(id(mask))
+            if cached is None or cached[0] is not mask:
+                cached = (mask, hip_prefill_mask_tiles(mask))
+                self._mask_tiles[id(mask)] = cached
+            tiles = cached[1]
         return hip_prefill_attention(
             query, key, value, mask, scale=float(attributes["scale"]),
             causal=attributes.get("causal") is True,
-            softmax_order=str(attributes.get("softmax_order", "online")),
+            softmax_order=str(attributes.get("softmax_order", "online")), mask_tiles=tiles,
         )
 
     def _decode_attention(self, operands, attributes):

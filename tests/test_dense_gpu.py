@@ -414,3 +414,100 @@ def test_linear_bf16_partial_tiles(gpu, m, n, k):
     y = hip_linear(x.to(gpu), w.to(gpu), b.to(gpu))
     torch.cuda.synchronize()
     _check_linear_bf16(y, x, w, b)
+
+
+# ------------------------------------------------ mask tile classes (prefill)
+
+
+def _class_masks(batch, tokens, dtype, seed):
+    """Masks whose tiles cover every class: the causal mask, a left-padded
+    causal mask (padding keys -inf for some rows), a block-sparse mask
+    (random -inf tiles among random values), and a causal mask written with
+    -0 in place of +0 (not the causal pattern bit for bit: class 2)."""
+
+    g = generator(seed)
+    future = torch.triu(torch.ones(tokens, tokens, dtype=torch.bool), diagonal=1)
+    causal = torch.zeros(batch, 1, tokens, tokens).masked_fill(future, float("-inf"))
+    padded = causal.clone()
+    for b in range(batch):
+        padded[b, :, :, : 37 * b] = float("-inf")
+    tiles = -(-tokens // 64)
+    dead = torch.rand(batch, tiles, tiles, generator=g) < 0.4
+    sparse = torch.randn(batch, 1, tokens, tokens, generator=g)
+    sparse = sparse.masked_fill(dead.repeat_interleave(64, 1).repeat_interleave(64, 2)[:, None, :tokens, :tokens],
+                                float("-inf"))
+    negzero = torch.full((batch, 1, tokens, tokens), -0.0).masked_fill(future, float("-inf"))
+    return {name: m.to(dtype) for name, m in
+            (("causal", causal), ("padded", padded), ("sparse", sparse), ("negzero", negzero))}
+
+
+def _classes_reference(mask: torch.Tensor) -> torch.Tensor:
+    """The class definition, restated on the host over the bit patterns."""
+
+    batch, _, tokens, _ = mask.shape
+    tiles = -(-tokens // 64)
+    width = {2: torch.int16, 4: torch.int32}[mask.element_size()]
+    bits = mask[:, 0].contiguous().view(width).long()
+    ninf = int(torch.tensor(float("-inf"), dtype=mask.dtype).view(width))
+    q = torch.arange(tokens).view(-1, 1)
+    k = torch.arange(tokens).view(1, -1)
+    pattern = torch.where(k <= q, torch.zeros((), dtype=torch.long), torch.tensor(ninf))
+    out = torch.empty(batch, tiles, tiles, dtype=torch.uint8)
+    for b in range(batch):
+        for i in range(tiles):
+            for j in range(tiles):
+                blk = bits[b, 64 * i:64 * (i + 1), 64 * j:64 * (j + 1)]
+                pat = pattern[64 * i:64 * (i + 1), 64 * j:64 * (j + 1)]
+                out[b, i, j] = 0 if bool((blk == ninf).all()) else (1 if torch.equal(blk, pat) else 2)
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("tokens", [64, 100, 200, 512])  # 100 in bf16/fp16: the scalar-load path
+def test_prefill_mask_tile_classes(gpu, dtype, tokens):
+    from stateful_llm_compiler_hip.backends import hip_prefill_mask_tiles
+
+    for name, mask in _class_masks(3, tokens, dtype, tokens).items():
+        announce(f"prefill mask tile classes {name} {dtype} T={tokens}")
+        classes = hip_prefill_mask_tiles(mask.to(gpu)).cpu()
+        expected = _classes_reference(mask)
+        assert torch.equal(classes, expected), name
+        if name == "causal":
+            # below the diagonal 1, above 0, the diagonal tile 1
+            assert int(classes.max()) == 1 and bool((classes[:, 0, 1:] == 0).all() if classes.shape[1] > 1 else True)
+        if name == "negzero":
+            assert bool((classes <= 2).all()) and int(classes.max()) == 2
+
+
+@pytest.mark.parametrize("tokens", [200, 512])
+@pytest.mark.parametrize("order", ["online", "exact"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_prefill_mask_classes_are_bit_identical(gpu, tokens, order, causal):
+    """Skipping dead tiles and applying causal-pattern tiles from indices
+    gives the same bits as loading and adding every mask tile (classes all
+    2), and both are within the bf16 bar of the oracle."""
+
+    from stateful_llm_compiler_hip.backends import hip_prefill_attention
+
+    batch, q_heads, kv_heads, head_dim = 3, 14, 2, 64
+    g = generator(tokens + 3)
+    q = torch.randn(batch, q_heads, tokens, head_dim, generator=g).bfloat16()
+    k = torch.randn(batch, kv_heads, tokens, head_dim, generator=g).bfloat16()
+    v = torch.randn(batch, kv_heads, tokens, head_dim, generator=g).bfloat16()
+    tiles = -(-tokens // 64)
+    every = torch.full((batch, tiles, tiles), 2, dtype=torch.uint8, device=gpu)
+    for mask_dtype in (torch.bfloat16, torch.float32):
+        for name, mask in _class_masks(batch, tokens, mask_dtype, 9).items():
+            announce(f"prefill classes bitwise {name} {mask_dtype} T={tokens} order={order} causal={causal}")
+            args = (q.to(gpu), k.to(gpu), v.to(gpu), mask.to(gpu))
+            fast = hip_prefill_attention(*args, scale=0.125, causal=causal, softmax_order=order)
+            slow = hip_prefill_attention(*args, scale=0.125, causal=causal, softmax_order=order,
+                                         mask_tiles=every)
+            torch.cuda.synchronize()
+            assert torch.equal(fast.view(torch.int16), slow.view(torch.int16)), name
+            if mask_dtype == torch.float32 and name in ("padded", "sparse"):
+                expected = ref.prefill_attention(q, k, v, mask, groups=q_heads // kv_heads, scale=0.125,
+                                                  causal=causal)
+                finite = torch.isfinite(expected)
+                assert torch.equal(finite, torch.isfinite(fast.cpu().float()))
+                assert_bf16_close(fast.cpu()[finite], expected[finite])
