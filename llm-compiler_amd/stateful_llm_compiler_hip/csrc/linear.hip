@@ -786,16 +786,19 @@ int launch_ring(const void* x, const void* w, const void* bias, void* y, int M, 
   return slc_host::check_launch("slc_hip_linear(ring)");
 }
 
-// Ring-kernel tile for a shape when the caller leaves it to the library:
-// 256 x 128 once that grid holds at least half a workgroup per CU per round
-// (two rounds of 128 on 256 CUs), else 128 x 128 under the same rule, else
-// the 64 x 64 tile (small grids: most CUs would idle at larger tiles, and the
-// deep ring hides the latency of K's many k-tiles).  Measured on MI355X at
-// the Qwen2-0.5B projection shapes for M = 128 .. 32768.
+// Ring-kernel tile for a shape when the caller leaves it to the library, by
+// the number of 128 x 128 tiles the shape has: 256 x 128 from 300 of them
+// (the larger tile reads less per flop once the grid is a few rounds deep),
+// 128 x 128 from 128 (half a round on 256 CUs), then 128 x 64 while that
+// grid has 192 workgroups, else 64 x 64 (small grids: the deep ring hides the
+// latency of K's many k-tiles).  The winners measured on MI355X at the
+// Qwen2-0.5B projection shapes for M = 128 .. 32768.
 inline int auto_ring_tile(int64_t M, int64_t n_tiles128) {
-  const int64_t n256 = ((M + 255) / 256) * n_tiles128;
   const int64_t n128 = ((M + 127) / 128) * n_tiles128;
-  return n256 >= 128 ? SLC_TILE_R256X128 : (n128 >= 128 ? SLC_TILE_R128X128 : SLC_TILE_R64X64);
+  if (n128 >= 300) return SLC_TILE_R256X128;
+  if (n128 >= 128) return SLC_TILE_R128X128;
+  if (2 * n128 >= 192) return SLC_TILE_R128X64;
+  return SLC_TILE_R64X64;
 }
 
 // One of the ring tiles; kNoResidualPath (nothing launched) where the shape
