@@ -65,7 +65,7 @@ int launch_mfma(const void* query, const void* kb, const void* vb,
                    ? counters
                    : nullptr;
   const size_t dyn_lds =
-      exact ? static_cast<size_t>(slc_host::ceil_div(std::min(mask_len, capacity), kTile) * 1024) : 0;
+      exact ? static_cast<size_t>(exact_dyn_bytes<T, D>()) : 0;
 #define SLC_MFMA_K(MK, L64, ROPE, EX)                                                      \
   do {                                                                                     \
     if (EX && exact_lds_limit<T, D, MK, L64, ROPE, EX>(static_cast<int>(dyn_lds)) != hipSuccess) \

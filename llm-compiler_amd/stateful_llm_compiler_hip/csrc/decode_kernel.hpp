@@ -478,25 +478,35 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   using KV = std::integral_constant<int, 3>;
   using KOnly = std::integral_constant<int, 1>;
   using VOnly = std::integral_constant<int, 2>;
-  using First = std::conditional_t<EXACT, KOnly, KV>;
   // kTilesInFlight tiles per wave: tile i is consumed, then refilled
   // kTilesInFlight sweeps ahead.  sched_barrier keeps each prologue tile's
   // loads ahead of the next one's: the loop consumes them in that order, and
   // a later tile issued first would make the first step wait for every load
   // (vmcnt(0)) -- a wait that, sitting in the loop header, would then drain
-  // the prefetch on every iteration.
+  // the prefetch on every iteration.  The prologue runs first in each path
+  // below (no code precedes it there).
   Tile tiles[kTilesInFlight];
+  auto prologue = [&](auto which) {
 #pragma unroll
-  for (int i = 0; i < kTilesInFlight; ++i) {
-    load_tile(t_first + i * kStride, tiles[i], chunk_end, First{});
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  if constexpr (ROPE) {
-    rope_slices<T, KK>(qraw, cs, sn);
+    for (int i = 0; i < kTilesInFlight; ++i) {
+      load_tile(t_first + i * kStride, tiles[i], chunk_end, which);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (ROPE) {
+      rope_slices<T, KK>(qraw, cs, sn);
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) qv[kk] = as_vec<T>(qraw[kk]);
-    store_new_row();
-  }
+      for (int kk = 0; kk < KK; ++kk) qv[kk] = as_vec<T>(qraw[kk]);
+      store_new_row();
+    }
+  };
+  // EXACT: when the chunk's tiles fit in the dynamic LDS with their V rows
+  // (per 32-token tile: the 8 fp32 log2-domain scores of every lane, 2 KB,
+  // and the lanes' V registers, 64 * D bytes), pass 1 loads K and V together
+  // and keeps both, and pass 2 reads no memory.  Otherwise pass 1 keeps the
+  // rounded scores (1 KB per tile) and pass 2 streams V.
+  constexpr int kStashTileBytes = 2048 + 64 * D;
+  const int ntiles = (chunk_end - chunk_start + kTile - 1) / kTile;
+  const bool stash = EXACT && ntiles * kStashTileBytes <= exact_dyn_bytes<T, D>();
 
   // S^T tile: two 16-token MFMA blocks; lane holds tokens 16j+4g+r, head c.
   // q.k and its scaling are materialised in the tensor dtype, as the
@@ -645,15 +655,9 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
   float* sm_m = reinterpret_cast<float*>(smem);
   float* sm_l = sm_m + kWaves * kMaxGroups;
   float* sm_o = sm_l + kWaves * kMaxGroups;  // [wave][head][D]
-  if constexpr (EXACT) {
-    // Pass 1, then the row max and sum over the 4 lane groups and the waves.
-    sweep(score_tile, KOnly{});
-    move_window(t_first, t_first + kAhead - kStride + kTile - 1);
-#pragma unroll
-    for (int i = 0; i < kTilesInFlight; ++i) {  // pass 2's first tiles fly during the combine
-      load_tile(t_first + i * kStride, tiles[i], chunk_end, VOnly{});
-      __builtin_amdgcn_sched_barrier(0);
-    }
+  // EXACT: the row max and sum over the 4 lane groups and the waves, and
+  // from them the shift of pass 2.
+  auto exact_norm = [&]() {
     l_run += __shfl_xor(l_run, 16, 64);
     l_run += __shfl_xor(l_run, 32, 64);
     if (g == 0) {
@@ -672,10 +676,71 @@ __global__ __launch_bounds__(kThreads) void decode_attention_mfma_kernel(
     // An empty row (no token, or all of them masked to -inf) has sum 0 and
     // gives NaN, as the reference's softmax over an all -inf row does.
     norm_shift = lsum > 0.0f ? mu + __builtin_amdgcn_logf(lsum) : __builtin_nanf("");
-    sweep(weigh_tile, VOnly{});
+  };
+  if constexpr (EXACT) {
+    if (stash) {
+      // Tile i of the chunk: scores at [2i, 2i + 1][lane], V at [2KK i ..][lane]
+      // (16-byte words).
+      uint4* s_lds = score_lds;
+      uint4* v_lds = score_lds + ntiles * 128;
+      auto stash_tile = [&](int t0, const Tile& tile) {
+        float s[8];
+        u16x8 r_bits;
+        tile_scores(t0, tile, s, r_bits);
+        const int ti = (t0 - chunk_start) / kTile;
+        s_lds[(2 * ti) * 64 + lane] = make_uint4(__float_as_uint(s[0]), __float_as_uint(s[1]),
+                                                 __float_as_uint(s[2]), __float_as_uint(s[3]));
+        s_lds[(2 * ti + 1) * 64 + lane] = make_uint4(__float_as_uint(s[4]), __float_as_uint(s[5]),
+                                                     __float_as_uint(s[6]), __float_as_uint(s[7]));
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int kk = 0; kk < KK; ++kk) v_lds[((2 * ti + j) * KK + kk) * 64 + lane] = tile.v[j][kk];
+        update_max(s);
+        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+        float psum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) psum += fast_exp2(s[i] - m_use);
+        l_run += psum;
+      };
+      prologue(KV{});
+      sweep(stash_tile, KV{});
+      exact_norm();
+      // Pass 2 from LDS: each wave weighs its own tiles (the words it wrote).
+      for (int t0 = t_first; t0 < chunk_end; t0 += kStride) {
+        const int ti = (t0 - chunk_start) / kTile;
+        Tile tile;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int kk = 0; kk < KK; ++kk) tile.v[j][kk] = v_lds[((2 * ti + j) * KK + kk) * 64 + lane];
+        const uint4 s0 = s_lds[(2 * ti) * 64 + lane];
+        const uint4 s1 = s_lds[(2 * ti + 1) * 64 + lane];
+        const float s[8] = {__uint_as_float(s0.x), __uint_as_float(s0.y), __uint_as_float(s0.z),
+                            __uint_as_float(s0.w), __uint_as_float(s1.x), __uint_as_float(s1.y),
+                            __uint_as_float(s1.z), __uint_as_float(s1.w)};
+        u16x8 pbits;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pbits.v[i] = bits_of<T>(fast_exp2(s[i] - norm_shift));
+        accumulate_pv(tile, __builtin_bit_cast(typename M::vec, pbits));
+      }
+    } else {
+      // Pass 1, the norm, then pass 2 streaming V.
+      prologue(KOnly{});
+      sweep(score_tile, KOnly{});
+      move_window(t_first, t_first + kAhead - kStride + kTile - 1);
+#pragma unroll
+      for (int i = 0; i < kTilesInFlight; ++i) {  // pass 2's first tiles fly during the combine
+        load_tile(t_first + i * kStride, tiles[i], chunk_end, VOnly{});
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      exact_norm();
+      sweep(weigh_tile, VOnly{});
+    }
     __syncthreads();  // the LDS combine area is reused below
   } else {
-    sweep(compute_tile, First{});
+    prologue(KV{});
+    sweep(compute_tile, KV{});
     // Finish the per-lane partial sums of l over the 4 lane groups.
     l_run += __shfl_xor(l_run, 16, 64);
     l_run += __shfl_xor(l_run, 32, 64);
@@ -964,7 +1029,8 @@ int64_t partial_bytes(int64_t batch, int64_t q_heads, int64_t head_dim, int64_t 
 }
 
 // Longest sequence (mask length) the EXACT MFMA kernel holds in LDS: 1 KB of
-// rounded scores per 32 tokens next to the static combine area.
+// rounded scores per 32 tokens next to the static combine area (the dynamic
+// LDS of every EXACT launch is exact_dyn_bytes).
 int64_t exact_max_tokens(int64_t head_dim) {
   return head_dim == 64 ? 4096 : head_dim == 128 ? 2048 : 0;
 }
@@ -986,7 +1052,7 @@ hipError_t exact_lds_limit(int bytes) {
     status = hipFuncSetAttribute(
         reinterpret_cast<const void*>(&decode_attention_mfma_kernel<T, D, MK, L64, ROPE, EXACT, PG>),
         hipFuncAttributeMaxDynamicSharedMemorySize,
-        static_cast<int>(slc_host::ceil_div(exact_max_tokens(D), kTile) * 1024));
+        exact_dyn_bytes<T, D>());
   });
   (void)bytes;
   return status;

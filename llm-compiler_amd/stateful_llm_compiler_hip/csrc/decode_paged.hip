@@ -52,7 +52,7 @@ int launch_paged(const void* query, const void* kp, const void* vp, const void* 
                    ? counters
                    : nullptr;
   const size_t dyn_lds =
-      exact ? static_cast<size_t>(slc_host::ceil_div(std::min(mask_len, capacity), kTile) * 1024) : 0;
+      exact ? static_cast<size_t>(exact_dyn_bytes<T, D>()) : 0;
   RopeStore rs{};
 #define SLC_PAGED_K(MK, L64, ROPE, EX)                                                      \
   do {                                                                                      \

@@ -81,6 +81,15 @@ struct SharedLayout {
   static constexpr int kBytes = kVBytes > kCombineBytes ? kVBytes : kCombineBytes;
 };
 
+// Dynamic LDS of every EXACT-order launch: 128 KB, or less where the static
+// area and the 160 KB of a CU leave less.  (The runtime granted 128 KB here
+// and refused the 141 KB that 160 KB minus the static area would allow.)
+template <typename T, int D>
+constexpr int exact_dyn_bytes() {
+  constexpr int room = (160 * 1024 - SharedLayout<T, D>::kBytes - 1024) / 1024 * 1024;
+  return room < 128 * 1024 ? room : 128 * 1024;
+}
+
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
 // Raw buffer resource over [base, base + bytes): loads at or past the end

@@ -557,6 +557,7 @@ def test_decode_attention_workspaces_replay_concurrently(gpu):
     (3, 65, [7, 31, 65], "zeros", torch.bfloat16, 64),       # reference KAT lengths
     (8, 1024, None, "random", torch.bfloat16, 64),           # config 2, random mask
     (4, 4096, None, "zeros", torch.bfloat16, 64),            # the exact order's longest mask
+    (4, 800, [1, 672, 673, 800], "random", torch.bfloat16, 64),  # either side of the LDS-kept V (672 tokens)
     (3, 700, [0, 1, 700], "random", torch.float16, 128),     # D = 128, an empty row (NaN)
     (2, 300, [150, 299], "zeros", torch.bfloat16, 80),       # generic kernel
 ])
