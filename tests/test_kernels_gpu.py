@@ -585,6 +585,34 @@ def test_decode_attention_exact_softmax_order(gpu, batch, capacity, lengths, mas
     assert e >= 0.97 and e >= o
 
 
+@pytest.mark.parametrize("order", ["exact", "online"])
+def test_decode_attention_ignores_rows_past_the_length(gpu, order):
+    """Rows past a sequence's length take no part, whatever the cache holds
+    there: NaN and inf in them leave the output bit for bit as zeros do
+    (lengths on either side of the exact order's LDS-kept V)."""
+    from stateful_llm_compiler_hip.backends import hip_decode_attention
+
+    announce(f"decode attention ignores rows past the length order={order}")
+    g = generator(41)
+    batch, cap = 4, 1024
+    lengths = torch.tensor([5, 300, 672, 900], dtype=torch.int64)
+    q = torch.randn(batch, 14, 1, 64, generator=g).to(torch.bfloat16).to(gpu)
+    k = torch.randn(batch, cap, 2, 64, generator=g).to(torch.bfloat16)
+    v = torch.randn(batch, cap, 2, 64, generator=g).to(torch.bfloat16)
+    past = torch.arange(cap).view(1, cap) >= lengths.view(batch, 1)
+    outs = []
+    for fill in (0.0, float("nan"), float("inf")):
+        kf, vf = k.clone(), v.clone()
+        kf[past] = fill
+        vf[past] = fill
+        out = hip_decode_attention(q, kf.to(gpu), vf.to(gpu), lengths.to(gpu), None,
+                                   scale=0.125, softmax_order=order)
+        outs.append(out.cpu())
+    assert torch.isfinite(outs[0].float()).all()
+    for out in outs[1:]:
+        assert torch.equal(out.view(torch.int16), outs[0].view(torch.int16))
+
+
 def test_decode_attention_exact_order_rejects_long_masks(gpu):
     from stateful_llm_compiler_hip._native import KernelLaunchError
     from stateful_llm_compiler_hip.backends import hip_decode_attention
