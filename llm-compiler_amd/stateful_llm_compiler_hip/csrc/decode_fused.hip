@@ -358,7 +358,10 @@ int launch_rows(FusedArgs& a, hipStream_t stream) {
 // (no cross-wave reduction, nothing through LDS) and keeps U k-steps of
 // weights in flight.
 constexpr int kWideBlocks = 1024;
-template <typename T, int MB, int U>
+// XL: the input rows are staged in LDS once per workgroup (row stride K + 8
+// elements, so the 16 rows of an operand read fall 4 banks apart) instead of
+// being re-read from the cache by every wave at every k-step.
+template <typename T, int MB, int U, bool XL = false>
 __global__ __launch_bounds__(256) void wide_rows_kernel(FusedArgs p) {
   using MF = Mfma<T>;
   const int lane = threadIdx.x & 63;
@@ -366,7 +369,9 @@ __global__ __launch_bounds__(256) void wide_rows_kernel(FusedArgs p) {
   const int g = lane >> 4;
   const int K = p.hidden, M = p.rows, N = p.n[0];
   const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16;
-  if (n0 >= N) return;
+  extern __shared__ uint4 x_lds[];
+  const int x_stride = K / 8 + 1;  // 16-byte words per staged row
+  if (n0 >= N && !XL) return;
   const T* w = static_cast<const T*>(p.w[0]);
   const int w_rows = min(16, N - n0);
   const __amdgpu_buffer_rsrc_t rw =
@@ -388,28 +393,49 @@ __global__ __launch_bounds__(256) void wide_rows_kernel(FusedArgs p) {
       const int s = s0 + u;
       const bool ok = s < steps && s * 32 + g * 8 < K;
       wr[u] = ok ? buffer_load16(rw, w_off + s * 64) : make_uint4(0, 0, 0, 0);
+      if constexpr (!XL) {
 #pragma unroll
-      for (int i = 0; i < MB; ++i)
-        xr[u][i] = ok ? buffer_load16(rx, x_off[i] + s * 64) : make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < MB; ++i)
+          xr[u][i] = ok ? buffer_load16(rx, x_off[i] + s * 64) : make_uint4(0, 0, 0, 0);
+      }
     }
   };
-  auto multiply = [&](const uint4 (&wr)[U], const uint4 (&xr)[U][MB]) {
+  auto multiply = [&](int s0, const uint4 (&wr)[U], const uint4 (&xr)[U][MB]) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int i = 0; i < MB; ++i)
-        acc[i] = MF::run(__builtin_bit_cast(typename MF::vec, xr[u][i]),
+      for (int i = 0; i < MB; ++i) {
+        uint4 xv = xr[u][i];
+        if constexpr (XL) {
+          const int s = s0 + u;
+          const int row = i * 16 + c;
+          xv = row < M && s < steps && s * 32 + g * 8 < K ? x_lds[row * x_stride + s * 4 + g]
+                                                          : make_uint4(0, 0, 0, 0);
+        }
+        acc[i] = MF::run(__builtin_bit_cast(typename MF::vec, xv),
                          __builtin_bit_cast(typename MF::vec, wr[u]), acc[i]);
+      }
   };
   int s0 = 0;
   fetch(s0, wa, xa);
+  if constexpr (XL) {
+    // The weight loads above do not wait for this.  Every wave passes the
+    // barrier (the waves past N leave only after it).
+    const T* x = static_cast<const T*>(p.x);
+    for (int idx = threadIdx.x; idx < M * (K / 8); idx += 256) {
+      const int r = idx / (K / 8), v = idx % (K / 8);
+      x_lds[r * x_stride + v] = *reinterpret_cast<const uint4*>(x + r * p.x_rs + v * 8);
+    }
+    __syncthreads();
+    if (n0 >= N) return;
+  }
   while (s0 < steps) {
     fetch(s0 + U, wb, xb);
-    multiply(wa, xa);
+    multiply(s0, wa, xa);
     s0 += U;
     if (s0 >= steps) break;
     fetch(s0 + U, wa, xa);
-    multiply(wb, xb);
+    multiply(s0, wb, xb);
     s0 += U;
   }
   // C layout: lane (col c = feature, rows 4g..4g+3 of block i).
@@ -429,11 +455,22 @@ __global__ __launch_bounds__(256) void wide_rows_kernel(FusedArgs p) {
     }
 }
 
+#ifndef SLC_WIDE_U
+#define SLC_WIDE_U 8
+#endif
+#ifndef SLC_WIDE_XL
+#define SLC_WIDE_XL 1
+#endif
 template <typename T>
 int launch_wide(FusedArgs& a, hipStream_t stream) {
   const int blocks = (a.n[0] + 63) / 64;
-  if (a.rows <= 16) {
-    hipLaunchKernelGGL((wide_rows_kernel<T, 1, 8>), dim3(blocks), dim3(256), 0, stream, a);
+  const int x_bytes = a.rows * (a.hidden / 8 + 1) * 16;
+  const bool x_aligned = reinterpret_cast<uintptr_t>(a.x) % 16 == 0 && a.x_rs % 8 == 0;
+  if (a.rows <= 16 && SLC_WIDE_XL && a.hidden % 8 == 0 && x_aligned && x_bytes <= 32 * 1024) {
+    hipLaunchKernelGGL((wide_rows_kernel<T, 1, SLC_WIDE_U, true>), dim3(blocks), dim3(256),
+                       static_cast<unsigned>(x_bytes), stream, a);
+  } else if (a.rows <= 16) {
+    hipLaunchKernelGGL((wide_rows_kernel<T, 1, SLC_WIDE_U>), dim3(blocks), dim3(256), 0, stream, a);
   } else {
     hipLaunchKernelGGL((wide_rows_kernel<T, 2, 4>), dim3(blocks), dim3(256), 0, stream, a);
   }
