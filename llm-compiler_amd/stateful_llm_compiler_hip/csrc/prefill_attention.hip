@@ -434,14 +434,14 @@ __global__ __launch_bounds__(256) void mask_tile_class_kernel(const void* __rest
 }
 
 // ---- grouped-head kernel (v2) ------------------------------------------------
-// A workgroup owns 64 queries of ALL the query heads of one KV head (GQA
-// group G): G compute waves (one query head each, 64 queries = 4 MFMA column
-// blocks) plus one producer wave that streams the K, V (and mask) tiles of 64
+// A workgroup owns kV2Queries queries of ALL the query heads of one KV head
+// (GQA group G): G compute waves (one query head each, kQB MFMA column
+// blocks of 16 queries) plus one producer wave that streams the K, V (and mask) tiles of 64
 // keys into an LDS ring with direct-to-LDS loads.  K, V and the mask are thus
 // read once per workgroup for all G heads (the single-head kernel reads them
 // G times), and no VALU work or VGPR goes into staging.
 //  * S^T[key, query] = K . Q^T: K rows straight from the XOR-swizzled tile
-//    (ds_read_b128), Q^T in registers (4 query blocks reuse every K read).
+//    (ds_read_b128), Q^T in registers (kQB query blocks reuse every K read).
 //  * O^T[dim, query] += V^T . P^T: V^T operands come from the natural V tile
 //    through the LDS transpose read (ds_read_b64_tr_b16), whose lane j of a
 //    16-lane group addresses 4 dims of key row T(j/4) and receives dim j of
@@ -449,14 +449,24 @@ __global__ __launch_bounds__(256) void mask_tile_class_kernel(const void* __rest
 //  * One barrier per tile: the producer waits for tile i, the barrier hands
 //    it to the consumers, then the producer refills the ring slot consumers
 //    released at that barrier.
-constexpr int kV2Queries = 64;
+// Query blocks of 16 per consumer wave: 4 (64 queries per workgroup, about
+// 214 VGPRs, one workgroup per CU) or 2 (32 queries, at most 128 VGPRs, two
+// workgroups per CU whose MFMA and VALU phases need not coincide).
+#ifndef SLC_PREFILL_QB
+#define SLC_PREFILL_QB 2
+#endif
+constexpr int kQB = SLC_PREFILL_QB;
+constexpr int kV2Queries = 16 * kQB;
 // Longest key range (in 64-key tiles) the tile-class list covers: T <= 65536.
 constexpr int kMaxClassTiles = 1024;
 // Two ring stages: the producer refills one stage while the consumers read
 // the other (measured 2-3 % faster than three stages, equal to four).
-constexpr int kV2Stages = 2;
+#ifndef SLC_PREFILL_STAGES
+#define SLC_PREFILL_STAGES 2
+#endif
+constexpr int kV2Stages = SLC_PREFILL_STAGES;
 constexpr int kV2TileBytes = kKeys * kRowBytes;                 // 8 KB of K or of V
-// Mask tile: 64 query rows x 64 keys of the mask element type (0: no mask).
+// Mask tile: kV2Queries query rows x 64 keys of the mask element type (0: no mask).
 template <int MK>
 constexpr int mask_elem_bytes() { return MK == 0 ? 0 : (MK == SLC_F32 + 1 ? 4 : 2); }
 template <int MK>
@@ -498,7 +508,7 @@ __device__ __forceinline__ uint2 lds_read_tr(const unsigned char* p) {
 // scores and weighs V with exp(score - max) / sum rounded to the I/O dtype,
 // so the rounding applies to the normalised probability as in the reference.
 template <typename T, int G, int MK, bool CAUSAL, bool POW2, bool EXACT>
-__global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
+__global__ __launch_bounds__((G + 1) * 64, kQB == 2 ? 4 : 1) void prefill_attention_v2_kernel(
     const T* __restrict__ query, const T* __restrict__ key, const T* __restrict__ value,
     const void* __restrict__ mask, T* __restrict__ output, int tokens, int kv_heads,
     int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t k_sb, int64_t k_sh, int64_t k_st,
@@ -538,7 +548,11 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
   const bool classed = MK != 0 && tile_class != nullptr;
   if (classed && wave == G) {
     // The producer lists the live tiles (class != 0) before the first barrier.
-    const unsigned char* row = tile_class + (b * nqb + qblk) * static_cast<int64_t>((tokens + kKeys - 1) / kKeys);
+    // The classes are per 64 x 64 tile: a block of kV2Queries rows takes its
+    // 64-row block's (the causal pattern and -inf throughout hold for every
+    // part of a tile that has them).
+    const int64_t key_tiles = (tokens + kKeys - 1) / kKeys;
+    const unsigned char* row = tile_class + (b * key_tiles + qblk * kV2Queries / 64) * key_tiles;
     int count = 0;
     for (int base = 0; base < all_tiles; base += 64) {
       const int t = base + lane;
@@ -620,9 +634,9 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
 
   // ---- consumers: wave w computes query head kvh * G + w ----------------------
   const int h = kvh * G + wave;
-  typename M::vec qv[4][2];
+  typename M::vec qv[kQB][2];
 #pragma unroll
-  for (int qb = 0; qb < 4; ++qb) {
+  for (int qb = 0; qb < kQB; ++qb) {
     const int qrow = min(q0 + 16 * qb + c, tokens - 1);
     const T* qp = query + b * q_sb + h * q_sh + static_cast<int64_t>(qrow) * q_st;
 #pragma unroll
@@ -634,10 +648,10 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
   // sums each query's probabilities (all 16 rows of the block hold the
   // same sum), so the matrix cores, not the VALU, do the row sums, and the
   // running rescale applies to it with the outputs.
-  float m_run[4];
-  f32x4_t acc[5][4];  // [dim block, then the row-sum block][query block]
+  float m_run[kQB];
+  f32x4_t acc[5][kQB];  // [dim block, then the row-sum block][query block]
 #pragma unroll
-  for (int qb = 0; qb < 4; ++qb) {
+  for (int qb = 0; qb < kQB; ++qb) {
     m_run[qb] = -INFINITY;
 #pragma unroll
     for (int db = 0; db < 5; ++db) acc[db][qb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -660,8 +674,8 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
   const int kv_off0 = c * kRowBytes;  // K operand row 16kb + c
   // EXACT: per-lane partial row sums of pass 1 (the lane's 16 keys of each
   // tile), then the exponent shift max + log2(sum) of pass 2.
-  float l_part[4] = {0.f, 0.f, 0.f, 0.f};
-  float shift[4] = {0.f, 0.f, 0.f, 0.f};
+  float l_part[kQB] = {};
+  float shift[kQB] = {};
 
   for (int step = 0; step < nsteps; ++step) {
     __syncthreads();  // tile of this step is in ring[step % kStages]
@@ -674,7 +688,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
     if (EXACT && step == ntiles) {
       // Pass 1 done: row sums over the 4 lane groups, then the shift.
 #pragma unroll
-      for (int qb = 0; qb < 4; ++qb) {
+      for (int qb = 0; qb < kQB; ++qb) {
         float l = l_part[qb];
         l += __shfl_xor(l, 16, 64);
         l += __shfl_xor(l, 32, 64);
@@ -722,7 +736,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
     }
 
     // S^T blocks: 4 key blocks x 4 query blocks.
-    f32x4_t st[4][4];
+    f32x4_t st[4][kQB];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       typename M::vec ka[2];
@@ -731,7 +745,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
         ka[kk] = *reinterpret_cast<const typename M::vec*>(
             kt + (16 * kb) * kRowBytes + kv_off0 + (((4 * kk + g) ^ (c & 7)) << 4));
 #pragma unroll
-      for (int qb = 0; qb < 4; ++qb) {
+      for (int qb = 0; qb < kQB; ++qb) {
         f32x4_t a = f32x4_t{0.f, 0.f, 0.f, 0.f};
         a = M::run(ka[0], qv[qb][0], a);
         st[kb][qb] = M::run(ka[1], qv[qb][1], a);
@@ -741,7 +755,7 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
     // Scores with the mask and validity (fp32, as the reference's fused kernel).
     const bool full = !causal_tile ? k0 + kKeys <= tokens : k0 + kKeys <= q0 && k0 + kKeys <= tokens;
 #pragma unroll
-    for (int qb = 0; qb < 4; ++qb) {
+    for (int qb = 0; qb < kQB; ++qb) {
       const int my_query = q0 + 16 * qb + c;
       float mx = -INFINITY;
 #pragma unroll
@@ -856,9 +870,9 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
     // P^T operands and O^T += V^T . P^T.
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      typename M::vec pv[4];
+      typename M::vec pv[kQB];
 #pragma unroll
-      for (int qb = 0; qb < 4; ++qb) {
+      for (int qb = 0; qb < kQB; ++qb) {
         // Online: exp2 relative to the running max.  EXACT pass 2: relative
         // to max + log2(sum), i.e. the normalised probability, then rounded.
         const float m_use = EXACT ? shift[qb] : (m_run[qb] == -INFINITY ? 0.0f : m_run[qb]);
@@ -877,17 +891,17 @@ __global__ __launch_bounds__((G + 1) * 64) void prefill_attention_v2_kernel(
         const uint2 hi = lds_read_tr(vt + (half * 32 + 16) * kRowBytes + tr_off[db]);
         const typename M::vec va = __builtin_bit_cast(typename M::vec, make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
-        for (int qb = 0; qb < 4; ++qb) acc[db][qb] = M::run(va, pv[qb], acc[db][qb]);
+        for (int qb = 0; qb < kQB; ++qb) acc[db][qb] = M::run(va, pv[qb], acc[db][qb]);
       }
       if constexpr (!EXACT) {
 #pragma unroll
-        for (int qb = 0; qb < 4; ++qb) acc[4][qb] = M::run(ones, pv[qb], acc[4][qb]);
+        for (int qb = 0; qb < kQB; ++qb) acc[4][qb] = M::run(ones, pv[qb], acc[4][qb]);
       }
     }
   }
 
 #pragma unroll
-  for (int qb = 0; qb < 4; ++qb) {
+  for (int qb = 0; qb < kQB; ++qb) {
     const int my_query = q0 + 16 * qb + c;
     if (my_query < tokens) {
       // EXACT: the terms were normalised already.  An empty row (every key
