@@ -60,6 +60,38 @@ def test_linear_bf16_qwen_shapes(gpu, rows, k, n, bias):
     _check_linear_bf16(y, x, w, b)
 
 
+@pytest.mark.parametrize("rows,k,n,strided", [(8, 896, 151936, False), (1, 896, 20000, False),
+                                              (16, 2048, 17000, False), (8, 896, 20000, True),
+                                              (24, 896, 20000, False)])
+def test_linear_bf16_vocabulary_width(gpu, rows, k, n, strided):
+    """The vocabulary-width decode kernel (one wave per 16 features over all
+    of K; input rows staged in LDS when they are 16-byte aligned, read from
+    the cache otherwise, as a strided view here; rows past 16 take two
+    row blocks) within one bf16 ulp of the fp64 product."""
+    from stateful_llm_compiler_hip.backends import hip_linear
+
+    announce(f"linear bf16 vocabulary width M={rows} K={k} N={n} strided={strided}")
+    g = generator(rows + k + n)
+    x = torch.randn(rows, k + (3 if strided else 0), generator=g).bfloat16()
+    w = (torch.randn(n, k, generator=g) * 0.02).bfloat16()
+    xd, wd = x.to(gpu), w.to(gpu)
+    if strided:
+        # Row stride k + 3 and a 2-byte offset, through the C ABI (the
+        # Python wrapper takes contiguous inputs only).
+        from stateful_llm_compiler_hip import _native
+
+        x, xd = x[:, 1:k + 1], xd[:, 1:k + 1]
+        y = torch.empty(rows, n, dtype=torch.bfloat16, device=gpu)
+        status = _native.library().slc_hip_linear(
+            xd.data_ptr(), wd.data_ptr(), None, y.data_ptr(), _native.SLC_BF16, rows, n, k,
+            k + 3, n, _native.current_stream(xd.device))
+        _native.check(status, "slc_hip_linear")
+    else:
+        y = hip_linear(xd, wd)
+    torch.cuda.synchronize()
+    _check_linear_bf16(y, x, w, None, against_oracle=False)
+
+
 def test_linear_bf16_large_m_and_3d(gpu):
     from stateful_llm_compiler_hip.backends import hip_linear
 
