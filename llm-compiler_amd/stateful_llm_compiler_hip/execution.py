@@ -84,6 +84,20 @@ DTYPES = {
 DTYPE_NAMES = {value: key for key, value in DTYPES.items()}
 
 
+def _zeroed_layers(count: int, shape: tuple[int, ...], device, dtype, *, pairs: bool = False):
+    """``count`` zeroed per-layer tensors of ``shape`` as views of one
+    allocation, so that a whole state is cleared by one fill instead of one
+    launch per layer and tensor.  ``pairs``: the first half of the views
+    (keys) and the second half (values) as two tuples."""
+
+    block = torch.zeros((count, *shape), device=device, dtype=dtype)
+    views = tuple(block[i] for i in range(count))
+    if pairs:
+        half = count // 2
+        return views[:half], views[half:]
+    return (views,)
+
+
 @dataclass(frozen=True)
 class PreallocatedKVCacheState:
     """Shared physical KV buffers plus per-version logical lengths."""
@@ -132,12 +146,9 @@ class PreallocatedKVCacheState:
         if key.ndim != 4 or num_layers <= 0 or capacity <= 0:
             raise ExecutionError("KV init got an illegal template, layer count or capacity")
         batch, heads, _, head_dim = key.shape
-        keys = tuple(
-            torch.zeros(batch, capacity, heads, head_dim, device=key.device, dtype=key.dtype)
-            for _ in range(num_layers)
-        )
-        values = tuple(torch.zeros_like(buffer) for buffer in keys)
-        lengths = tuple(torch.zeros(batch, device=key.device, dtype=torch.int64) for _ in range(num_layers))
+        keys, values = _zeroed_layers(2 * num_layers, (batch, capacity, heads, head_dim),
+                                      key.device, key.dtype, pairs=True)
+        (lengths,) = _zeroed_layers(num_layers, (batch,), key.device, torch.int64)
         overflow = torch.zeros(1, device=key.device, dtype=torch.int32)
         return cls(keys, values, lengths, capacity, overflow=overflow,
                    in_place_lengths=in_place_lengths, zero_slots=frozenset(range(num_layers)),
@@ -486,10 +497,9 @@ class PagedKVCacheState(PreallocatedKVCacheState):
             raise ExecutionError("paged KV init got an illegal template, layer count, capacity or page size")
         batch, heads, _, head_dim = key.shape
         pages = capacity // page_tokens
-        keys = tuple(torch.zeros(batch * pages, page_tokens, heads, head_dim, device=key.device,
-                                 dtype=key.dtype) for _ in range(num_layers))
-        values = tuple(torch.zeros_like(pool) for pool in keys)
-        lengths = tuple(torch.zeros(batch, device=key.device, dtype=torch.int64) for _ in range(num_layers))
+        keys, values = _zeroed_layers(2 * num_layers, (batch * pages, page_tokens, heads, head_dim),
+                                      key.device, key.dtype, pairs=True)
+        (lengths,) = _zeroed_layers(num_layers, (batch,), key.device, torch.int64)
         return cls(keys, values, lengths, capacity,
                    overflow=torch.zeros(1, device=key.device, dtype=torch.int32),
                    in_place_lengths=in_place_lengths, zero_slots=frozenset(range(num_layers)),
