@@ -470,6 +470,10 @@ SLC_API int slc_hip_argmax(const void* logits, int64_t* output, int dtype, int64
  *                       kernel.triton.rms_norm (round_before_weight=1) plus
  *                       one kernel.triton.linear per matrix
  *                       (triton_rmsnorm.py:205-443, triton_linear.py:87-148).
+ *                       One matrix of >= 16384 rows with a norm (the LM head
+ *                       and the final norm): one launch for rows <= 16;
+ *                       SLC_ERR_UNSUPPORTED (nothing launched) above, where
+ *                       the caller runs the norm and the linear.
  *   norm_linear_swiglu: y = round(silu(round(x_n . w_gate^T))) *
  *                       round(x_n . w_up^T), x_n = rms_norm(x, norm_weight)
  *                       (the Qwen2 MLP front, qwen2.py:253-256).

@@ -77,6 +77,8 @@ def hip_norm_linear_group(
     norm = norm_weight is not None
     if not _fusable_rows(tensor, norm=norm):
         x = hip_rms_norm(tensor, norm_weight, epsilon=epsilon, round_before_weight=True) if norm else tensor
+        if len(weights) == 1:
+            return [hip_linear(x, weights[0], biases[0])]
         grouped = _linear_group(x, weights, biases)
         if grouped is not None:
             return grouped
@@ -100,6 +102,9 @@ def hip_norm_linear_group(
         float(epsilon), rows, hidden, len(weights), *per_matrix,
         _native.dtype_tag(tensor.dtype), _native.current_stream(tensor.device),
     )
+    if status == _UNSUPPORTED:  # nothing launched: the norm, then the linear
+        x = hip_rms_norm(tensor, norm_weight, epsilon=epsilon, round_before_weight=True) if norm else tensor
+        return [hip_linear(x, w, b) for w, b in zip(weights, biases)]
     _native.check(status, "slc_hip_norm_linear_group")
     return outputs
 

@@ -361,7 +361,11 @@ constexpr int kWideBlocks = 1024;
 // XL: the input rows are staged in LDS once per workgroup (row stride K + 8
 // elements, so the 16 rows of an operand read fall 4 banks apart) instead of
 // being re-read from the cache by every wave at every k-step.
-template <typename T, int MB, int U, bool XL = false>
+// NNV > 0 (with XL): the staged rows are the RMS-normalised input, NNV
+// 16-byte vectors per lane, computed by every workgroup with the function
+// the rms_norm kernel uses (so the result equals rms_norm then linear bit
+// for bit): the vocabulary head and its norm in one launch.
+template <typename T, int MB, int U, bool XL = false, int NNV = 0>
 __global__ __launch_bounds__(256) void wide_rows_kernel(FusedArgs p) {
   using MF = Mfma<T>;
   const int lane = threadIdx.x & 63;
@@ -422,9 +426,21 @@ __global__ __launch_bounds__(256) void wide_rows_kernel(FusedArgs p) {
     // The weight loads above do not wait for this.  Every wave passes the
     // barrier (the waves past N leave only after it).
     const T* x = static_cast<const T*>(p.x);
-    for (int idx = threadIdx.x; idx < M * (K / 8); idx += 256) {
-      const int r = idx / (K / 8), v = idx % (K / 8);
-      x_lds[r * x_stride + v] = *reinterpret_cast<const uint4*>(x + r * p.x_rs + v * 8);
+    if constexpr (NNV > 0) {
+      const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+      const T* nw = static_cast<const T*>(p.norm_w);
+      for (int m = wave; m < M; m += 4) {
+        uint4 out[NNV];
+        slc::rms_norm_row<T, NNV, true>(x + m * p.x_rs, nw, K, p.eps, lane, out);
+#pragma unroll
+        for (int i = 0; i < NNV; ++i)
+          if (lane + 64 * i < K / 8) x_lds[m * x_stride + lane + 64 * i] = out[i];
+      }
+    } else {
+      for (int idx = threadIdx.x; idx < M * (K / 8); idx += 256) {
+        const int r = idx / (K / 8), v = idx % (K / 8);
+        x_lds[r * x_stride + v] = *reinterpret_cast<const uint4*>(x + r * p.x_rs + v * 8);
+      }
     }
     __syncthreads();
     if (n0 >= N) return;
@@ -466,6 +482,28 @@ int launch_wide(FusedArgs& a, hipStream_t stream) {
   const int blocks = (a.n[0] + 63) / 64;
   const int x_bytes = a.rows * (a.hidden / 8 + 1) * 16;
   const bool x_aligned = reinterpret_cast<uintptr_t>(a.x) % 16 == 0 && a.x_rs % 8 == 0;
+  if (a.norm_w != nullptr) {
+    // Norm and head in one launch: only with the rows staged in LDS.
+    if (a.rows > 16 || a.hidden % 8 != 0 || !x_aligned || x_bytes > 32 * 1024)
+      return SLC_ERR_UNSUPPORTED;
+    const int nv = (a.hidden / 8 + 63) / 64;
+#define SLC_WIDE_NORM(NV)                                                                 \
+  hipLaunchKernelGGL((wide_rows_kernel<T, 1, SLC_WIDE_U, true, NV>), dim3(blocks), dim3(256), \
+                     static_cast<unsigned>(x_bytes), stream, a)
+    if (nv == 1) {
+      SLC_WIDE_NORM(1);
+    } else if (nv == 2) {
+      SLC_WIDE_NORM(2);
+    } else if (nv == 3) {
+      SLC_WIDE_NORM(3);
+    } else if (nv == 4) {
+      SLC_WIDE_NORM(4);
+    } else {
+      return SLC_ERR_UNSUPPORTED;
+    }
+#undef SLC_WIDE_NORM
+    return slc_host::check_launch("decode norm + linear (wide)");
+  }
   if (a.rows <= 16 && SLC_WIDE_XL && a.hidden % 8 == 0 && x_aligned && x_bytes <= 32 * 1024) {
     hipLaunchKernelGGL((wide_rows_kernel<T, 1, SLC_WIDE_U, true>), dim3(blocks), dim3(256),
                        static_cast<unsigned>(x_bytes), stream, a);
@@ -676,6 +714,15 @@ extern "C" int slc_hip_norm_linear_group(
       a.n[i] = static_cast<int>(ns[i]);
       a.y_rs[i] = yrs[i];
     }
+  }
+  // One vocabulary-width matrix: the wide kernel, normalising in its
+  // staging.  The single linear runs such a head on the wide kernel too, so
+  // when that kernel cannot take the norm (rows past 16) nothing is launched
+  // and the caller runs the norm and the linear: the equal-workgroup kernel
+  // would sum K in another order.
+  if (count == 1 && (a.n[0] + 15) / 16 >= kWideBlocks && norm_weight != nullptr) {
+    return dtype == SLC_BF16 ? launch_wide<slc::bf16_t>(a, static_cast<hipStream_t>(stream))
+                             : launch_wide<slc::f16_t>(a, static_cast<hipStream_t>(stream));
   }
   assign_blocks(a, count);
   return dispatch_rows<kStore>(a, dtype, static_cast<hipStream_t>(stream));

@@ -20,6 +20,14 @@ __device__ __forceinline__ void rms_norm_row(const T* __restrict__ xr, const T* 
   const int nvec = hidden / VEC;
   float v[NV][VEC];
   float sq = 0.0f;
+  // The weight vectors are requested with the row (they do not depend on
+  // it), so the sum's reduction does not wait on a second round trip.
+  uint4 wraw[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = lane + 64 * i;
+    wraw[i] = idx < nvec ? *reinterpret_cast<const uint4*>(w + idx * VEC) : make_uint4(0, 0, 0, 0);
+  }
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int idx = lane + 64 * i;
@@ -40,8 +48,7 @@ __device__ __forceinline__ void rms_norm_row(const T* __restrict__ xr, const T* 
     const int idx = lane + 64 * i;
     out[i] = make_uint4(0, 0, 0, 0);
     if (idx < nvec) {
-      const uint4 wraw = *reinterpret_cast<const uint4*>(w + idx * VEC);
-      const T* we = reinterpret_cast<const T*>(&wraw);
+      const T* we = reinterpret_cast<const T*>(&wraw[i]);
       T* oe = reinterpret_cast<T*>(&out[i]);
 #pragma unroll
       for (int k = 0; k < VEC; ++k) {

@@ -29,6 +29,9 @@ from ..pass_manager import CompilerPass, PassResult
 
 
 MAX_GROUP_FEATURES = 16384
+# A head at least this wide (1024 blocks of 16 features) runs on the wide
+# decode kernel, which takes the norm into its input staging.
+WIDE_FEATURES = 16384
 
 
 class FuseDecodeKernelsPass(CompilerPass):
@@ -150,11 +153,14 @@ def _fuse_group(function: Function) -> str | None:
         if not 1 <= len(users) <= 3:
             continue
         # Every workgroup of the fused kernel re-normalises the input rows, so
-        # it pays only for projections of modest width (Q/K/V, not a
-        # vocabulary-sized head, which keeps its own norm launch).
+        # it pays for projections of modest width (Q/K/V) and for a single
+        # vocabulary-sized head, whose kernel normalises while its first
+        # weight loads are in flight; not for wide groups in between.
         widths = [ops[i].attributes.get("output_features") if i < len(ops) else None
                   for i, _ in users]
-        if any(not isinstance(n, int) for n in widths) or sum(widths) > MAX_GROUP_FEATURES:
+        if any(not isinstance(n, int) for n in widths):
+            continue
+        if sum(widths) > MAX_GROUP_FEATURES and not (len(widths) == 1 and widths[0] >= WIDE_FEATURES):
             continue
         linears = [ops[i] if i < len(ops) else None for i, _ in users]
         if any(op is None or op.name != "kernel.hip.linear" for op in linears):

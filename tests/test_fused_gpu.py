@@ -54,6 +54,27 @@ def test_norm_linear_group_matches_norm_then_linears(gpu, rows, dtype, hidden, n
     assert_bitwise_equal(got1[0], hip_linear(h, ws[0]))
 
 
+@pytest.mark.parametrize("rows", [1, 8, 16, 17, 40])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hidden,vocab,bias", [(896, 151936, False), (2048, 17000, True),
+                                               (256, 20000, False)])
+def test_norm_vocabulary_head_matches_norm_then_linear(gpu, rows, dtype, hidden, vocab, bias):
+    """The final norm and a vocabulary-width head in one launch (the wide
+    kernel normalises in its input staging; rows past 16 take the
+    equal-workgroup kernel, past 32 the unfused pair) equal rms_norm then
+    linear bit for bit."""
+    announce(f"norm + vocabulary head rows={rows} {dtype} hidden={hidden} vocab={vocab}")
+    g = generator(300 + rows + hidden)
+    h = _t(g, rows, 1, hidden, dtype=dtype, device=gpu)
+    nw = _t(g, hidden, dtype=dtype, scale=0.5, device=gpu) + 1
+    w = _t(g, vocab, hidden, dtype=dtype, scale=0.02, device=gpu)
+    b = _t(g, vocab, dtype=dtype, scale=0.1, device=gpu) if bias else None
+    (got,) = hip_norm_linear_group(h, nw, [w], [b], epsilon=1e-6)
+    want = hip_linear(hip_rms_norm(h, nw, epsilon=1e-6, round_before_weight=True), w, b)
+    torch.cuda.synchronize()
+    assert_bitwise_equal(got, want)
+
+
 @pytest.mark.parametrize("rows", ROWS)
 @pytest.mark.parametrize("hidden,features", [(896, 4864), (2048, 5000)])
 def test_norm_linear_swiglu_matches_the_mlp_front(gpu, rows, hidden, features):

@@ -165,10 +165,10 @@ def test_full_lowering_of_24_layer_graphs(mode):
         # ... and the store, advance and attention run as one kernel.
         assert counts["kernel.hip.rope_store_attention"] == 24
         assert "kernel.hip.rope_kv_store" not in counts
-        # Every layer's chains are fused; the vocabulary-sized LM head keeps
-        # its own norm and linear.
-        assert counts["kernel.hip.linear"] == 1 and counts["kernel.hip.rms_norm"] == 1
-        assert counts["kernel.hip.norm_linear_group"] == 24
+        # Every layer's chains are fused, and the final norm with the
+        # vocabulary-sized LM head.
+        assert "kernel.hip.linear" not in counts and "kernel.hip.rms_norm" not in counts
+        assert counts["kernel.hip.norm_linear_group"] == 25
         assert counts["kernel.hip.norm_linear_swiglu"] == 24
         assert counts["kernel.hip.linear_residual"] == 48
         assert "kernel.hip.decode_attention" not in counts
