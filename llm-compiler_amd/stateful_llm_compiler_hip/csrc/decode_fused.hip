@@ -231,18 +231,39 @@ __global__ __launch_bounds__(KW * 64) void fused_rows_kernel(FusedArgs p) {
     }
   };
 
+  // Norm prologue: this wave's input rows and the norm weight are requested
+  // first, then the first weight batch, and the rows are normalised (exactly
+  // as the rms_norm kernel does) while the weights stream: the loads
+  // complete in issue order, so waiting for the rows does not wait for the
+  // weights.
+  constexpr int RPW = (MB * 16 + kWaves - 1) / kWaves;  // rows per wave
+  constexpr int NVR = NV > 0 ? NV : 1;
+  uint4 xrow[NV > 0 ? RPW : 1][NVR], wnorm[NVR];
+  if constexpr (NV > 0) {
+    const T* x = static_cast<const T*>(p.x);
+    slc::rms_norm_load<T, NV>(static_cast<const T*>(p.norm_w), K, lane, wnorm);
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+      const int m = wave + q * kWaves;
+      if (m < M) {
+        slc::rms_norm_load<T, NV>(x + m * p.x_rs, K, lane, xrow[q]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) xrow[q][i] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
   int s0 = s_begin;
   fetch(s0, wa, xa);
   if constexpr (NV > 0) {
-    // Normalised input rows, exactly as the rms_norm kernel computes them
-    // (after the first weight loads are in flight: they do not depend on it).
     constexpr int VEC = 16 / sizeof(T);
-    const T* x = static_cast<const T*>(p.x);
-    const T* nw = static_cast<const T*>(p.norm_w);
-    for (int m = wave; m < MB * 16; m += kWaves) {
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+      const int m = wave + q * kWaves;
+      if (m >= MB * 16) break;
       uint4 out[NV];
       if (m < M) {
-        slc::rms_norm_row<T, NV, true>(x + m * p.x_rs, nw, K, p.eps, lane, out);
+        slc::rms_norm_from<T, NV, true>(xrow[q], wnorm, K, p.eps, lane, out);
       } else {
 #pragma unroll
         for (int i = 0; i < NV; ++i) out[i] = make_uint4(0, 0, 0, 0);
@@ -420,23 +441,40 @@ __global__ __launch_bounds__(256) void wide_rows_kernel(FusedArgs p) {
                          __builtin_bit_cast(typename MF::vec, wr[u]), acc[i]);
       }
   };
+  // XL with NNV: the rows to normalise and the norm weight are requested
+  // before the first weight batch and normalised after it is issued: the
+  // loads complete in issue order, so the norm waits for the rows only.
+  // (The launch keeps M <= 16 rows, 4 per wave.)
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const T* x = static_cast<const T*>(p.x);
+  uint4 xrow[NNV > 0 ? 4 : 1][NNV > 0 ? NNV : 1], wnorm[NNV > 0 ? NNV : 1];
+  if constexpr (XL && NNV > 0) {
+    slc::rms_norm_load<T, NNV>(static_cast<const T*>(p.norm_w), K, lane, wnorm);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int m = wave + 4 * q;
+      if (m < M) slc::rms_norm_load<T, NNV>(x + m * p.x_rs, K, lane, xrow[q]);
+    }
+  }
   int s0 = 0;
   fetch(s0, wa, xa);
   if constexpr (XL) {
-    // The weight loads above do not wait for this.  Every wave passes the
-    // barrier (the waves past N leave only after it).
-    const T* x = static_cast<const T*>(p.x);
+    // Every wave passes the barrier (the waves past N leave only after it).
     if constexpr (NNV > 0) {
-      const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-      const T* nw = static_cast<const T*>(p.norm_w);
-      for (int m = wave; m < M; m += 4) {
-        uint4 out[NNV];
-        slc::rms_norm_row<T, NNV, true>(x + m * p.x_rs, nw, K, p.eps, lane, out);
 #pragma unroll
-        for (int i = 0; i < NNV; ++i)
-          if (lane + 64 * i < K / 8) x_lds[m * x_stride + lane + 64 * i] = out[i];
+      for (int q = 0; q < 4; ++q) {
+        const int m = wave + 4 * q;
+        if (m < M) {
+          uint4 out[NNV];
+          slc::rms_norm_from<T, NNV, true>(xrow[q], wnorm, K, p.eps, lane, out);
+#pragma unroll
+          for (int i = 0; i < NNV; ++i)
+            if (lane + 64 * i < K / 8) x_lds[m * x_stride + lane + 64 * i] = out[i];
+        }
       }
     } else {
+      // The plain rows: requested here, after the weights (their wait covers
+      // the first weight batch; staging them earlier spilled registers).
       for (int idx = threadIdx.x; idx < M * (K / 8); idx += 256) {
         const int r = idx / (K / 8), v = idx % (K / 8);
         x_lds[r * x_stride + v] = *reinterpret_cast<const uint4*>(x + r * p.x_rs + v * 8);

@@ -13,27 +13,32 @@ namespace slc {
 //   wave butterfly), out = round(round(x * inv) * w)  (round_before_weight)
 //                       or round(x * inv * w).
 // Semantics of src/stateful_llm_compiler/execution.py:674-692.
+// The row's and the weight's 16-byte vectors of this lane (rms_norm_row's
+// loads), and the normalisation from them: a kernel may request them before
+// other loads and normalise later.
+template <typename T, int NV>
+__device__ __forceinline__ void rms_norm_load(const T* __restrict__ row, int hidden, int lane,
+                                              uint4 (&raw)[NV]) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int nvec = hidden / VEC;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = lane + 64 * i;
+    raw[i] = idx < nvec ? *reinterpret_cast<const uint4*>(row + idx * VEC) : make_uint4(0, 0, 0, 0);
+  }
+}
 template <typename T, int NV, bool ROUND>
-__device__ __forceinline__ void rms_norm_row(const T* __restrict__ xr, const T* __restrict__ w,
-                                             int hidden, float eps, int lane, uint4 (&out)[NV]) {
+__device__ __forceinline__ void rms_norm_from(const uint4 (&xraw)[NV], const uint4 (&wraw)[NV],
+                                              int hidden, float eps, int lane, uint4 (&out)[NV]) {
   constexpr int VEC = 16 / sizeof(T);
   const int nvec = hidden / VEC;
   float v[NV][VEC];
   float sq = 0.0f;
-  // The weight vectors are requested with the row (they do not depend on
-  // it), so the sum's reduction does not wait on a second round trip.
-  uint4 wraw[NV];
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int idx = lane + 64 * i;
-    wraw[i] = idx < nvec ? *reinterpret_cast<const uint4*>(w + idx * VEC) : make_uint4(0, 0, 0, 0);
-  }
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int idx = lane + 64 * i;
     if (idx < nvec) {
-      const uint4 raw = *reinterpret_cast<const uint4*>(xr + idx * VEC);
-      const T* e = reinterpret_cast<const T*>(&raw);
+      const T* e = reinterpret_cast<const T*>(&xraw[i]);
 #pragma unroll
       for (int k = 0; k < VEC; ++k) {
         v[i][k] = to_f32(e[k]);
@@ -58,6 +63,16 @@ __device__ __forceinline__ void rms_norm_row(const T* __restrict__ xr, const T* 
       }
     }
   }
+}
+// The weight vectors are requested with the row (they do not depend on it),
+// so the sum's reduction does not wait on a second round trip.
+template <typename T, int NV, bool ROUND>
+__device__ __forceinline__ void rms_norm_row(const T* __restrict__ xr, const T* __restrict__ w,
+                                             int hidden, float eps, int lane, uint4 (&out)[NV]) {
+  uint4 wraw[NV], xraw[NV];
+  rms_norm_load<T, NV>(w, hidden, lane, wraw);
+  rms_norm_load<T, NV>(xr, hidden, lane, xraw);
+  rms_norm_from<T, NV, ROUND>(xraw, wraw, hidden, eps, lane, out);
 }
 
 // SwiGLU of one element: round(silu(g)) * u, silu(g) = g / (1 + exp(-g)),
