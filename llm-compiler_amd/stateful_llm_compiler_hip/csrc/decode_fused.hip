@@ -255,6 +255,36 @@ __global__ __launch_bounds__(KW * 64) void fused_rows_kernel(FusedArgs p) {
   }
   int s0 = s_begin;
   fetch(s0, wa, xa);
+  // The epilogue's bias and residual elements of this thread, requested
+  // behind the first weight batch (so the multiply does not wait for them)
+  // instead of after the cross-wave sum (a dependent round trip at the end).
+  constexpr int kEpiStride = kWaves * 64;
+  constexpr int kEpiIters = (TILES * MB * 256 + kEpiStride - 1) / kEpiStride;
+  float pre_bias[kEpiIters], pre_res[kEpiIters];
+  auto epi_coords = [&](int idx, int& t, int& i, int& l, int& r, int& f, int& n, int& m) {
+    t = idx / (MB * 256);
+    const int e = idx % (MB * 256);
+    i = e / 256;
+    l = (e / 4) % 64;
+    r = e % 4;
+    f = 16 * t + (l & 15);
+    n = n0 + f;
+    m = i * 16 + 4 * (l >> 4) + r;
+  };
+  if constexpr (EPI != kSwiglu) {
+#pragma unroll
+    for (int k = 0; k < kEpiIters; ++k) {
+      const int idx = tid + k * kEpiStride;
+      int t, i, l, r, f, n, m;
+      epi_coords(idx, t, i, l, r, f, n, m);
+      const bool valid = idx < TILES * MB * 256 && f < w_rows && m < M;
+      pre_bias[k] = valid && p.bias[j] != nullptr
+                        ? slc::to_f32(static_cast<const T*>(p.bias[j])[n]) : 0.0f;
+      pre_res[k] = 0.0f;
+      if constexpr (EPI == kResidual)
+        pre_res[k] = valid ? slc::to_f32(static_cast<const T*>(p.residual)[m * p.r_rs + n]) : 0.0f;
+    }
+  }
   if constexpr (NV > 0) {
     constexpr int VEC = 16 / sizeof(T);
 #pragma unroll
@@ -301,13 +331,12 @@ __global__ __launch_bounds__(KW * 64) void fused_rows_kernel(FusedArgs p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) part(h, t, wave, i, lane, r) = acc[h][t][i][r];
   __syncthreads();
-  for (int idx = tid; idx < TILES * MB * 256; idx += kWaves * 64) {
-    const int t = idx / (MB * 256);
-    const int e = idx % (MB * 256);
-    const int i = e / 256, l = (e / 4) % 64, r = e % 4;
-    const int f = 16 * t + (l & 15);
-    const int n = n0 + f;
-    const int m = i * 16 + 4 * (l >> 4) + r;
+#pragma unroll
+  for (int k = 0; k < kEpiIters; ++k) {
+    const int idx = tid + k * kEpiStride;
+    if (idx >= TILES * MB * 256) break;
+    int t, i, l, r, f, n, m;
+    epi_coords(idx, t, i, l, r, f, n, m);
     if (f >= w_rows || m >= M) continue;
     float sum = 0.0f;
 #pragma unroll
@@ -320,11 +349,8 @@ __global__ __launch_bounds__(KW * 64) void fused_rows_kernel(FusedArgs p) {
       static_cast<T*>(p.y[0])[m * p.y_rs[0] + n] =
           slc::from_f32<T>(slc::swiglu_value<T>(gate, slc::round_to<T>(up)));
     } else {
-      if (p.bias[j] != nullptr) sum += slc::to_f32(static_cast<const T*>(p.bias[j])[n]);
-      if constexpr (EPI == kResidual) {
-        const float res = slc::to_f32(static_cast<const T*>(p.residual)[m * p.r_rs + n]);
-        sum = res + slc::round_to<T>(sum);
-      }
+      if (p.bias[j] != nullptr) sum += pre_bias[k];
+      if constexpr (EPI == kResidual) sum = pre_res[k] + slc::round_to<T>(sum);
       static_cast<T*>(p.y[j])[m * p.y_rs[j] + n] = slc::from_f32<T>(sum);
     }
   }
