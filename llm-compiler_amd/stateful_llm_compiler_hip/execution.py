@@ -230,7 +230,8 @@ class PreallocatedKVCacheState:
         if runner is not hip_decode_attention:
             return runner(query, key_buffer, value_buffer, lengths, attention_mask, scale=scale)
         order = attention_order(softmax_order, attention_mask.shape[-1], query)
-        return runner(query, key_buffer, value_buffer, lengths, attention_mask, scale=scale,
+        return runner(query, key_buffer, value_buffer, lengths,
+                      _kernel_mask(attention_mask, self.capacity), scale=scale,
                       softmax_order=order, workspace=self.workspace, split_tokens=split_tokens)
 
     def _attention_inputs(self, slot, query, attention_mask, groups):
@@ -342,7 +343,7 @@ class PreallocatedKVCacheState:
         if key.shape[2] == 1:
             result = hip_rope_decode_attention(
                 query, key, value, cosine, sine, buffer_key, buffer_value, positions, out,
-                attention_mask, scale=scale, overflow=self.overflow,
+                _kernel_mask(attention_mask, self.capacity), scale=scale, overflow=self.overflow,
                 softmax_order=attention_order(softmax_order, attention_mask.shape[-1], query),
                 workspace=self.workspace,
             )
@@ -583,7 +584,8 @@ class PagedKVCacheState(PreallocatedKVCacheState):
         lengths = self._check_attention(slot, query, attention_mask, groups)
         order = attention_order(softmax_order, attention_mask.shape[-1], query)
         return hip_paged_decode_attention(
-            query, self.keys[slot], self.values[slot], self.block_table, lengths, attention_mask,
+            query, self.keys[slot], self.values[slot], self.block_table, lengths,
+            _kernel_mask(attention_mask, self.capacity),
             scale=scale, softmax_order=order, workspace=self.workspace, split_tokens=split_tokens)
 
     def _validate_store(self, slot, key, value, positions):
@@ -633,8 +635,8 @@ class PagedKVCacheState(PreallocatedKVCacheState):
         if key.shape[2] == 1:
             result = hip_paged_rope_decode_attention(
                 query, key, value, cosine, sine, self.keys[slot], self.values[slot],
-                self.block_table, positions, out, attention_mask, scale=scale,
-                overflow=self.overflow,
+                self.block_table, positions, out, _kernel_mask(attention_mask, self.capacity),
+                scale=scale, overflow=self.overflow,
                 softmax_order=attention_order(softmax_order, attention_mask.shape[-1], query),
                 workspace=self.workspace)
         if result is None:
@@ -650,6 +652,27 @@ class PagedKVCacheState(PreallocatedKVCacheState):
 
 def _device_workspace(device: torch.device) -> _native.DeviceWorkspace | None:
     return _native.DeviceWorkspace(device) if device.type == "cuda" else None
+
+
+def mark_zero_mask(mask: torch.Tensor) -> torch.Tensor:
+    """Declare ``mask`` an all-zero additive attention mask for as long as it
+    lives (its owner never writes it): the HIP decode attention kernels then
+    do not read it when it spans the whole capacity.  Adding +0.0 to a score
+    changes no result, so the outputs are the same bit for bit; the kernels
+    save the mask loads.  The graph decoder's capacity-long mask is one."""
+
+    mask._slc_zero_mask = True
+    return mask
+
+
+def _kernel_mask(mask: torch.Tensor, capacity: int) -> torch.Tensor | None:
+    """The mask a HIP decode attention kernel needs: None for a marked zero
+    mask over the whole capacity (the kernel's range is then the capacity,
+    as it is the mask's), else the mask."""
+
+    if getattr(mask, "_slc_zero_mask", False) and mask.shape[-1] == capacity:
+        return None
+    return mask
 
 
 def attention_order(requested: str, mask_len: int, query: torch.Tensor) -> str:

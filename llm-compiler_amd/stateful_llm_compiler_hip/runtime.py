@@ -21,7 +21,7 @@ import torch
 from ._native import DeviceWorkspace
 from .backends import hip_argmax
 from .compiler import CompileOptions, compile_module
-from .execution import HipExecutor, PreallocatedKVCacheState
+from .execution import HipExecutor, PreallocatedKVCacheState, mark_zero_mask
 from .qwen2 import Qwen2Config, build_decode_module, build_prefill_module, weight_arguments
 
 
@@ -91,7 +91,10 @@ class GraphDecoder:
         self.runtime = runtime
         batch = first_tokens.shape[0]
         self.tokens = first_tokens.reshape(batch, 1).to(torch.int64).contiguous().clone()
-        self.mask = torch.zeros(batch, 1, 1, runtime.capacity, dtype=runtime.dtype, device=runtime.device)
+        # All zeros for the decoder's life (never written), so the attention
+        # kernels skip it.
+        self.mask = mark_zero_mask(
+            torch.zeros(batch, 1, 1, runtime.capacity, dtype=runtime.dtype, device=runtime.device))
         # The decoder's own scratch (arrival counters, partials): graphs of two
         # decoders may replay concurrently on different streams.
         self.workspace = DeviceWorkspace(runtime.device)

@@ -585,6 +585,31 @@ def test_decode_attention_exact_softmax_order(gpu, batch, capacity, lengths, mas
     assert e >= 0.97 and e >= o
 
 
+@pytest.mark.parametrize("mask_len", [1024, 700])
+def test_marked_zero_mask_is_skipped_only_over_the_capacity(gpu, mask_len):
+    """A mask marked all-zero (the graph decoder's) gives the unmarked mask's
+    output bit for bit; one shorter than the capacity still bounds the
+    attended range, so it is read."""
+    from stateful_llm_compiler_hip.execution import PreallocatedKVCacheState, mark_zero_mask
+
+    announce(f"marked zero mask mask_len={mask_len}")
+    g = generator(77)
+    batch, cap = 4, 1024
+    q = torch.randn(batch, 14, 1, 64, generator=g).bfloat16().to(gpu)
+    k = torch.randn(batch, cap, 2, 64, generator=g).bfloat16().to(gpu)
+    v = torch.randn(batch, cap, 2, 64, generator=g).bfloat16().to(gpu)
+    lengths = torch.tensor([1, 300, 900, 1024], dtype=torch.int64, device=gpu)
+    state = PreallocatedKVCacheState((k,), (v,), (lengths,), cap,
+                                     overflow=torch.zeros(1, dtype=torch.int32, device=gpu))
+    plain = torch.zeros(batch, 1, 1, mask_len, dtype=torch.bfloat16, device=gpu)
+    marked = mark_zero_mask(torch.zeros_like(plain))
+    for order in ("exact", "online"):
+        a = state.decode_attention(0, q, plain, groups=7, scale=0.125, softmax_order=order)
+        b = state.decode_attention(0, q, marked, groups=7, scale=0.125, softmax_order=order)
+        torch.cuda.synchronize()
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), order
+
+
 @pytest.mark.parametrize("order", ["exact", "online"])
 def test_decode_attention_ignores_rows_past_the_length(gpu, order):
     """Rows past a sequence's length take no part, whatever the cache holds
