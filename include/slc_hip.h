@@ -359,6 +359,10 @@ SLC_API int slc_hip_linear(const void* input, const void* weight,
 #define SLC_TILE_R256X128 7
 #define SLC_TILE_R128X64 8
 #define SLC_TILE_R64X64 9
+/* Persistent 256 x 128 ring (one workgroup per CU walks the output tiles;
+ * the next tile's k-tiles stream in while the current one is written out);
+ * calls with a residual run SLC_TILE_R256X128. */
+#define SLC_TILE_S256X128 10
 SLC_API int slc_hip_linear_tile(const void* input, const void* weight,
                                 const void* bias, void* output, int dtype,
                                 int64_t rows, int64_t out_features,

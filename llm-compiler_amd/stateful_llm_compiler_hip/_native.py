@@ -33,7 +33,8 @@ SLC_I64 = 4
 SOFTMAX_ORDERS = {"online": 0, "exact": 1}
 # Workgroup tiles of the prefill-sized linear (SLC_TILE_* in slc_hip.h).
 LINEAR_TILES = {"auto": 0, "t128x128": 1, "t128x64": 2, "t64x128": 3, "t64x64": 4, "t32x64": 5,
-                "r128x128": 6, "r256x128": 7, "r128x64": 8, "r64x64": 9}
+                "r128x128": 6, "r256x128": 7, "r128x64": 8, "r64x64": 9,
+                "s256x128": 10}
 
 # slc_split: decode attention's length-balanced split-sequence variant
 SPLIT_BALANCED = -1

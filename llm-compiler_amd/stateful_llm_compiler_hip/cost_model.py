@@ -50,7 +50,7 @@ VARIANTS: dict[str, tuple[str, ...]] = {
     "rms_norm": ("auto", "wave", "block"),
     "decode_attention": ("auto", "fixed", "balanced"),
     "linear": ("auto", "t128x128", "t128x64", "t64x128", "t64x64", "t32x64",
-               "r128x128", "r256x128", "r128x64", "r64x64"),
+               "r128x128", "r256x128", "r128x64", "r64x64", "s256x128"),
 }
 _CHUNK = re.compile(r"chunk(\d+)$")
 

@@ -125,6 +125,10 @@ namespace slc_host {
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
 
+// Compute units of the current device (cached per device; 256 if the query
+// fails).
+int device_cu_count();
+
 // Measurement hook: when the caller armed a pair of events on this thread
 // (slc_hip_set_timing_events), the entry point brackets its dominant kernel
 // with them on the launch stream.  Both are no-ops otherwise.

@@ -559,19 +559,6 @@ __global__ __launch_bounds__(kThreads) void decode_stream_kernel(StreamParams p)
   }
 }
 
-int g_cu_count[64] = {0};
-
-int device_cu_count() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
-  if (dev < 64 && g_cu_count[dev] > 0) return g_cu_count[dev];
-  int n = 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-    n = 256;
-  if (dev < 64) g_cu_count[dev] = n;
-  return n;
-}
-
 #ifndef SLC_STREAM_ONE_PER_CU
 #define SLC_STREAM_ONE_PER_CU 1
 #endif
@@ -639,7 +626,7 @@ int64_t stream_workspace_bytes(int64_t q_heads, int64_t kv_heads, int64_t head_d
 int64_t stream_grid(int64_t batch, int64_t segments, int64_t mask_len, int64_t capacity) {
   const int64_t limit = std::min(mask_len, capacity);
   const int64_t tiles = batch * segments * ((limit + kTile - 1) / kTile);
-  int64_t grid = int64_t{device_cu_count()} * SLC_STREAM_WGS_PER_CU;
+  int64_t grid = int64_t{slc_host::device_cu_count()} * SLC_STREAM_WGS_PER_CU;
   grid = std::min<int64_t>(grid, (tiles + SLC_STREAM_MIN_TILES - 1) / SLC_STREAM_MIN_TILES);
   grid = std::min<int64_t>(grid, kStreamMaxGrid);
   return std::max<int64_t>(grid, 1);

@@ -30,6 +30,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
 
 template <typename T>
 struct Mfma;
@@ -600,6 +601,237 @@ __global__ __launch_bounds__((CWM * CWN + PW) * 64) void linear_ring_kernel(
 }
 
 
+// Tile id -> (m_blk, n_blk) with the mapping of xcd_tile, for a tile id that
+// is not the workgroup id (persistent workgroups).  Tile ids of one residue
+// mod 8 run on one XCD when the grid is a multiple of 8 workgroups.
+template <int kGroupM>
+__device__ __forceinline__ void xcd_tile_of(int id, int n_tiles, int m_tiles, int& m_blk,
+                                            int& n_blk) {
+  constexpr int kXcds = 8;
+  const int per = n_tiles * m_tiles / kXcds;
+  const int t = id < per * kXcds ? (id % kXcds) * per + id / kXcds : id;
+  const int span = kGroupM * n_tiles;
+  const int first_m = (t / span) * kGroupM;
+  const int gm = m_tiles - first_m < kGroupM ? m_tiles - first_m : kGroupM;
+  m_blk = first_m + (t % span) % gm;
+  n_blk = (t % span) / gm;
+}
+
+// Persistent form of the 256 x 128 ring tile, for grids several rounds deep.
+// One workgroup per CU walks the output tiles id, id + grid, ...; its
+// producer waves stream k-tiles into the 3-stage ring without a break at tile
+// boundaries, so the first k-tiles of the next output tile land while the
+// consumers finish the current one and write it out.  The consumers multiply
+// with the operands swapped (W rows as the MFMA A operand, X rows as B): an
+// accumulator lane then holds four consecutive output features of one row,
+// which it stores with one 8-byte store straight from registers -- the ring
+// is never needed for staging the output.  Each output accumulates its k
+// range in the ring kernel's order (same fragments, same 32-k MFMA steps; a
+// product of two bf16 values does not depend on which operand slot holds
+// which), so both kernels give the same bits.
+// DUAL: each 128-row W stage holds 64 gate rows then 64 up rows; consumer
+// wave wn takes gate and up rows of the same 32 features (fragments 0-1 gate,
+// 2-3 up), so the SwiGLU pairs meet in one lane.
+template <typename T, bool DUAL>
+__global__ __launch_bounds__(12 * 64) void linear_stream_kernel(
+    const T* __restrict__ x, const T* __restrict__ w_arg, const T* __restrict__ bias_arg,
+    T* __restrict__ y_arg, int M, int N_arg, int K, int64_t x_rs, int64_t y_rs_arg, int n_tiles,
+    int m_tiles, const T* __restrict__ w2) {
+  using MF = Mfma<T>;
+  constexpr int BM = 256, BN = 128, CWN = 2, PW = 4, S = 3, GM = 4;
+  constexpr int CW = 8;                      // consumer waves, 4 x 2
+  constexpr int TM = 64, TN = 64;            // consumer wave tile
+  constexpr int FM = TM / 16, FN = TN / 16;  // fragments
+  constexpr int XB = BM * kBK * 2;
+  constexpr int kStage = (BM + BN) * kBK * 2;
+  constexpr int kOps = (BM + BN) / 8 / PW;
+  constexpr int XO = BM / 8 / PW;
+  constexpr int WO = (DUAL ? BN / 2 : BN) / 8 / PW;
+  static_assert(XO + WO * (DUAL ? 2 : 1) == kOps, "operands split evenly over the producers");
+  static_assert((S - 2) * kOps <= 63, "the wait count fits vmcnt");
+  __shared__ __attribute__((aligned(16))) unsigned char ring[S * kStage];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int total = n_tiles * m_tiles;
+  const int ktiles = K / kBK;
+  const int first = blockIdx.x;
+  const int step = gridDim.x;
+
+  struct Tile {
+    int m0, n0, N;
+    const T* w;
+    const T* bias;
+    T* y;
+    int64_t y_rs;
+  };
+  auto tile_of = [&](int id) {
+    int m_blk, n_blk;
+    xcd_tile_of<GM>(id, n_tiles, m_tiles, m_blk, n_blk);
+    Tile t{0, 0, N_arg, w_arg, bias_arg, y_arg, y_rs_arg};
+    t.n0 = n_blk * (DUAL ? BN / 2 : BN);
+    t.m0 = m_blk * BM;
+    return t;
+  };
+
+  if (wave >= CW) {
+    // ---- producers: one k-tile per barrier, S - 1 ahead, across tiles -------
+    const int pw = wave - CW;
+    int voff[kOps];
+#pragma unroll
+    for (int i = 0; i < kOps; ++i) {
+      const int local = i < XO ? i : (i - XO) % WO;
+      const int row = 8 * (pw + PW * local) + lane / 8;
+      const int chunk = (lane % 8) ^ (row & 7);
+      voff[i] = i < XO ? static_cast<int>(row * x_rs * 2) + chunk * 16 : row * K * 2 + chunk * 16;
+    }
+    // The operand ranges of the tile being loaded, as base + bytes: the
+    // resources are rebuilt from them (through readfirstlane) at every issue,
+    // so the compiler keeps them scalar; a resource variable reassigned at
+    // tile boundaries is taken for divergent, and every load then runs in a
+    // waterfall loop.
+    const T* xb = x;
+    const T* wb = x;
+    const T* w2b = x;
+    int64_t x_bytes = 0, w_bytes = 0;
+    int load_id = first, load_k = 0;
+    auto set_tile = [&](int id) {
+      x_bytes = w_bytes = 0;
+      if (id >= total) return;
+      const Tile t = tile_of(id);
+      const int64_t x_rows = M - t.m0 < BM ? M - t.m0 : BM;
+      const int64_t w_rows =
+          DUAL ? (t.N - t.n0 < BN / 2 ? t.N - t.n0 : BN / 2) : (t.N - t.n0 < BN ? t.N - t.n0 : BN);
+      xb = x + t.m0 * x_rs;
+      x_bytes = x_rows > 0 ? (x_rows - 1) * x_rs * 2 + K * 2 : 0;
+      wb = t.w + static_cast<int64_t>(t.n0) * K;
+      w2b = DUAL ? w2 + static_cast<int64_t>(t.n0) * K : t.w;
+      w_bytes = w_rows > 0 ? w_rows * K * 2 : 0;
+    };
+    set_tile(load_id);
+    int slot = 0;
+    auto issue = [&]() {
+      unsigned char* dst = ring + __builtin_amdgcn_readfirstlane(slot) * kStage;
+      const int kb = __builtin_amdgcn_readfirstlane(load_id < total ? load_k * kBK * 2 : 0);
+      const __amdgpu_buffer_rsrc_t lx = make_rsrc(xb, x_bytes);
+      const __amdgpu_buffer_rsrc_t lw = make_rsrc(wb, w_bytes);
+      const __amdgpu_buffer_rsrc_t lw2 = make_rsrc(w2b, DUAL ? w_bytes : 0);
+#pragma unroll
+      for (int i = 0; i < kOps; ++i) {
+        if (i < XO) {
+          lds_dma16(lx, dst + (pw + PW * i) * 1024, voff[i], kb);
+        } else if (i < XO + WO) {
+          lds_dma16(lw, dst + XB + (pw + PW * (i - XO)) * 1024, voff[i], kb);
+        } else {
+          lds_dma16(lw2, dst + XB + (BN / 2) * 128 + (pw + PW * (i - XO - WO)) * 1024, voff[i], kb);
+        }
+      }
+      slot = slot == S - 1 ? 0 : slot + 1;
+      if (++load_k == ktiles) {
+        load_k = 0;
+        load_id += step;
+        set_tile(load_id);
+      }
+    };
+#pragma unroll
+    for (int t = 0; t < S - 1; ++t) issue();
+    const int steps = ((total - 1 - first) / step + 1) * ktiles;
+    for (int q = 0; q < steps; ++q) {
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"i"((S - 2) * kOps) : "memory");
+      issue();
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
+
+  // ---- consumers ------------------------------------------------------------
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int wm = wave / CWN;
+  const int wn = wave % CWN;
+  int slot = 0;
+  for (int id = first; id < total; id += step) {
+    const Tile t = tile_of(id);
+    // Bias of this lane's four features per fragment, requested before the
+    // k loop so that the epilogue does not wait for it.
+    uint32_t braw[FN][2];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      braw[j][0] = braw[j][1] = 0u;
+      const int n = t.n0 + wn * TN + j * 16 + 4 * g;
+      if (!DUAL && t.bias != nullptr && n < t.N) {
+        const uint16_t* bp = reinterpret_cast<const uint16_t*>(t.bias + n);
+        braw[j][0] = bp[0] | (static_cast<uint32_t>(bp[1]) << 16);
+        braw[j][1] = bp[2] | (static_cast<uint32_t>(bp[3]) << 16);
+      }
+    }
+    f32x4_t acc[FN][FM];
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int i = 0; i < FM; ++i) acc[j][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int kt = 0; kt < ktiles; ++kt) {
+      // Tile kt is in its stage; the stage read before may be refilled.  No
+      // wait on stores: the previous tile's output may still be in flight.
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      const unsigned char* xs = ring + slot * kStage;
+      const unsigned char* ws = xs + XB;
+      slot = slot == S - 1 ? 0 : slot + 1;
+#pragma unroll
+      for (int kk = 0; kk < kBK / 32; ++kk) {
+        typename MF::vec a[FM], b[FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+          a[i] = *reinterpret_cast<const typename MF::vec*>(xs + lds_offset(wm * TM + i * 16 + c, kk * 4 + g));
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int wrow = DUAL ? (j < 2 ? wn * 32 + j * 16 : BN / 2 + wn * 32 + (j - 2) * 16)
+                                : wn * TN + j * 16;
+          b[j] = *reinterpret_cast<const typename MF::vec*>(ws + lds_offset(wrow + c, kk * 4 + g));
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int i = 0; i < FM; ++i) acc[j][i] = MF::run(b[j], a[i], acc[j][i]);
+      }
+    }
+    // Epilogue: lane (c, g) of fragment (j, i) holds features 4g .. 4g + 3 of
+    // row c.
+    const int rows = M - t.m0 < BM ? M - t.m0 : BM;
+    const __amdgpu_buffer_rsrc_t ry =
+        make_rsrc(t.y + t.m0 * t.y_rs, (static_cast<int64_t>(rows) - 1) * t.y_rs * 2 + t.N * 2);
+    constexpr int kOutFrags = DUAL ? FN / 2 : FN;
+#pragma unroll
+    for (int j = 0; j < kOutFrags; ++j) {
+      const int n = t.n0 + (DUAL ? wn * 32 : wn * TN) + j * 16 + 4 * g;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int m_local = wm * TM + i * 16 + c;
+        uint16_t o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if constexpr (DUAL) {
+            const T ge = slc::from_f32<T>(acc[j][i][r]);
+            const T ue = slc::from_f32<T>(acc[j + 2][i][r]);
+            o[r] = slc::from_f32<T>(slc::swiglu_value<T>(slc::to_f32(ge), slc::to_f32(ue))).bits;
+          } else {
+            T bt;
+            bt.bits = static_cast<uint16_t>(braw[j][r >> 1] >> (16 * (r & 1)));
+            o[r] = slc::from_f32<T>(acc[j][i][r] + slc::to_f32(bt)).bits;
+          }
+        }
+        if (m_local < rows && n < t.N) {
+          const uint2 packed = make_uint2(o[0] | (static_cast<uint32_t>(o[1]) << 16),
+                                          o[2] | (static_cast<uint32_t>(o[3]) << 16));
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2_t, packed), ry,
+                                                static_cast<int>(m_local * t.y_rs + n) * 2, 0, 0);
+        }
+      }
+    }
+  }
+}
+
 // Decode-sized M (<= 64): Y is a handful of rows, W streams from HBM once.
 // One workgroup owns 16 output features and all M rows; its KW waves split K
 // between them (partial sums meet in LDS at the end), so even a 896-wide
@@ -786,6 +1018,41 @@ int launch_ring(const void* x, const void* w, const void* bias, void* y, int M, 
   return slc_host::check_launch("slc_hip_linear(ring)");
 }
 
+#ifndef SLC_STREAM_MIN_ROUNDS
+#define SLC_STREAM_MIN_ROUNDS 2
+#endif
+
+// The persistent 256 x 128 form (linear_stream_kernel): one workgroup per CU
+// (a multiple of 8, so each one's tiles stay on its XCD), or one per tile
+// when there are fewer tiles.  kNoResidualPath where the shape does not fit.
+// The library launches it for gate/up + SwiGLU (4-9 % faster there than the
+// ring kernel, whose SwiGLU epilogue stages the whole tile in LDS); for plain
+// linears it times within 2 % of the ring kernel and is a plan's choice.
+template <typename T, bool DUAL>
+int launch_stream(const void* x, const void* w, const void* bias, void* y, int M, int N, int K,
+                  int64_t x_rs, int64_t y_rs, int n_tiles, hipStream_t stream,
+                  const void* w2 = nullptr) {
+  const bool fits = K % kBK == 0 && x_rs % 8 == 0 && N % 8 == 0 && y_rs % 8 == 0 &&
+                    256 * x_rs * 2 < (int64_t{1} << 31) && 256 * y_rs * 2 < (int64_t{1} << 31);
+  if (!fits) return kNoResidualPath;
+  const int m_tiles = (M + 255) / 256;
+  const int64_t total = int64_t{n_tiles} * m_tiles;
+  const int cus = slc_host::device_cu_count() / 8 * 8;
+  const int grid = static_cast<int>(total < cus ? total : (cus > 0 ? cus : 8));
+  hipLaunchKernelGGL((linear_stream_kernel<T, DUAL>), dim3(grid), dim3(12 * 64), 0, stream,
+                     static_cast<const T*>(x), static_cast<const T*>(w),
+                     static_cast<const T*>(bias), static_cast<T*>(y), M, N, K, x_rs, y_rs,
+                     n_tiles, m_tiles, static_cast<const T*>(w2));
+  return slc_host::check_launch("slc_hip_linear(stream)");
+}
+
+// Whether the persistent form takes a 256 x 128 grid of `tiles` output tiles:
+// from SLC_STREAM_MIN_ROUNDS rounds of one workgroup per CU.
+inline bool stream_grid(int64_t tiles) {
+  return SLC_STREAM_MIN_ROUNDS > 0 &&
+         tiles >= int64_t{SLC_STREAM_MIN_ROUNDS} * slc_host::device_cu_count();
+}
+
 // Ring-kernel tile for a shape when the caller leaves it to the library, by
 // the number of 128 x 128 tiles the shape has: 256 x 128 from 300 of them
 // (the larger tile reads less per flop once the grid is a few rounds deep),
@@ -816,6 +1083,13 @@ int launch_ring_tile(int tile, const void* x, const void* w, const void* bias, v
       return launch_ring<T, 256, 128, 4, 2, 4, 3, 4>(x, w, bias, y, M, N, K, x_rs, y_rs, s, residual, r_rs);
     case SLC_TILE_R128X64:
       return launch_ring<T, 128, 64, 2, 2, 1, 3>(x, w, bias, y, M, N, K, x_rs, y_rs, s, residual, r_rs);
+    case SLC_TILE_S256X128:
+      if (residual == nullptr) {
+        const int rc = launch_stream<T, false>(x, w, bias, y, M, N, K, x_rs, y_rs,
+                                                      (N + 127) / 128, s);
+        if (rc != kNoResidualPath) return rc;
+      }
+      return launch_ring<T, 256, 128, 4, 2, 4, 3, 4>(x, w, bias, y, M, N, K, x_rs, y_rs, s, residual, r_rs);
     default:
       return launch_ring<T, 64, 64, 2, 2, 1, 5>(x, w, bias, y, M, N, K, x_rs, y_rs, s, residual, r_rs);
   }
@@ -922,6 +1196,16 @@ int gemm_swiglu(const void* x, int64_t x_rs, int64_t rows, int64_t K, int64_t N,
   // The ring kernel; each 128-wide column tile holds 64 gate and 64 up rows.
   const bool big = auto_ring_tile(M, (n + 63) / 64) == SLC_TILE_R256X128 &&
                    256 * x_rs * 2 < (int64_t{1} << 31) && 256 * y_rs * 2 < (int64_t{1} << 31);
+  if (big && stream_grid(int64_t{(M + 255) / 256} * ((n + 63) / 64))) {
+    // Several rounds of 256 x 128 tiles: the persistent form, whose
+    // SwiGLU pairs meet in registers instead of a staged LDS tile.
+    const int rc = dtype == SLC_BF16
+                       ? launch_stream<slc::bf16_t, true>(x, w_gate, nullptr, y, M, n, k, x_rs, y_rs,
+                                                          (n + 63) / 64, stream, w_up)
+                       : launch_stream<slc::f16_t, true>(x, w_gate, nullptr, y, M, n, k, x_rs, y_rs,
+                                                         (n + 63) / 64, stream, w_up);
+    if (rc != kNoResidualPath) return rc;
+  }
 #define SLC_DUAL(TT, BM, CWM, PW, S, GM)                                                          \
   hipLaunchKernelGGL((linear_ring_kernel<TT, BM, 128, CWM, 2 * 4 / CWM, PW, S, GM, true>),         \
                      dim3((n + 63) / 64, (M + BM - 1) / BM), dim3((8 + PW) * 64), 0, stream,      \
@@ -1022,7 +1306,7 @@ extern "C" int slc_hip_linear_tile(const void* input, const void* weight,
                                    int64_t rows, int64_t out_features,
                                    int64_t in_features, int64_t in_stride_row,
                                    int64_t out_stride_row, int tile, void* stream) {
-  SLC_REQUIRE(tile >= SLC_TILE_AUTO && tile <= SLC_TILE_R64X64, "slc_hip_linear_tile: bad tile %d",
+  SLC_REQUIRE(tile >= SLC_TILE_AUTO && tile <= SLC_TILE_S256X128, "slc_hip_linear_tile: bad tile %d",
               tile);
   SLC_REQUIRE(slc_host::is_float_dtype(dtype), "slc_hip_linear: bad dtype %d", dtype);
   SLC_REQUIRE(rows >= 0 && out_features > 0 && in_features > 0,

@@ -30,6 +30,18 @@ int check_launch(const char* what) {
   return SLC_OK;
 }
 
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    n = 256;
+  if (dev < 64) cached[dev] = n;
+  return n;
+}
+
 void mark_kernel_begin(hipStream_t stream) {
   if (g_begin != nullptr) hipEventRecord(g_begin, stream);
 }

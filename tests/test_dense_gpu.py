@@ -125,12 +125,13 @@ def test_linear_bf16_bench_rows(gpu, k, n):
     print(f"bitwise agreement with the oracle: {sum(agree) / len(agree):.4f}")
 
 
-TILES = ("t128x128", "t128x64", "t64x128", "t64x64", "t32x64", "r128x128", "r256x128", "r128x64", "r64x64")
+TILES = ("t128x128", "t128x64", "t64x128", "t64x64", "t32x64", "r128x128", "r256x128", "r128x64", "r64x64",
+         "s256x128")
 
 
 @pytest.mark.parametrize("rows,k,n,bias", [(4096, 896, 128, True), (300, 896, 896, True),
                                            (1000, 4864, 896, False), (77, 200, 136, True),
-                                           (520, 896, 4864, False)])
+                                           (520, 896, 4864, False), (1100, 896, 9728, True)])
 def test_linear_tiles_are_bit_identical_and_exact(gpu, rows, k, n, bias):
     """Every GEMM tile variant a plan may pick: within the fp64 product's bar
     and bit-identical to every other tile (same k order per output)."""
@@ -150,6 +151,24 @@ def test_linear_tiles_are_bit_identical_and_exact(gpu, rows, k, n, bias):
     _check_linear_bf16(outputs["t128x128"], x, w, b)
     for tile in TILES[1:]:
         assert torch.equal(outputs[tile], outputs["t128x128"]), tile
+
+
+@pytest.mark.parametrize("rows,n", [(1000, 151936), (4096, 4864)])
+def test_linear_persistent_tile_equals_ring_tile(gpu, rows, n):
+    """The persistent 256 x 128 kernel over grids many rounds deep (a
+    vocabulary-wide head, ragged M) gives the ring kernel's bits."""
+
+    from stateful_llm_compiler_hip.backends import hip_linear
+
+    announce(f"linear persistent tile M={rows} N={n}")
+    g = torch.Generator(device=gpu).manual_seed(rows + n)
+    x = torch.randn(rows, 896, device=gpu, generator=g, dtype=torch.bfloat16)
+    w = torch.randn(n, 896, device=gpu, generator=g, dtype=torch.bfloat16) * 0.02
+    got = hip_linear(x, w, tile="s256x128")
+    want = hip_linear(x, w, tile="r256x128")
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert torch.isfinite(got.float()).all()
 
 
 def test_linear_tile_plan_reaches_the_c_abi(gpu, monkeypatch):

@@ -317,7 +317,7 @@ def test_fused_ops_reject_host_operands(gpu):
 
 
 @pytest.mark.parametrize("rows,hidden,features", [(300, 896, 4864), (4096, 896, 4864),
-                                                  (129, 128, 200), (100, 64, 100)])
+                                                  (2100, 896, 4864), (129, 128, 200), (100, 64, 100)])
 def test_norm_linear_swiglu_prefill_rows(gpu, rows, hidden, features):
     # Prefill-sized rows: the norm, then gate/up and SwiGLU in one tile kernel
     # (features = 100: not a multiple of 8, the two-linear path), bit for bit
@@ -337,6 +337,7 @@ def test_norm_linear_swiglu_prefill_rows(gpu, rows, hidden, features):
 
 @pytest.mark.parametrize("rows,hidden,ns,bias", [(300, 896, (896, 128, 128), True),
                                                  (4096, 896, (896, 128, 128), True),
+                                                 (8192, 896, (4864, 896, 128), True),
                                                  (129, 64, (200, 8), False),
                                                  (100, 64, (96, 100), True)])
 def test_norm_linear_group_prefill_rows(gpu, rows, hidden, ns, bias):
