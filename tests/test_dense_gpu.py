@@ -169,6 +169,12 @@ def test_linear_persistent_tile_equals_ring_tile(gpu, rows, n):
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     assert torch.isfinite(got.float()).all()
+    xh, wh = x.half(), w.half()
+    bh = torch.randn(n, device=gpu, generator=g, dtype=torch.float16) * 0.02
+    got = hip_linear(xh, wh, bh, tile="s256x128")
+    want = hip_linear(xh, wh, bh, tile="r256x128")
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
 
 
 def test_linear_tile_plan_reaches_the_c_abi(gpu, monkeypatch):

@@ -316,18 +316,22 @@ def test_fused_ops_reject_host_operands(gpu):
         hip_norm_linear_group(x, torch.ones(896, dtype=torch.bfloat16), [w], [None], epsilon=1e-6)
 
 
-@pytest.mark.parametrize("rows,hidden,features", [(300, 896, 4864), (4096, 896, 4864),
-                                                  (2100, 896, 4864), (129, 128, 200), (100, 64, 100)])
-def test_norm_linear_swiglu_prefill_rows(gpu, rows, hidden, features):
+@pytest.mark.parametrize("rows,hidden,features,dtype", [(300, 896, 4864, torch.bfloat16),
+                                                        (4096, 896, 4864, torch.bfloat16),
+                                                        (2100, 896, 4864, torch.bfloat16),
+                                                        (2100, 896, 4864, torch.float16),
+                                                        (129, 128, 200, torch.bfloat16),
+                                                        (100, 64, 100, torch.bfloat16)])
+def test_norm_linear_swiglu_prefill_rows(gpu, rows, hidden, features, dtype):
     # Prefill-sized rows: the norm, then gate/up and SwiGLU in one tile kernel
     # (features = 100: not a multiple of 8, the two-linear path), bit for bit
     # the separate ops.
-    announce(f"norm_linear_swiglu prefill rows={rows} hidden={hidden} features={features}")
+    announce(f"norm_linear_swiglu prefill rows={rows} hidden={hidden} features={features} {dtype}")
     g = generator(rows + features)
-    h = _t(g, rows, 1, hidden, device=gpu)
-    nw = _t(g, hidden, scale=0.5, device=gpu) + 1
-    wg = _t(g, features, hidden, scale=0.05, device=gpu)
-    wu = _t(g, features, hidden, scale=0.05, device=gpu)
+    h = _t(g, rows, 1, hidden, dtype=dtype, device=gpu)
+    nw = _t(g, hidden, dtype=dtype, scale=0.5, device=gpu) + 1
+    wg = _t(g, features, hidden, dtype=dtype, scale=0.05, device=gpu)
+    wu = _t(g, features, hidden, dtype=dtype, scale=0.05, device=gpu)
     got = hip_norm_linear_swiglu(h, nw, wg, wu, epsilon=1e-6)
     x = hip_rms_norm(h, nw, epsilon=1e-6, round_before_weight=True)
     want = hip_swiglu(hip_linear(x, wg), hip_linear(x, wu))
