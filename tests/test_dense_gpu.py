@@ -568,3 +568,39 @@ def test_prefill_mask_classes_are_bit_identical(gpu, tokens, order, causal):
                 finite = torch.isfinite(expected)
                 assert torch.equal(finite, torch.isfinite(fast.cpu().float()))
                 assert_bf16_close(fast.cpu()[finite], expected[finite])
+
+
+@pytest.mark.parametrize("kind", ["causal-online", "mask-exact", "mask-online", "none-exact"])
+def test_prefill_short_and_long_workgroups_agree(gpu, kind):
+    """Short grids take 16-query workgroups, deeper ones 32-query workgroups
+    (at most two 32-query workgroups per CU picks the short form).  Batch
+    rows are independent, so a batch of 9 (32-query form on a 256-CU part)
+    and its first 8 rows (16-query form) give the same bits for those rows."""
+
+    from stateful_llm_compiler_hip.backends import hip_prefill_attention, hip_prefill_mask_tiles
+
+    batch, q_heads, kv_heads, tokens, head_dim = 9, 14, 2, 1024, 64
+    announce(f"prefill short/long workgroups {kind} T={tokens}")
+    g = torch.Generator(device=gpu).manual_seed(17)
+    q = torch.randn(batch, q_heads, tokens, head_dim, device=gpu, generator=g, dtype=torch.bfloat16)
+    k = torch.randn(batch, kv_heads, tokens, head_dim, device=gpu, generator=g, dtype=torch.bfloat16)
+    v = torch.randn(batch, kv_heads, tokens, head_dim, device=gpu, generator=g, dtype=torch.bfloat16)
+    structure, order = kind.split("-")
+    causal = structure == "causal"
+    mask = None
+    if structure == "mask":
+        future = torch.ones(tokens, tokens, dtype=torch.bool, device=gpu).triu(1)
+        mask = torch.zeros(tokens, tokens, device=gpu, dtype=torch.bfloat16).masked_fill(future, float("-inf"))
+        mask = mask.expand(batch, 1, tokens, tokens).contiguous()
+
+    def run(rows):
+        m = None if mask is None else mask[:rows].contiguous()
+        tiles = None if m is None else hip_prefill_mask_tiles(m)
+        return hip_prefill_attention(q[:rows].contiguous(), k[:rows].contiguous(), v[:rows].contiguous(), m,
+                                     scale=0.125, causal=causal, softmax_order=order, mask_tiles=tiles)
+
+    long_form = run(9)
+    short_form = run(8)
+    torch.cuda.synchronize()
+    assert torch.isfinite(short_form.float()).all()
+    assert torch.equal(long_form[:8].view(torch.int16), short_form.view(torch.int16))
