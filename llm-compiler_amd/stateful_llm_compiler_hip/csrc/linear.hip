@@ -358,6 +358,10 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, unsigned 
 
 // Workgroup id -> (m_blk, n_blk): gathered per XCD, then groups of 8 M-tiles
 // (see linear_mfma_kernel).
+#ifndef SLC_RING_PF
+#define SLC_RING_PF 1
+#endif
+
 template <int kGroupM>
 __device__ __forceinline__ void xcd_tile(int n_tiles, int m_tiles, int& m_blk, int& n_blk) {
   constexpr int kXcds = 8;
@@ -390,7 +394,17 @@ __global__ __launch_bounds__((CWM * CWN + PW) * 64) void linear_ring_kernel(
   constexpr int kStage = (BM + BN) * kBK * 2;
   constexpr int kOps = (BM + BN) / 8 / PW;  // 1 KB DMA instructions per producer wave per tile
   static_assert(((BM + BN) / 8) % PW == 0, "DMA instructions split evenly over the producers");
-  static_assert((S - 2) * kOps <= 63, "the wait count fits vmcnt");
+  // PF: at the barrier of tile kt the producers have landed tile kt + 1 as
+  // well, so the consumers read the next tile's first k-step fragments while
+  // this tile's MFMAs run, and no LDS latency follows a barrier.  The loads
+  // then keep S - 3 tiles in flight at a barrier instead of S - 2, so only
+  // rings of four or more stages take it: M4096 N896 K896 12.5 -> 10.8 us,
+  // Q/K/V group 30-32 -> 28.5 us; with three stages (256 x 128) the loads
+  // lose their lead (vocabulary head 1297 -> 1513 us).
+  constexpr bool kPF = SLC_RING_PF != 0 && S >= 4;
+  constexpr int kLeadTiles = kPF ? S - 3 : S - 2;
+  static_assert(!kPF || kBK == 64, "two k-steps per tile");
+  static_assert(kLeadTiles * kOps <= 63, "the wait count fits vmcnt");
   static_assert(TM % 16 == 0 && TN % 16 == 0, "whole MFMA fragments per wave");
   constexpr int kEpiWave = TM * (TN + 8) * 2;
   constexpr int kEpiDual = BM * (BN + 8) * 2;
@@ -471,7 +485,7 @@ __global__ __launch_bounds__((CWM * CWN + PW) * 64) void linear_ring_kernel(
 #pragma unroll
     for (int t = 0; t < S - 1; ++t) issue(t);
     for (int kt = 0; kt < ktiles; ++kt) {
-      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"i"((S - 2) * kOps) : "memory");
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"i"(kLeadTiles * kOps) : "memory");
       issue(kt + S - 1);
     }
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
@@ -489,10 +503,34 @@ __global__ __launch_bounds__((CWM * CWN + PW) * 64) void linear_ring_kernel(
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+  auto fragments = [&](const unsigned char* xs, int kk, typename MF::vec* a, typename MF::vec* b) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      a[i] = *reinterpret_cast<const typename MF::vec*>(xs + lds_offset(wm * TM + i * 16 + c, kk * 4 + g));
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      b[j] = *reinterpret_cast<const typename MF::vec*>(xs + XB + lds_offset(wn * TN + j * 16 + c, kk * 4 + g));
+  };
+  typename MF::vec na[FM], nb[FN];  // PF: first k-step fragments of the next tile
   for (int kt = 0; kt < ktiles; ++kt) {
     __syncthreads();  // tile kt is in its stage; the stage of kt - 1 may be refilled
     const unsigned char* xs = ring + (kt % S) * kStage;
     const unsigned char* ws = xs + XB;
+    if constexpr (kPF) {
+      if (kt == 0) fragments(xs, 0, na, nb);
+      typename MF::vec a[FM], b[FN];
+      fragments(xs, 1, a, b);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = MF::run(na[i], nb[j], acc[i][j]);
+      if (kt + 1 < ktiles) fragments(ring + ((kt + 1) % S) * kStage, 0, na, nb);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = MF::run(a[i], b[j], acc[i][j]);
+      continue;
+    }
 #pragma unroll
     for (int kk = 0; kk < kBK / 32; ++kk) {
       typename MF::vec a[FM], b[FN];
