@@ -1071,6 +1071,7 @@ int launch_stream(const void* x, const void* w, const void* bias, void* y, int M
                   int64_t x_rs, int64_t y_rs, int n_tiles, hipStream_t stream,
                   const void* w2 = nullptr) {
   const bool fits = K % kBK == 0 && x_rs % 8 == 0 && N % 8 == 0 && y_rs % 8 == 0 &&
+                    (reinterpret_cast<uintptr_t>(y) & 15) == 0 &&
                     256 * x_rs * 2 < (int64_t{1} << 31) && 256 * y_rs * 2 < (int64_t{1} << 31);
   if (!fits) return kNoResidualPath;
   const int m_tiles = (M + 255) / 256;

@@ -177,6 +177,30 @@ def test_linear_persistent_tile_equals_ring_tile(gpu, rows, n):
     assert torch.equal(got, want)
 
 
+def test_linear_persistent_tile_with_unaligned_output(gpu):
+    """The persistent tile stores 8 bytes per lane from registers: an output
+    whose base is 2 bytes off 16-byte alignment takes the staged-store
+    kernel instead, with the same bits."""
+
+    from stateful_llm_compiler_hip import _native
+    from stateful_llm_compiler_hip.backends import hip_linear
+
+    rows, n, k = 1100, 9728, 896
+    announce(f"linear persistent tile, unaligned output M={rows} N={n}")
+    g = torch.Generator(device=gpu).manual_seed(5)
+    x = torch.randn(rows, k, device=gpu, generator=g, dtype=torch.bfloat16)
+    w = torch.randn(n, k, device=gpu, generator=g, dtype=torch.bfloat16) * 0.02
+    want = hip_linear(x, w, tile="r256x128")
+    flat = torch.full((rows * n + 1,), float("nan"), device=gpu, dtype=torch.bfloat16)
+    got = flat[1:].view(rows, n)
+    status = _native.library().slc_hip_linear_tile(
+        x.data_ptr(), w.data_ptr(), None, got.data_ptr(), _native.SLC_BF16, rows, n, k, k, n,
+        _native.LINEAR_TILES["s256x128"], _native.current_stream(x.device))
+    _native.check(status, "slc_hip_linear_tile")
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
 def test_linear_tile_plan_reaches_the_c_abi(gpu, monkeypatch):
     """A profile plan's tile choice is the tile argument slc_hip_linear_tile
     receives (recorded by a pass-through proxy of the loaded library)."""
