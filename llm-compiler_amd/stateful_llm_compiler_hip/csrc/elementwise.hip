@@ -278,11 +278,18 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_split_kernel(
     const int slot = r * kArgmaxSegs + seg;
     __hip_atomic_store(&ws.value[slot], best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(&ws.index[slot], best_i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int before = __hip_atomic_fetch_add(&ws.counters[r], 1, __ATOMIC_ACQ_REL,
+    // Release per workgroup, acquire only in the one completing the count
+    // (an acquire invalidates the XCD's L2, so paying it once per row is
+    // cheaper than in every workgroup).  The fence, the barrier below and
+    // the completing wave's loads order its reads after every segment's
+    // stores.
+    const int before = __hip_atomic_fetch_add(&ws.counters[r], 1, __ATOMIC_RELEASE,
                                               __HIP_MEMORY_SCOPE_AGENT);
     is_last = before == segs - 1;
-    if (is_last)
+    if (is_last) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       __hip_atomic_store(&ws.counters[r], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   __syncthreads();
   if (!is_last || threadIdx.x >= 64) return;
